@@ -1,0 +1,188 @@
+/*
+ * gdn.h -- C ABI of libgdn, the gfx950 (MI355X) GatedDeltaNet decode/prefill
+ * path with a device-resident per-sequence state pool.
+ *
+ * Reference interfaces this ABI replaces (qwen-mlx, Rust + MLX):
+ *   - gated_delta_kernel(q,k,v,g,beta,state,T,B,Hk,Hv,Dk,Dv)
+ *       src/models/metal_gdn.rs:170-218           -> gdn_recurrent
+ *   - compiled_beta_g(b,a,A_log,dt_bias)
+ *       src/models/compiled_ops.rs:68-94          -> fused into gdn_decode / gdn_prefill_varlen
+ *   - GatedDeltaNet::forward_with_cache, conv/split/norm/gates/recurrence
+ *       src/models/qwen3_5.rs:588-658             -> gdn_decode (S=1), gdn_prefill_varlen (S>1)
+ *   - Qwen35Executor::stack_caches / unstack_caches
+ *       src/scheduler/mlx_executor.rs:42-130      -> the pool itself (slot ids replace copies);
+ *                                                    gdn_slots_read / gdn_slots_write keep the
+ *                                                    gather / scatter semantics for callers that
+ *                                                    need the stacked tensors.
+ *   - state init `zeros f32 [B,Hv,Dv,Dk]` / `zeros bf16 [B,3,D]`
+ *       src/models/qwen3_5.rs:598-601,613-616,644-648 -> gdn_slots_zero
+ *   - error convention of mlx_fast_metal_kernel_apply: 0 = ok, nonzero = failure
+ *       src/models/metal_gdn.rs:197-208          -> every function returns gdn_status.
+ *
+ * Conventions
+ *   - All tensors are plain device pointers. bf16 tensors are passed as raw
+ *     16-bit patterns (uint16_t). No function allocates caller-visible memory.
+ *   - Every compute call is asynchronous on the caller's hipStream_t (passed as
+ *     void* so this header needs no HIP include; NULL = the null stream).
+ *   - slot_ids are DEVICE int32 arrays. A slot id outside [0, num_slots) makes
+ *     the affected work-group skip its sequence entirely (no memory touched) and
+ *     latches GDN_FLAG_BAD_SLOT in the pool's device status word, which
+ *     gdn_pool_check() reads (synchronously) and clears.
+ *   - Slot ids within one call must be distinct: two work-groups updating the
+ *     same slot in one launch race. gdn_slots_validate() checks this on demand.
+ *   - One pool is not reentrant: calls that touch the same slots must be
+ *     ordered on one stream by the caller.
+ *   - Model shape limits: head_k_dim == head_v_dim == 128, conv_kernel == 4,
+ *     num_v_heads / num_k_heads in {1, 2, 4}.
+ *
+ * Tensor layouts (row-major, innermost last)
+ *   pool recurrent state, per layer : [num_slots, Hv, Dv, Dk] f32   (metal_gdn.rs:25-26,149)
+ *   pool conv state, per layer      : [num_slots, K-1, D]   bf16  (qwen3_5.rs:600-604)
+ *       D = 2*Hk*Dk + Hv*Dv conv channels, channel order q | k | v (qwen3_5.rs:627-629)
+ *   q, k                            : [B, T, Hk, Dk] bf16
+ *   v, y                            : [B, T, Hv, Dv] bf16
+ *   g (decay multiplier, in (0,1])  : [B, T, Hv] f32
+ *   beta                            : [B, T, Hv] bf16
+ *   mixed_qkv (pre-conv projection) : [ntok, D] bf16
+ *   ab (merged b|a projection)      : [ntok, 2*Hv] bf16, b = ab[:, :Hv], a = ab[:, Hv:]
+ *                                     (qwen3_5.rs:583,1037-1040)
+ *   A_log, dt_bias                  : [Hv] f32
+ *   conv_w (depthwise conv weight)  : [D, K] bf16 (MLX conv1d weight [D,K,1])
+ */
+#ifndef GDN_H_
+#define GDN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int gdn_status;
+#define GDN_OK 0
+#define GDN_ERR_INVALID 1     /* bad argument (shape, layer, null pointer)   */
+#define GDN_ERR_UNSUPPORTED 2 /* shape outside the compiled kernel family     */
+#define GDN_ERR_HIP 3         /* HIP runtime error (launch, memcpy, ...)      */
+#define GDN_ERR_OOM 4         /* device allocation failed                     */
+#define GDN_ERR_SLOTS 5       /* slot ids failed validation                   */
+
+/* Device status bits latched by kernels (gdn_pool_check). */
+#define GDN_FLAG_BAD_SLOT 0x1u      /* a slot id was outside [0, num_slots)      */
+#define GDN_FLAG_DUP_SLOT 0x2u      /* gdn_slots_validate found a repeated id    */
+#define GDN_FLAG_BAD_SEQLENS 0x4u   /* cu_seqlens not non-decreasing / too long  */
+
+#define GDN_ALL_LAYERS (-1)
+
+typedef struct gdn_pool gdn_pool;
+
+typedef struct gdn_pool_desc {
+  int32_t num_layers;  /* GDN layers held by the pool (30 for Qwen3.5-35B-A3B) */
+  int32_t num_slots;   /* sequence slots per layer                            */
+  int32_t num_k_heads; /* Hk  (linear_num_key_heads)                          */
+  int32_t num_v_heads; /* Hv  (linear_num_value_heads)                        */
+  int32_t head_k_dim;  /* Dk  (linear_key_head_dim), must be 128              */
+  int32_t head_v_dim;  /* Dv  (linear_value_head_dim), must be 128            */
+  int32_t conv_kernel; /* K   (linear_conv_kernel_dim), must be 4             */
+  int32_t device;      /* HIP device ordinal the pool lives on                */
+} gdn_pool_desc;
+
+/* Thread-local message describing the last non-OK status on this thread. */
+const char* gdn_last_error(void);
+
+/* Library version string ("gdn <major>.<minor> gfx950"). */
+const char* gdn_version(void);
+
+/* Allocate and zero a pool: per layer, [num_slots,Hv,Dv,Dk] f32 recurrent
+ * state and [num_slots,K-1,D] bf16 conv state (both start at +0.0). */
+gdn_status gdn_pool_create(const gdn_pool_desc* desc, gdn_pool** out);
+gdn_status gdn_pool_destroy(gdn_pool* pool);
+
+/* Device pointers of one layer's state arrays (for inspection / export). */
+gdn_status gdn_pool_layer_state(gdn_pool* pool, int32_t layer, float** state,
+                                uint16_t** conv_state);
+
+/* Sizes in bytes of one slot's recurrent and conv state in one layer. */
+gdn_status gdn_pool_slot_bytes(const gdn_pool* pool, size_t* state_bytes,
+                               size_t* conv_bytes);
+
+/* Read (and clear) the pool's latched device status flags. Synchronises the
+ * given stream first. */
+gdn_status gdn_pool_check(gdn_pool* pool, void* stream, uint32_t* flags);
+
+/* Host-side slot allocator (free list, lowest id first). Replaces the
+ * reference's per-sequence `Qwen35State` arrays (mlx_executor.rs:19-21):
+ * one slot id addresses the sequence's state in every layer. */
+gdn_status gdn_slot_alloc(gdn_pool* pool, int32_t* slot);
+gdn_status gdn_slot_free(gdn_pool* pool, int32_t slot);
+gdn_status gdn_slots_in_use(const gdn_pool* pool, int32_t* count);
+
+/* Zero the recurrent and conv state of n slots in `layer` (or every layer
+ * with GDN_ALL_LAYERS). Replaces the missing-cache zero init of
+ * qwen3_5.rs:598-601,613-616,644-648. Uses a fill kernel (no memset node), so
+ * it may be captured in a HIP graph. */
+gdn_status gdn_slots_zero(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
+                          int32_t n, void* stream);
+
+/* Gather n slots of `layer` into caller buffers (stack_caches,
+ * mlx_executor.rs:92-115): state_out [n,Hv,Dv,Dk] f32, conv_out [n,K-1,D] bf16.
+ * Either output may be NULL. Bit-exact copies. */
+gdn_status gdn_slots_read(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
+                          int32_t n, float* state_out, uint16_t* conv_out,
+                          void* stream);
+
+/* Scatter caller buffers into n slots (unstack_caches, mlx_executor.rs:118-130).
+ * Either input may be NULL. Bit-exact copies. */
+gdn_status gdn_slots_write(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
+                           int32_t n, const float* state_in, const uint16_t* conv_in,
+                           void* stream);
+
+/* Device-side check of a slot-id list: range and uniqueness. Latches
+ * GDN_FLAG_BAD_SLOT / GDN_FLAG_DUP_SLOT (read them with gdn_pool_check). */
+gdn_status gdn_slots_validate(gdn_pool* pool, const int32_t* slot_ids, int32_t n,
+                              void* stream);
+
+/* The gated delta rule recurrence on already-prepared q/k/v/g/beta, state in
+ * pool slots, updated in place. Same arithmetic as gated_delta_kernel
+ * (metal_gdn.rs:10-67,170-218): per t, s *= g; kv = s.k; d = (v-kv)*beta;
+ * s += k*d; y = s.q. q and k are used as given (the caller normalises them).
+ * B sequences x T tokens each; slot_ids[B]. */
+gdn_status gdn_recurrent(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
+                         int32_t B, int32_t T, const uint16_t* q, const uint16_t* k,
+                         const uint16_t* v, const float* g, const uint16_t* beta,
+                         uint16_t* y, void* stream);
+
+/* Fused S=1 decode step of one GDN layer for B sequences (qwen3_5.rs:593-610,
+ * 626-658 + compiled_ops.rs:30-43), in one launch:
+ *   conv window [state | x] . w  -> silu -> split q|k|v -> q,k rms-norm with the
+ *   baked weights bf16(1/Dk), bf16(1/sqrt(Dk)), eps 1e-6 -> beta = sigmoid(b),
+ *   g = exp(-exp(A_log) * log(exp(a+dt_bias)+1)) -> recurrence -> y.
+ * The rolling conv state and the recurrent state of each slot are updated in
+ * place. mixed_qkv [B,D], ab [B,2Hv], y [B,Hv,Dv]. */
+gdn_status gdn_decode(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
+                      int32_t B, const uint16_t* mixed_qkv, const uint16_t* ab,
+                      const float* A_log, const float* dt_bias,
+                      const uint16_t* conv_w, uint16_t* y, void* stream);
+
+/* Varlen prefill of nseq sequences packed along the token axis
+ * (qwen3_5.rs:611-658 with S>1; the reference runs them one at a time, B=1):
+ * sequence i owns tokens [cu_seqlens[i], cu_seqlens[i+1]) of mixed_qkv / ab / y
+ * and slot slot_ids[i]. Each sequence starts from its slot's current conv and
+ * recurrent state (zero after gdn_slots_zero, as the reference's fresh
+ * prefill) and leaves its final states there. cu_seqlens is a DEVICE int32
+ * array of nseq+1 entries with cu_seqlens[0] == 0 and
+ * cu_seqlens[nseq] == total_tokens. Uses the chunked (WY form, chunk 64)
+ * algorithm; results equal the token-by-token recurrence within f32/bf16
+ * rounding. */
+gdn_status gdn_prefill_varlen(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
+                              const int32_t* cu_seqlens, int32_t nseq,
+                              int32_t total_tokens, const uint16_t* mixed_qkv,
+                              const uint16_t* ab, const float* A_log,
+                              const float* dt_bias, const uint16_t* conv_w,
+                              uint16_t* y, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN_H_ */

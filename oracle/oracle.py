@@ -1,0 +1,276 @@
+"""NumPy front end of the CPU restatement in gdn_oracle.c.
+
+TEST INFRASTRUCTURE ONLY: the checker for libgdn. Only tests, the smoke check
+and the bench's CPU-baseline leg import this module; the product path never
+does.
+
+bf16 tensors are numpy uint16 arrays holding the raw bit patterns. Every
+function returns new arrays and leaves its inputs untouched. The restated
+reference lines are cited in gdn_oracle.c next to each C function.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle_gdn.so")
+_lib = None
+
+_u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_c_int, _c_i64, _c_float = ctypes.c_int, ctypes.c_int64, ctypes.c_float
+
+
+def build() -> str:
+    """Compile liboracle_gdn.so with oracle/Makefile (gcc + OpenMP)."""
+    subprocess.run(["make", "-s", "-C", _HERE, "liboracle_gdn.so"], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(_LIB_PATH):
+        build()
+    L = ctypes.CDLL(_LIB_PATH)
+    L.orc_beta_g.argtypes = [_u16p, _c_i64, _c_int, _f32p, _f32p, _u16p, _f32p]
+    L.orc_conv_update.argtypes = [_u16p, _u16p, _u16p, _c_int, _c_int, _c_int, _u16p, _u16p]
+    L.orc_conv_prefill.argtypes = [_u16p, _u16p, _u16p, _c_int, _c_int, _c_int, _u16p, _u16p]
+    L.orc_rms_norm.argtypes = [_u16p, _c_i64, _c_int, _c_float, _c_float, _u16p]
+    L.orc_q_norm_weight.argtypes = [_c_int]
+    L.orc_q_norm_weight.restype = _c_float
+    L.orc_k_norm_weight.argtypes = [_c_int]
+    L.orc_k_norm_weight.restype = _c_float
+    L.orc_recurrent_io.argtypes = [_u16p, _u16p, _u16p, _f32p, _u16p, _f32p, _f32p, _u16p,
+                                   _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]
+    L.orc_recurrent_f64.argtypes = [_u16p, _u16p, _u16p, _f32p, _u16p, _f32p, _u16p, _f64p,
+                                    _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]
+    L.orc_decode_io.argtypes = [_u16p, _u16p, _f32p, _f32p, _u16p, _u16p, _f32p, _f32p, _u16p,
+                                _u16p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]
+    L.orc_prefill.argtypes = [_u16p, _f32p, _u16p, _u16p, _f32p, _f32p, _u16p, _u16p,
+                              _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]
+    L.orc_num_threads.restype = _c_int
+    L.orc_baseline_step.restype = None
+    _lib = L
+    return L
+
+
+# --------------------------------------------------------------- bf16 -----
+
+def f32_to_bf16(x) -> np.ndarray:
+    """Round float32 to bf16 (round to nearest even), returned as uint16 bits.
+    Finite values and infinities cannot overflow the uint32 sum; NaNs are
+    patched to quiet NaNs afterwards."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    u = x.view(np.uint32)
+    r = ((u + np.uint32(0x7FFF) + ((u >> 16) & np.uint32(1))) >> 16).astype(np.uint16)
+    nan = np.isnan(x)
+    if nan.any():
+        r[nan] = ((u[nan] >> 16) | np.uint32(0x40)).astype(np.uint16)
+    return r
+
+
+def bf16_to_f32(h) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    return (h.astype(np.uint32) << 16).view(np.float32)
+
+
+def round_bf16(x) -> np.ndarray:
+    return bf16_to_f32(f32_to_bf16(x))
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+# -------------------------------------------------------------- steps -----
+
+def beta_g(ab, A_log, dt_bias):
+    """compiled_beta_g on merged ab [..., 2Hv] -> (beta bf16 [...,Hv], g f32 [...,Hv])."""
+    ab = _c(ab, np.uint16)
+    hv2 = ab.shape[-1]
+    Hv = hv2 // 2
+    ntok = ab.size // hv2
+    beta = np.empty(ab.shape[:-1] + (Hv,), np.uint16)
+    g = np.empty(ab.shape[:-1] + (Hv,), np.float32)
+    lib().orc_beta_g(ab, ntok, Hv, _c(A_log, np.float32), _c(dt_bias, np.float32), beta, g)
+    return beta, g
+
+
+def conv_update(conv_state, x, w):
+    """S=1 conv step. conv_state [B,K-1,D], x [B,D], w [D,K] -> (new_state, out[B,D])."""
+    conv_state = _c(conv_state, np.uint16)
+    B, km1, D = conv_state.shape
+    out = np.empty((B, D), np.uint16)
+    new = np.empty_like(conv_state)
+    lib().orc_conv_update(conv_state, _c(x, np.uint16), _c(w, np.uint16), B, D, km1 + 1, new, out)
+    return new, out
+
+
+def conv_prefill(conv_state, x, w):
+    """Prefill conv. conv_state [K-1,D], x [S,D], w [D,K] -> (new_state, out[S,D])."""
+    conv_state = _c(conv_state, np.uint16)
+    km1, D = conv_state.shape
+    x = _c(x, np.uint16)
+    S = x.shape[0]
+    out = np.empty((S, D), np.uint16)
+    new = np.empty_like(conv_state)
+    lib().orc_conv_prefill(conv_state, x, _c(w, np.uint16), S, D, km1 + 1, new, out)
+    return new, out
+
+
+def rms_norm(x, w: float, eps: float = 1e-6):
+    x = _c(x, np.uint16)
+    dim = x.shape[-1]
+    out = np.empty_like(x)
+    lib().orc_rms_norm(x, x.size // dim, dim, w, eps, out)
+    return out
+
+
+def q_norm_weight(dk: int) -> float:
+    return float(lib().orc_q_norm_weight(dk))
+
+
+def k_norm_weight(dk: int) -> float:
+    return float(lib().orc_k_norm_weight(dk))
+
+
+def recurrent(q, k, v, g, beta, state):
+    """gated_delta_kernel on q,k [B,T,Hk,Dk], v [B,T,Hv,Dv], g [B,T,Hv] f32,
+    beta [B,T,Hv] bf16, state [B,Hv,Dv,Dk] f32 -> (y [B,T,Hv,Dv], new_state)."""
+    q, k, v = _c(q, np.uint16), _c(k, np.uint16), _c(v, np.uint16)
+    B, T, Hk, Dk = q.shape
+    Hv, Dv = v.shape[2], v.shape[3]
+    st = _c(state, np.float32)
+    out_state = np.empty_like(st)
+    y = np.empty((B, T, Hv, Dv), np.uint16)
+    lib().orc_recurrent_io(q, k, v, _c(g, np.float32), _c(beta, np.uint16), st, out_state, y,
+                           B, T, Hk, Hv, Dk, Dv)
+    return y, out_state
+
+
+def recurrent_f64(q, k, v, g, beta, state):
+    """As recurrent() with f64 arithmetic; returns (y bf16, y f64, new_state f32)."""
+    q, k, v = _c(q, np.uint16), _c(k, np.uint16), _c(v, np.uint16)
+    B, T, Hk, Dk = q.shape
+    Hv, Dv = v.shape[2], v.shape[3]
+    st = np.array(state, dtype=np.float32, copy=True, order="C")
+    y = np.empty((B, T, Hv, Dv), np.uint16)
+    y64 = np.empty((B, T, Hv, Dv), np.float64)
+    lib().orc_recurrent_f64(q, k, v, _c(g, np.float32), _c(beta, np.uint16), st, y, y64,
+                            B, T, Hk, Hv, Dk, Dv)
+    return y, y64, st
+
+
+def decode(conv_state, state, mixed_qkv, ab, A_log, dt_bias, conv_w, Hk: int, Hv: int):
+    """Fused S=1 layer step on stacked states.
+    conv_state [B,K-1,D], state [B,Hv,Dv,Dk], mixed_qkv [B,D], ab [B,2Hv],
+    conv_w [D,K] -> (y [B,Hv,Dv], new_conv_state, new_state)."""
+    cs = _c(conv_state, np.uint16)
+    st = _c(state, np.float32)
+    B, km1, D = cs.shape
+    _, _, Dv, Dk = st.shape
+    cs_out = np.empty_like(cs)
+    st_out = np.empty_like(st)
+    y = np.empty((B, Hv, Dv), np.uint16)
+    lib().orc_decode_io(cs, cs_out, st, st_out, _c(mixed_qkv, np.uint16), _c(ab, np.uint16),
+                        _c(A_log, np.float32), _c(dt_bias, np.float32), _c(conv_w, np.uint16),
+                        y, B, Hk, Hv, Dk, Dv, km1 + 1)
+    return y, cs_out, st_out
+
+
+def prefill(conv_state, state, mixed_qkv, ab, A_log, dt_bias, conv_w, Hk: int, Hv: int,
+            f64: bool = False):
+    """One sequence of S tokens. conv_state [K-1,D], state [Hv,Dv,Dk],
+    mixed_qkv [S,D], ab [S,2Hv] -> (y [S,Hv,Dv], new_conv_state, new_state)."""
+    cs = np.array(conv_state, dtype=np.uint16, copy=True, order="C")
+    st = np.array(state, dtype=np.float32, copy=True, order="C")
+    km1, D = cs.shape
+    _, Dv, Dk = st.shape
+    x = _c(mixed_qkv, np.uint16)
+    S = x.shape[0]
+    y = np.empty((S, Hv, Dv), np.uint16)
+    lib().orc_prefill(cs, st, x, _c(ab, np.uint16), _c(A_log, np.float32),
+                      _c(dt_bias, np.float32), _c(conv_w, np.uint16), y, S, Hk, Hv, Dk, Dv,
+                      km1 + 1, 1 if f64 else 0)
+    return y, cs, st
+
+
+def split_qkv(x, Hk: int, Hv: int, Dk: int, Dv: int):
+    """Channel split of a conv output [..., D] into q, k [...,Hk,Dk], v [...,Hv,Dv]
+    (src/models/qwen3_5.rs:626-634)."""
+    qk = Hk * Dk
+    q = x[..., :qk].reshape(x.shape[:-1] + (Hk, Dk))
+    k = x[..., qk:2 * qk].reshape(x.shape[:-1] + (Hk, Dk))
+    v = x[..., 2 * qk:].reshape(x.shape[:-1] + (Hv, Dv))
+    return q, k, v
+
+
+def stack(pool, slot_ids):
+    """stack_caches for one GDN layer (mlx_executor.rs:42-55): gather by slot id."""
+    return np.ascontiguousarray(pool[np.asarray(slot_ids, dtype=np.int64)])
+
+
+def unstack(pool, slot_ids, batched):
+    """unstack_caches (mlx_executor.rs:118-130): scatter rows back (in place)."""
+    pool[np.asarray(slot_ids, dtype=np.int64)] = batched
+
+
+def num_threads() -> int:
+    return int(lib().orc_num_threads())
+
+
+class BaselineStep:
+    """CPU baseline of a B-sequence, L-layer decode step as the reference runs it
+    (stack by concat copy, out-of-place kernel, unstack as views); see
+    orc_baseline_step in gdn_oracle.c. Buffers are allocated once here."""
+
+    def __init__(self, L, B, Hk, Hv, Dk, Dv, K, seed=0):
+        self.L, self.B, self.Hk, self.Hv, self.Dk, self.Dv, self.K = L, B, Hk, Hv, Dk, Dv, K
+        D = 2 * Hk * Dk + Hv * Dv
+        se, ce = Hv * Dv * Dk, (K - 1) * D
+        rng = np.random.default_rng(seed)
+        # one random slot state, replicated: the timing does not depend on the values
+        one_state = rng.standard_normal(se, dtype=np.float32) * 0.01
+        one_conv = f32_to_bf16(rng.standard_normal(ce, dtype=np.float32))
+        self.seq_state_buf = np.empty((L, B, se), np.float32)
+        self.seq_state_buf[...] = one_state
+        self.seq_conv_buf = np.empty((L, B, ce), np.uint16)
+        self.seq_conv_buf[...] = one_conv
+        self.out_state = np.zeros((L, B * se), np.float32)
+        self.out_conv = np.zeros((L, B * ce), np.uint16)
+        self.in_state = np.zeros(B * se, np.float32)
+        self.in_conv = np.zeros(B * ce, np.uint16)
+        self.mixed = f32_to_bf16(rng.standard_normal((L, B, D), dtype=np.float32))
+        self.ab = f32_to_bf16(rng.standard_normal((L, B, 2 * Hv), dtype=np.float32))
+        self.A_log = rng.uniform(0, np.log(16), (L, Hv)).astype(np.float32)
+        self.dt_bias = (rng.standard_normal((L, Hv)) * 0.1).astype(np.float32)
+        self.conv_w = f32_to_bf16(rng.standard_normal((L, D, K), dtype=np.float32) * 0.25)
+        self.y = np.zeros((L, B, Hv, Dv), np.uint16)
+        P = ctypes.POINTER
+        self._ss = (P(ctypes.c_float) * (L * B))()
+        self._sc = (P(ctypes.c_uint16) * (L * B))()
+        for l in range(L):
+            for b in range(B):
+                self._ss[l * B + b] = self.seq_state_buf[l, b].ctypes.data_as(P(ctypes.c_float))
+                self._sc[l * B + b] = self.seq_conv_buf[l, b].ctypes.data_as(P(ctypes.c_uint16))
+        self._os = (P(ctypes.c_float) * L)(*[self.out_state[l].ctypes.data_as(P(ctypes.c_float))
+                                             for l in range(L)])
+        self._oc = (P(ctypes.c_uint16) * L)(*[self.out_conv[l].ctypes.data_as(P(ctypes.c_uint16))
+                                              for l in range(L)])
+
+    def step(self):
+        vp = ctypes.c_void_p
+        lib().orc_baseline_step(
+            _c_int(self.L), _c_int(self.B), self._ss, self._sc,
+            vp(self.in_state.ctypes.data), vp(self.in_conv.ctypes.data), self._os, self._oc,
+            vp(self.mixed.ctypes.data), vp(self.ab.ctypes.data), vp(self.A_log.ctypes.data),
+            vp(self.dt_bias.ctypes.data), vp(self.conv_w.ctypes.data), vp(self.y.ctypes.data),
+            _c_int(self.Hk), _c_int(self.Hv), _c_int(self.Dk), _c_int(self.Dv), _c_int(self.K))

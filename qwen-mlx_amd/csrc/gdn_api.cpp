@@ -1,0 +1,426 @@
+// gdn_api.cpp -- C ABI of libgdn: pool lifetime, slot allocator, argument
+// validation and kernel launches. See include/gdn.h for the contract.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <set>
+#include <string>
+#include <vector>
+
+#include "gdn.h"
+#include "gdn_common.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+gdn_status fail(gdn_status code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+gdn_status hip_fail(hipError_t e, const char* what) {
+  return fail(GDN_ERR_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+// Makes the pool's device current for the duration of a call.
+class DeviceGuard {
+ public:
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev_) != hipSuccess) prev_ = -1;
+    if (prev_ != dev) ok_ = hipSetDevice(dev) == hipSuccess;
+  }
+  ~DeviceGuard() {
+    if (ok_ && prev_ >= 0) {
+      int cur = -1;
+      if (hipGetDevice(&cur) == hipSuccess && cur != prev_) (void)hipSetDevice(prev_);
+    }
+  }
+  bool ok() const { return ok_; }
+
+ private:
+  int prev_ = -1;
+  bool ok_ = true;
+};
+
+}  // namespace
+
+struct gdn_pool {
+  gdn_pool_desc d{};
+  int R = 0, D = 0;
+  size_t state_elems = 0;  // per slot per layer, f32
+  size_t conv_elems = 0;   // per slot per layer, bf16
+  std::vector<float*> state;
+  std::vector<uint16_t*> conv;
+  float** d_state_ptrs = nullptr;
+  uint16_t** d_conv_ptrs = nullptr;
+  uint32_t* d_status = nullptr;
+  void* workspace = nullptr;
+  size_t workspace_bytes = 0;
+  std::set<int32_t> free_slots;
+  std::vector<uint8_t> in_use;
+};
+
+namespace {
+
+void release(gdn_pool* p) {
+  for (float* s : p->state)
+    if (s) (void)hipFree(s);
+  for (uint16_t* c : p->conv)
+    if (c) (void)hipFree(c);
+  if (p->d_state_ptrs) (void)hipFree(p->d_state_ptrs);
+  if (p->d_conv_ptrs) (void)hipFree(p->d_conv_ptrs);
+  if (p->d_status) (void)hipFree(p->d_status);
+  if (p->workspace) (void)hipFree(p->workspace);
+  delete p;
+}
+
+gdn_status check_layer(const gdn_pool* p, int32_t layer, bool allow_all) {
+  if (!p) return fail(GDN_ERR_INVALID, "pool is NULL");
+  if (allow_all && layer == GDN_ALL_LAYERS) return GDN_OK;
+  if (layer < 0 || layer >= p->d.num_layers)
+    return fail(GDN_ERR_INVALID, "layer %d outside [0, %d)", layer, p->d.num_layers);
+  return GDN_OK;
+}
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+}  // namespace
+
+extern "C" {
+
+const char* gdn_last_error(void) { return g_err.c_str(); }
+
+const char* gdn_version(void) { return "gdn 0.1 gfx950"; }
+
+gdn_status gdn_pool_create(const gdn_pool_desc* desc, gdn_pool** out) {
+  if (!desc || !out) return fail(GDN_ERR_INVALID, "desc/out is NULL");
+  *out = nullptr;
+  const gdn_pool_desc& d = *desc;
+  if (d.num_layers < 1 || d.num_slots < 1 || d.num_k_heads < 1 || d.num_v_heads < 1)
+    return fail(GDN_ERR_INVALID, "num_layers/num_slots/heads must be >= 1");
+  if (d.num_v_heads % d.num_k_heads != 0)
+    return fail(GDN_ERR_INVALID, "num_v_heads (%d) not a multiple of num_k_heads (%d)",
+                d.num_v_heads, d.num_k_heads);
+  const int R = d.num_v_heads / d.num_k_heads;
+  if (R != 1 && R != 2 && R != 4)
+    return fail(GDN_ERR_UNSUPPORTED, "num_v_heads/num_k_heads = %d not in {1,2,4}", R);
+  if (d.head_k_dim != gdn::kDk || d.head_v_dim != gdn::kDv)
+    return fail(GDN_ERR_UNSUPPORTED, "head dims %dx%d unsupported (compiled for 128x128)",
+                d.head_k_dim, d.head_v_dim);
+  if (d.conv_kernel != gdn::kConvK)
+    return fail(GDN_ERR_UNSUPPORTED, "conv_kernel %d unsupported (compiled for 4)", d.conv_kernel);
+  int ndev = 0;
+  hipError_t e = hipGetDeviceCount(&ndev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+  if (d.device < 0 || d.device >= ndev)
+    return fail(GDN_ERR_INVALID, "device %d outside [0, %d)", d.device, ndev);
+  DeviceGuard guard(d.device);
+  if (!guard.ok()) return fail(GDN_ERR_HIP, "hipSetDevice(%d) failed", d.device);
+
+  gdn_pool* p = new gdn_pool();
+  p->d = d;
+  p->R = R;
+  p->D = 2 * d.num_k_heads * gdn::kDk + d.num_v_heads * gdn::kDv;
+  p->state_elems = (size_t)d.num_v_heads * gdn::kTileElems;
+  p->conv_elems = (size_t)(gdn::kConvK - 1) * p->D;
+  p->state.assign(d.num_layers, nullptr);
+  p->conv.assign(d.num_layers, nullptr);
+  const size_t sbytes = p->state_elems * sizeof(float) * (size_t)d.num_slots;
+  const size_t cbytes = p->conv_elems * sizeof(uint16_t) * (size_t)d.num_slots;
+  for (int l = 0; l < d.num_layers; ++l) {
+    if (hipMalloc(&p->state[l], sbytes) != hipSuccess ||
+        hipMalloc(&p->conv[l], cbytes) != hipSuccess) {
+      (void)hipGetLastError();
+      release(p);
+      return fail(GDN_ERR_OOM, "hipMalloc of layer %d (%zu + %zu bytes) failed", l, sbytes,
+                  cbytes);
+    }
+    if ((e = hipMemset(p->state[l], 0, sbytes)) != hipSuccess ||
+        (e = hipMemset(p->conv[l], 0, cbytes)) != hipSuccess) {
+      release(p);
+      return hip_fail(e, "hipMemset(pool)");
+    }
+  }
+  if (hipMalloc(&p->d_state_ptrs, sizeof(float*) * d.num_layers) != hipSuccess ||
+      hipMalloc(&p->d_conv_ptrs, sizeof(uint16_t*) * d.num_layers) != hipSuccess ||
+      hipMalloc(&p->d_status, sizeof(uint32_t)) != hipSuccess) {
+    (void)hipGetLastError();
+    release(p);
+    return fail(GDN_ERR_OOM, "hipMalloc of pool tables failed");
+  }
+  if ((e = hipMemcpy(p->d_state_ptrs, p->state.data(), sizeof(float*) * d.num_layers,
+                     hipMemcpyHostToDevice)) != hipSuccess ||
+      (e = hipMemcpy(p->d_conv_ptrs, p->conv.data(), sizeof(uint16_t*) * d.num_layers,
+                     hipMemcpyHostToDevice)) != hipSuccess ||
+      (e = hipMemset(p->d_status, 0, sizeof(uint32_t))) != hipSuccess ||
+      (e = hipDeviceSynchronize()) != hipSuccess) {
+    release(p);
+    return hip_fail(e, "pool table upload");
+  }
+  for (int32_t s = 0; s < d.num_slots; ++s) p->free_slots.insert(s);
+  p->in_use.assign(d.num_slots, 0);
+  *out = p;
+  return GDN_OK;
+}
+
+gdn_status gdn_pool_destroy(gdn_pool* pool) {
+  if (!pool) return GDN_OK;
+  DeviceGuard guard(pool->d.device);
+  hipError_t e = hipDeviceSynchronize();
+  release(pool);
+  if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize before pool release");
+  return GDN_OK;
+}
+
+gdn_status gdn_pool_layer_state(gdn_pool* pool, int32_t layer, float** state,
+                                uint16_t** conv_state) {
+  gdn_status st = check_layer(pool, layer, false);
+  if (st) return st;
+  if (state) *state = pool->state[layer];
+  if (conv_state) *conv_state = pool->conv[layer];
+  return GDN_OK;
+}
+
+gdn_status gdn_pool_slot_bytes(const gdn_pool* pool, size_t* state_bytes, size_t* conv_bytes) {
+  if (!pool) return fail(GDN_ERR_INVALID, "pool is NULL");
+  if (state_bytes) *state_bytes = pool->state_elems * sizeof(float);
+  if (conv_bytes) *conv_bytes = pool->conv_elems * sizeof(uint16_t);
+  return GDN_OK;
+}
+
+gdn_status gdn_pool_check(gdn_pool* pool, void* stream, uint32_t* flags) {
+  if (!pool || !flags) return fail(GDN_ERR_INVALID, "pool/flags is NULL");
+  DeviceGuard guard(pool->d.device);
+  hipError_t e = hipStreamSynchronize(as_stream(stream));
+  if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+  uint32_t v = 0;
+  if ((e = hipMemcpy(&v, pool->d_status, sizeof(v), hipMemcpyDeviceToHost)) != hipSuccess)
+    return hip_fail(e, "read status");
+  if ((e = hipMemset(pool->d_status, 0, sizeof(v))) != hipSuccess) return hip_fail(e, "clear status");
+  if ((e = hipDeviceSynchronize()) != hipSuccess) return hip_fail(e, "clear status sync");
+  *flags = v;
+  return GDN_OK;
+}
+
+gdn_status gdn_slot_alloc(gdn_pool* pool, int32_t* slot) {
+  if (!pool || !slot) return fail(GDN_ERR_INVALID, "pool/slot is NULL");
+  if (pool->free_slots.empty())
+    return fail(GDN_ERR_SLOTS, "no free slot (pool holds %d)", pool->d.num_slots);
+  const int32_t s = *pool->free_slots.begin();
+  pool->free_slots.erase(pool->free_slots.begin());
+  pool->in_use[s] = 1;
+  *slot = s;
+  return GDN_OK;
+}
+
+gdn_status gdn_slot_free(gdn_pool* pool, int32_t slot) {
+  if (!pool) return fail(GDN_ERR_INVALID, "pool is NULL");
+  if (slot < 0 || slot >= pool->d.num_slots)
+    return fail(GDN_ERR_SLOTS, "slot %d outside [0, %d)", slot, pool->d.num_slots);
+  if (!pool->in_use[slot]) return fail(GDN_ERR_SLOTS, "slot %d is not allocated", slot);
+  pool->in_use[slot] = 0;
+  pool->free_slots.insert(slot);
+  return GDN_OK;
+}
+
+gdn_status gdn_slots_in_use(const gdn_pool* pool, int32_t* count) {
+  if (!pool || !count) return fail(GDN_ERR_INVALID, "pool/count is NULL");
+  *count = pool->d.num_slots - (int32_t)pool->free_slots.size();
+  return GDN_OK;
+}
+
+static gdn_status slot_move(gdn_pool* pool, int32_t layer, const int32_t* slot_ids, int32_t n,
+                            float* sbuf, uint16_t* cbuf, gdn::SlotOp op, void* stream,
+                            const char* what) {
+  gdn_status st = check_layer(pool, layer, op == gdn::SlotOp::kZero);
+  if (st) return st;
+  if (n < 0) return fail(GDN_ERR_INVALID, "%s: n = %d < 0", what, n);
+  if (n == 0) return GDN_OK;
+  if (!slot_ids) return fail(GDN_ERR_INVALID, "%s: slot_ids is NULL", what);
+  if (n > 65535) return fail(GDN_ERR_INVALID, "%s: n = %d > 65535", what, n);
+  DeviceGuard guard(pool->d.device);
+  gdn::SlotArgs a{};
+  a.op = op;
+  a.layers.state = pool->d_state_ptrs;
+  a.layers.conv = pool->d_conv_ptrs;
+  a.layer0 = layer == GDN_ALL_LAYERS ? 0 : layer;
+  a.nlayers = layer == GDN_ALL_LAYERS ? pool->d.num_layers : 1;
+  a.n = n;
+  a.num_slots = pool->d.num_slots;
+  a.Hv = pool->d.num_v_heads;
+  a.conv_elems = (int)pool->conv_elems;
+  a.slot_ids = slot_ids;
+  a.state_buf = sbuf;
+  a.conv_buf = cbuf;
+  a.status = pool->d_status;
+  a.stream = as_stream(stream);
+  hipError_t e = gdn::launch_slots(a);
+  if (e != hipSuccess) return hip_fail(e, what);
+  return GDN_OK;
+}
+
+gdn_status gdn_slots_zero(gdn_pool* pool, int32_t layer, const int32_t* slot_ids, int32_t n,
+                          void* stream) {
+  return slot_move(pool, layer, slot_ids, n, nullptr, nullptr, gdn::SlotOp::kZero, stream,
+                   "gdn_slots_zero");
+}
+
+gdn_status gdn_slots_read(gdn_pool* pool, int32_t layer, const int32_t* slot_ids, int32_t n,
+                          float* state_out, uint16_t* conv_out, void* stream) {
+  return slot_move(pool, layer, slot_ids, n, state_out, conv_out, gdn::SlotOp::kRead, stream,
+                   "gdn_slots_read");
+}
+
+gdn_status gdn_slots_write(gdn_pool* pool, int32_t layer, const int32_t* slot_ids, int32_t n,
+                           const float* state_in, const uint16_t* conv_in, void* stream) {
+  return slot_move(pool, layer, slot_ids, n, const_cast<float*>(state_in),
+                   const_cast<uint16_t*>(conv_in), gdn::SlotOp::kWrite, stream,
+                   "gdn_slots_write");
+}
+
+gdn_status gdn_slots_validate(gdn_pool* pool, const int32_t* slot_ids, int32_t n, void* stream) {
+  if (!pool) return fail(GDN_ERR_INVALID, "pool is NULL");
+  if (n < 0) return fail(GDN_ERR_INVALID, "n = %d < 0", n);
+  if (n == 0) return GDN_OK;
+  if (!slot_ids) return fail(GDN_ERR_INVALID, "slot_ids is NULL");
+  DeviceGuard guard(pool->d.device);
+  hipError_t e = gdn::launch_validate(slot_ids, n, pool->d.num_slots, pool->d_status,
+                                      as_stream(stream));
+  if (e != hipSuccess) return hip_fail(e, "gdn_slots_validate");
+  return GDN_OK;
+}
+
+gdn_status gdn_recurrent(gdn_pool* pool, int32_t layer, const int32_t* slot_ids, int32_t B,
+                         int32_t T, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                         const float* g, const uint16_t* beta, uint16_t* y, void* stream) {
+  gdn_status st = check_layer(pool, layer, false);
+  if (st) return st;
+  if (B < 0 || T < 0) return fail(GDN_ERR_INVALID, "B = %d, T = %d must be >= 0", B, T);
+  if (B == 0 || T == 0) return GDN_OK;
+  if (B > 65535) return fail(GDN_ERR_INVALID, "B = %d > 65535", B);
+  if (!slot_ids || !q || !k || !v || !g || !beta || !y)
+    return fail(GDN_ERR_INVALID, "gdn_recurrent: NULL tensor pointer");
+  DeviceGuard guard(pool->d.device);
+  gdn::RecurrentArgs a{};
+  a.R = pool->R;
+  a.Hk = pool->d.num_k_heads;
+  a.B = B;
+  a.T = T;
+  a.num_slots = pool->d.num_slots;
+  a.state = pool->state[layer];
+  a.slot_ids = slot_ids;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.g = g;
+  a.beta = beta;
+  a.y = y;
+  a.status = pool->d_status;
+  a.stream = as_stream(stream);
+  hipError_t e = gdn::launch_recurrent(a);
+  if (e != hipSuccess) return hip_fail(e, "gdn_recurrent launch");
+  return GDN_OK;
+}
+
+gdn_status gdn_decode(gdn_pool* pool, int32_t layer, const int32_t* slot_ids, int32_t B,
+                      const uint16_t* mixed_qkv, const uint16_t* ab, const float* A_log,
+                      const float* dt_bias, const uint16_t* conv_w, uint16_t* y, void* stream) {
+  gdn_status st = check_layer(pool, layer, false);
+  if (st) return st;
+  if (B < 0) return fail(GDN_ERR_INVALID, "B = %d < 0", B);
+  if (B == 0) return GDN_OK;
+  if (B > 65535) return fail(GDN_ERR_INVALID, "B = %d > 65535", B);
+  if (!slot_ids || !mixed_qkv || !ab || !A_log || !dt_bias || !conv_w || !y)
+    return fail(GDN_ERR_INVALID, "gdn_decode: NULL tensor pointer");
+  if (reinterpret_cast<uintptr_t>(conv_w) % 8 != 0)
+    return fail(GDN_ERR_INVALID, "gdn_decode: conv_w must be 8-byte aligned");
+  DeviceGuard guard(pool->d.device);
+  gdn::DecodeArgs a{};
+  a.R = pool->R;
+  a.Hk = pool->d.num_k_heads;
+  a.B = B;
+  a.num_slots = pool->d.num_slots;
+  a.state = pool->state[layer];
+  a.conv = pool->conv[layer];
+  a.slot_ids = slot_ids;
+  a.mixed = mixed_qkv;
+  a.ab = ab;
+  a.A_log = A_log;
+  a.dt_bias = dt_bias;
+  a.conv_w = conv_w;
+  a.y = y;
+  a.status = pool->d_status;
+  a.stream = as_stream(stream);
+  hipError_t e = gdn::launch_decode(a);
+  if (e != hipSuccess) return hip_fail(e, "gdn_decode launch");
+  return GDN_OK;
+}
+
+gdn_status gdn_prefill_varlen(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
+                              const int32_t* cu_seqlens, int32_t nseq, int32_t total_tokens,
+                              const uint16_t* mixed_qkv, const uint16_t* ab, const float* A_log,
+                              const float* dt_bias, const uint16_t* conv_w, uint16_t* y,
+                              void* stream) {
+  gdn_status st = check_layer(pool, layer, false);
+  if (st) return st;
+  if (nseq < 0 || total_tokens < 0)
+    return fail(GDN_ERR_INVALID, "nseq = %d, total_tokens = %d must be >= 0", nseq, total_tokens);
+  if (nseq == 0) return GDN_OK;
+  if (nseq > 65535) return fail(GDN_ERR_INVALID, "nseq = %d > 65535", nseq);
+  if (!slot_ids || !cu_seqlens || !A_log || !dt_bias || !conv_w)
+    return fail(GDN_ERR_INVALID, "gdn_prefill_varlen: NULL pointer");
+  if (total_tokens > 0 && (!mixed_qkv || !ab || !y))
+    return fail(GDN_ERR_INVALID, "gdn_prefill_varlen: NULL token tensor");
+  if (reinterpret_cast<uintptr_t>(conv_w) % 8 != 0)
+    return fail(GDN_ERR_INVALID, "gdn_prefill_varlen: conv_w must be 8-byte aligned");
+  DeviceGuard guard(pool->d.device);
+  const size_t need = gdn::prefill_workspace_bytes(pool->R, pool->d.num_k_heads, total_tokens);
+  if (need > pool->workspace_bytes) {
+    hipError_t e;
+    if (pool->workspace) {
+      if ((e = hipStreamSynchronize(as_stream(stream))) != hipSuccess)
+        return hip_fail(e, "workspace grow sync");
+      (void)hipFree(pool->workspace);
+      pool->workspace = nullptr;
+      pool->workspace_bytes = 0;
+    }
+    if (hipMalloc(&pool->workspace, need) != hipSuccess) {
+      (void)hipGetLastError();
+      pool->workspace = nullptr;
+      return fail(GDN_ERR_OOM, "prefill workspace of %zu bytes", need);
+    }
+    pool->workspace_bytes = need;
+  }
+  gdn::PrefillArgs a{};
+  a.R = pool->R;
+  a.Hk = pool->d.num_k_heads;
+  a.nseq = nseq;
+  a.total_tokens = total_tokens;
+  a.num_slots = pool->d.num_slots;
+  a.state = pool->state[layer];
+  a.conv = pool->conv[layer];
+  a.slot_ids = slot_ids;
+  a.cu_seqlens = cu_seqlens;
+  a.mixed = mixed_qkv;
+  a.ab = ab;
+  a.A_log = A_log;
+  a.dt_bias = dt_bias;
+  a.conv_w = conv_w;
+  a.y = y;
+  a.status = pool->d_status;
+  a.workspace = pool->workspace;
+  a.workspace_bytes = pool->workspace_bytes;
+  a.stream = as_stream(stream);
+  hipError_t e = gdn::launch_prefill(a);
+  if (e != hipSuccess) return hip_fail(e, "gdn_prefill_varlen launch");
+  return GDN_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,155 @@
+// gdn_common.h -- shared definitions of libgdn's gfx950 kernels and host code.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gdn.h"
+
+namespace gdn {
+
+// Compiled kernel family: Dk = Dv = 128, conv width 4. The value/key head
+// ratio R = Hv / Hk is a template parameter (1, 2 or 4).
+constexpr int kDk = 128;
+constexpr int kDv = 128;
+constexpr int kConvK = 4;
+constexpr int kTileElems = kDv * kDk;  // one (slot, value head) recurrent tile
+
+// Native 4 x f32 vector (16-byte loads/stores, usable with the nontemporal
+// builtins).
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// Per-layer device pointers handed to kernels that span several layers.
+struct LayerPtrs {
+  float** state;      // [L] -> [num_slots, Hv, Dv, Dk]
+  uint16_t** conv;    // [L] -> [num_slots, K-1, D]
+};
+
+// ------------------------------------------------------------------ bf16 --
+__device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// Round to nearest even (quiet NaN preserved), as the CPU restatement does.
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+
+// MLX's f32 sigmoid: 1/(1+exp(-|x|)), mirrored for x < 0.
+__device__ __forceinline__ float sigmoid_f32(float x) {
+  float y = 1.0f / (1.0f + expf(-fabsf(x)));
+  return x < 0.0f ? 1.0f - y : y;
+}
+
+// silu on a bf16 value with each elementwise op rounded to bf16.
+__device__ __forceinline__ float silu_bf16(float x) { return rbf(x * rbf(sigmoid_f32(x))); }
+
+// --------------------------------------------------------- lane reductions --
+// DPP moves within a 16-lane row: quad_perm xor-1 / xor-2, and row_half_mirror
+// (lane i <- lane 7-i inside each group of 8).
+__device__ __forceinline__ float dpp_quad_xor1(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float dpp_quad_xor2(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float dpp_half_mirror(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+}
+
+// Sum over the 8 aligned lanes (lane & ~7) of a wave; every lane of the group
+// receives the same bits.
+__device__ __forceinline__ float sum8(float v) {
+  v += dpp_quad_xor1(v);
+  v += dpp_quad_xor2(v);
+  v += dpp_half_mirror(v);
+  return v;
+}
+
+// Sum over a full 64-lane wave (result in every lane).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ void flag_status(uint32_t* status, uint32_t bit) {
+  if (status) atomicOr(status, bit);
+}
+
+}  // namespace gdn
+
+// ------------------------------------------------- host launch interface --
+namespace gdn {
+
+struct DecodeArgs {
+  int R, Hk, B, num_slots;
+  float* state;
+  uint16_t* conv;
+  const int32_t* slot_ids;
+  const uint16_t* mixed;
+  const uint16_t* ab;
+  const float* A_log;
+  const float* dt_bias;
+  const uint16_t* conv_w;
+  uint16_t* y;
+  uint32_t* status;
+  hipStream_t stream;
+};
+
+struct RecurrentArgs {
+  int R, Hk, B, T, num_slots;
+  float* state;
+  const int32_t* slot_ids;
+  const uint16_t *q, *k, *v;
+  const float* g;
+  const uint16_t* beta;
+  uint16_t* y;
+  uint32_t* status;
+  hipStream_t stream;
+};
+
+enum class SlotOp { kZero = 0, kRead = 1, kWrite = 2 };
+
+struct SlotArgs {
+  SlotOp op;
+  LayerPtrs layers;     // device arrays of per-layer base pointers
+  int layer0, nlayers;  // layers [layer0, layer0 + nlayers)
+  int n, num_slots, Hv, conv_elems;  // conv_elems = (K-1)*D per slot
+  const int32_t* slot_ids;
+  float* state_buf;     // read: destination [n,...]; write: source
+  uint16_t* conv_buf;
+  uint32_t* status;
+  hipStream_t stream;
+};
+
+struct PrefillArgs {
+  int R, Hk, nseq, total_tokens, num_slots;
+  float* state;
+  uint16_t* conv;
+  const int32_t* slot_ids;
+  const int32_t* cu_seqlens;
+  const uint16_t* mixed;
+  const uint16_t* ab;
+  const float* A_log;
+  const float* dt_bias;
+  const uint16_t* conv_w;
+  uint16_t* y;
+  uint32_t* status;
+  void* workspace;       // device scratch sized by prefill_workspace_bytes
+  size_t workspace_bytes;
+  hipStream_t stream;
+};
+
+hipError_t launch_decode(const DecodeArgs& a);
+hipError_t launch_recurrent(const RecurrentArgs& a);
+hipError_t launch_slots(const SlotArgs& a);
+hipError_t launch_validate(const int32_t* slot_ids, int n, int num_slots, uint32_t* status,
+                           hipStream_t stream);
+size_t prefill_workspace_bytes(int R, int Hk, int total_tokens);
+hipError_t launch_prefill(const PrefillArgs& a);
+
+}  // namespace gdn

@@ -1,0 +1,223 @@
+"""ctypes binding of libgdn (include/gdn.h) for torch device tensors.
+
+The library is the product; this module only passes device pointers across
+the C ABI. It never computes anything itself and has no CPU fallback: if
+lib/libgdn.so is missing or the GPU is absent, calls raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+_PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG_ROOT, "lib", "libgdn.so")
+HEADER_PATH = os.path.join(os.path.dirname(_PKG_ROOT), "include", "gdn.h")
+
+GDN_OK = 0
+GDN_ERR_INVALID = 1
+GDN_ERR_UNSUPPORTED = 2
+GDN_ERR_HIP = 3
+GDN_ERR_OOM = 4
+GDN_ERR_SLOTS = 5
+GDN_FLAG_BAD_SLOT = 0x1
+GDN_FLAG_DUP_SLOT = 0x2
+GDN_FLAG_BAD_SEQLENS = 0x4
+GDN_ALL_LAYERS = -1
+
+# Exported symbols and their signatures (restype is int status unless noted).
+_VP = ctypes.c_void_p
+_I32 = ctypes.c_int32
+SIGNATURES = {
+    "gdn_last_error": ([], ctypes.c_char_p),
+    "gdn_version": ([], ctypes.c_char_p),
+    "gdn_pool_create": ([_VP, ctypes.POINTER(_VP)], ctypes.c_int),
+    "gdn_pool_destroy": ([_VP], ctypes.c_int),
+    "gdn_pool_layer_state": ([_VP, _I32, ctypes.POINTER(_VP), ctypes.POINTER(_VP)], ctypes.c_int),
+    "gdn_pool_slot_bytes": ([_VP, ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)],
+                            ctypes.c_int),
+    "gdn_pool_check": ([_VP, _VP, ctypes.POINTER(ctypes.c_uint32)], ctypes.c_int),
+    "gdn_slot_alloc": ([_VP, ctypes.POINTER(_I32)], ctypes.c_int),
+    "gdn_slot_free": ([_VP, _I32], ctypes.c_int),
+    "gdn_slots_in_use": ([_VP, ctypes.POINTER(_I32)], ctypes.c_int),
+    "gdn_slots_zero": ([_VP, _I32, _VP, _I32, _VP], ctypes.c_int),
+    "gdn_slots_read": ([_VP, _I32, _VP, _I32, _VP, _VP, _VP], ctypes.c_int),
+    "gdn_slots_write": ([_VP, _I32, _VP, _I32, _VP, _VP, _VP], ctypes.c_int),
+    "gdn_slots_validate": ([_VP, _VP, _I32, _VP], ctypes.c_int),
+    "gdn_recurrent": ([_VP, _I32, _VP, _I32, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _VP],
+                      ctypes.c_int),
+    "gdn_decode": ([_VP, _I32, _VP, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _VP], ctypes.c_int),
+    "gdn_prefill_varlen": ([_VP, _I32, _VP, _VP, _I32, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _VP],
+                           ctypes.c_int),
+}
+
+
+class GdnError(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"libgdn status {status}: {msg}")
+        self.status = status
+
+
+class PoolDesc(ctypes.Structure):
+    _fields_ = [("num_layers", _I32), ("num_slots", _I32), ("num_k_heads", _I32),
+                ("num_v_heads", _I32), ("head_k_dim", _I32), ("head_v_dim", _I32),
+                ("conv_kernel", _I32), ("device", _I32)]
+
+
+_lib = None
+
+
+def build(jobs: int = 4) -> str:
+    """Compile lib/libgdn.so for gfx950 with the package Makefile (hipcc)."""
+    subprocess.run(["make", "-s", f"-j{jobs}", "-C", _PKG_ROOT, "lib/libgdn.so"], check=True)
+    return LIB_PATH
+
+
+def load(path: str = LIB_PATH):
+    """Load libgdn.so and bind its signatures. Raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is not built; run __graft_entry__.build()")
+    lib = ctypes.CDLL(path)
+    for name, (args, res) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = lib
+    return lib
+
+
+def _check(status: int):
+    if status != GDN_OK:
+        raise GdnError(status, load().gdn_last_error().decode())
+
+
+def _ptr(t) -> int | None:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("libgdn takes device tensors")
+    if not t.is_contiguous():
+        raise ValueError("libgdn takes contiguous tensors")
+    return t.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    import torch
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream
+
+
+class Pool:
+    """Device-resident GDN state pool: per layer [slots,Hv,Dv,Dk] f32 recurrent
+    state and [slots,K-1,D] bf16 conv state. Tensors passed in are torch device
+    tensors; bf16 tensors may be torch.bfloat16 or int16/uint16 bit patterns."""
+
+    def __init__(self, num_layers: int, num_slots: int, num_k_heads: int = 16,
+                 num_v_heads: int = 32, head_k_dim: int = 128, head_v_dim: int = 128,
+                 conv_kernel: int = 4, device: int = 0):
+        self.lib = load()
+        self.desc = PoolDesc(num_layers, num_slots, num_k_heads, num_v_heads, head_k_dim,
+                             head_v_dim, conv_kernel, device)
+        h = _VP()
+        _check(self.lib.gdn_pool_create(ctypes.byref(self.desc), ctypes.byref(h)))
+        self.handle = h
+        self.L, self.S = num_layers, num_slots
+        self.Hk, self.Hv, self.Dk, self.Dv, self.K = (num_k_heads, num_v_heads, head_k_dim,
+                                                       head_v_dim, conv_kernel)
+        self.D = 2 * num_k_heads * head_k_dim + num_v_heads * head_v_dim
+        self.device = device
+
+    def close(self):
+        if getattr(self, "handle", None):
+            _check(self.lib.gdn_pool_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- views of the pool memory (no copies) --
+    def layer_views(self, layer: int):
+        """(state [S,Hv,Dv,Dk] f32, conv [S,K-1,D] int16) torch views of one layer."""
+        import torch
+        sp, cp = _VP(), _VP()
+        _check(self.lib.gdn_pool_layer_state(self.handle, layer, ctypes.byref(sp), ctypes.byref(cp)))
+        n_state = self.S * self.Hv * self.Dv * self.Dk
+        n_conv = self.S * (self.K - 1) * self.D
+        state = _wrap_device(sp.value, n_state, torch.float32, self.device).view(
+            self.S, self.Hv, self.Dv, self.Dk)
+        conv = _wrap_device(cp.value, n_conv, torch.int16, self.device).view(
+            self.S, self.K - 1, self.D)
+        return state, conv
+
+    def check(self, stream=None) -> int:
+        f = ctypes.c_uint32()
+        _check(self.lib.gdn_pool_check(self.handle, _stream(stream), ctypes.byref(f)))
+        return f.value
+
+    def alloc_slot(self) -> int:
+        s = _I32()
+        _check(self.lib.gdn_slot_alloc(self.handle, ctypes.byref(s)))
+        return s.value
+
+    def free_slot(self, slot: int):
+        _check(self.lib.gdn_slot_free(self.handle, slot))
+
+    def slots_in_use(self) -> int:
+        c = _I32()
+        _check(self.lib.gdn_slots_in_use(self.handle, ctypes.byref(c)))
+        return c.value
+
+    def zero(self, layer: int, slot_ids, stream=None):
+        _check(self.lib.gdn_slots_zero(self.handle, layer, _ptr(slot_ids), slot_ids.numel(),
+                                       _stream(stream)))
+
+    def read(self, layer: int, slot_ids, state_out=None, conv_out=None, stream=None):
+        _check(self.lib.gdn_slots_read(self.handle, layer, _ptr(slot_ids), slot_ids.numel(),
+                                       _ptr(state_out), _ptr(conv_out), _stream(stream)))
+
+    def write(self, layer: int, slot_ids, state_in=None, conv_in=None, stream=None):
+        _check(self.lib.gdn_slots_write(self.handle, layer, _ptr(slot_ids), slot_ids.numel(),
+                                        _ptr(state_in), _ptr(conv_in), _stream(stream)))
+
+    def validate(self, slot_ids, stream=None):
+        _check(self.lib.gdn_slots_validate(self.handle, _ptr(slot_ids), slot_ids.numel(),
+                                           _stream(stream)))
+
+    def recurrent(self, layer, slot_ids, q, k, v, g, beta, y, stream=None):
+        B, T = q.shape[0], q.shape[1]
+        _check(self.lib.gdn_recurrent(self.handle, layer, _ptr(slot_ids), B, T, _ptr(q), _ptr(k),
+                                      _ptr(v), _ptr(g), _ptr(beta), _ptr(y), _stream(stream)))
+
+    def decode(self, layer, slot_ids, mixed_qkv, ab, A_log, dt_bias, conv_w, y, stream=None):
+        _check(self.lib.gdn_decode(self.handle, layer, _ptr(slot_ids), slot_ids.numel(),
+                                   _ptr(mixed_qkv), _ptr(ab), _ptr(A_log), _ptr(dt_bias),
+                                   _ptr(conv_w), _ptr(y), _stream(stream)))
+
+    def prefill(self, layer, slot_ids, cu_seqlens, total_tokens, mixed_qkv, ab, A_log, dt_bias,
+                conv_w, y, stream=None):
+        _check(self.lib.gdn_prefill_varlen(self.handle, layer, _ptr(slot_ids), _ptr(cu_seqlens),
+                                           slot_ids.numel(), total_tokens, _ptr(mixed_qkv),
+                                           _ptr(ab), _ptr(A_log), _ptr(dt_bias), _ptr(conv_w),
+                                           _ptr(y), _stream(stream)))
+
+
+def _wrap_device(ptr: int, numel: int, dtype, device: int):
+    """Zero-copy torch view of device memory owned by the pool."""
+    import torch
+
+    class _Holder:
+        def __init__(self, p, n, nbytes):
+            self.__cuda_array_interface__ = {
+                "shape": (n,), "typestr": {torch.float32: "<f4", torch.int16: "<i2"}[dtype],
+                "data": (p, False), "version": 3, "strides": None,
+            }
+    esz = torch.empty(0, dtype=dtype).element_size()
+    with torch.cuda.device(device):
+        return torch.as_tensor(_Holder(ptr, numel, numel * esz), device=f"cuda:{device}")

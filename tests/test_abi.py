@@ -1,0 +1,58 @@
+"""CPU checks of the C ABI: libgdn.so loads, exports every function that
+include/gdn.h declares, and rejects bad arguments on the host (no GPU call)."""
+import ctypes
+import re
+
+import pytest
+
+import gdn_amd
+
+
+def _declared():
+    src = open(gdn_amd.HEADER_PATH).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(gdn_[a-z_0-9]+)\s*\(", src)))
+
+
+def test_header_declares_the_bound_functions():
+    assert _declared() == sorted(gdn_amd.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = gdn_amd.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert b"gfx950" in lib.gdn_version()
+
+
+def test_invalid_pool_descriptors_fail_on_host():
+    lib = gdn_amd.load()
+    h = ctypes.c_void_p()
+    cases = [
+        (gdn_amd.PoolDesc(0, 4, 16, 32, 128, 128, 4, 0), gdn_amd.GDN_ERR_INVALID),
+        (gdn_amd.PoolDesc(1, 4, 16, 24, 128, 128, 4, 0), gdn_amd.GDN_ERR_INVALID),
+        (gdn_amd.PoolDesc(1, 4, 4, 32, 128, 128, 4, 0), gdn_amd.GDN_ERR_UNSUPPORTED),
+        (gdn_amd.PoolDesc(1, 4, 16, 32, 64, 128, 4, 0), gdn_amd.GDN_ERR_UNSUPPORTED),
+        (gdn_amd.PoolDesc(1, 4, 16, 32, 128, 128, 3, 0), gdn_amd.GDN_ERR_UNSUPPORTED),
+    ]
+    for desc, code in cases:
+        assert lib.gdn_pool_create(ctypes.byref(desc), ctypes.byref(h)) == code
+        assert h.value is None
+        assert lib.gdn_last_error()
+    assert lib.gdn_pool_create(None, ctypes.byref(h)) == gdn_amd.GDN_ERR_INVALID
+
+
+def test_null_pool_is_rejected():
+    lib = gdn_amd.load()
+    assert lib.gdn_decode(None, 0, None, 1, None, None, None, None, None, None, None) \
+        == gdn_amd.GDN_ERR_INVALID
+    assert b"NULL" in lib.gdn_last_error()
+    assert lib.gdn_pool_destroy(None) == gdn_amd.GDN_OK
+    assert lib.gdn_slot_free(None, 0) == gdn_amd.GDN_ERR_INVALID
+
+
+def test_product_has_no_cpu_fallback():
+    """The binding only forwards device pointers: host tensors are refused."""
+    import torch
+    with pytest.raises(ValueError):
+        gdn_amd._ptr(torch.zeros(4))

@@ -1,0 +1,128 @@
+"""GPU parity of the varlen prefill (gdn_prefill_varlen) against the oracle's
+sequential per-sequence prefill (the reference prefills one sequence at a
+time with one T-long recurrence launch), including the hand-off of final
+recurrent and conv states into slots for later decode steps."""
+import numpy as np
+import pytest
+
+from gdn_testlib import (O, DK, DV, K, conv_dim, dev, gen_layer_params, gen_states, gen_tokens,
+                         host, rel_l2, say)
+
+pytestmark = pytest.mark.gpu
+
+Y_TOL = 2e-2
+STATE_TOL = 1e-3
+
+
+def _ids(lst):
+    return dev(np.asarray(lst, np.int32))
+
+
+def _run_prefill(pool, layer, slots, lens, mixed, ab, p, gpu):
+    import torch
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    total = int(cu[-1])
+    Hv = pool.Hv
+    y = torch.zeros((max(total, 1), Hv, DV), dtype=torch.int16, device=gpu)
+    pool.prefill(layer, _ids(slots), dev(cu), total, dev(mixed) if total else None,
+                 dev(ab) if total else None, dev(p["A_log"]), dev(p["dt_bias"]), dev(p["conv_w"]),
+                 y if total else None)
+    return host(y)[:total], cu
+
+
+def _read(pool, layer, slots, gpu):
+    import torch
+    n = len(slots)
+    s = torch.empty((n, pool.Hv, DV, DK), dtype=torch.float32, device=gpu)
+    c = torch.empty((n, K - 1, pool.D), dtype=torch.int16, device=gpu)
+    pool.read(layer, _ids(slots), s, c)
+    return host(s), host(c)
+
+
+def test_prefill_mixed_batch_config3(gpu):
+    """4 prefills {128, 512, 1000, 2048} (the 1000 one ends in a partial
+    64-token chunk) + 28 single-token decodes in one layer, then 3 decode
+    steps for all 32 sequences from the handed-off states."""
+    import gdn_amd
+    import torch
+    Hk, Hv = 16, 32
+    lens = [128, 512, 1000, 2048]
+    say("gdn_prefill_varlen", f"config3 lens={lens} + 28 decode, seed=500")
+    rng = np.random.default_rng(500)
+    pool = gdn_amd.Pool(1, 48, Hk, Hv)
+    p = gen_layer_params(rng, Hk, Hv)
+    slots = rng.permutation(48)[:32].astype(np.int32)
+    pre_slots, dec_slots = slots[:4], slots[4:]
+    # decode sequences carry random states; prefill slots are admitted (zeroed)
+    dst, dcs = gen_states(rng, 28, Hk, Hv)
+    pool.write(0, _ids(dec_slots), dev(dst), dev(dcs))
+    pool.zero(0, _ids(pre_slots))
+    mixed, ab = gen_tokens(rng, sum(lens), Hk, Hv)
+    y, cu = _run_prefill(pool, 0, pre_slots, lens, mixed, ab, p, gpu)
+    xd, abd = gen_tokens(rng, 28, Hk, Hv)
+    yd = torch.zeros((28, Hv, DV), dtype=torch.int16, device=gpu)
+    pool.decode(0, _ids(dec_slots), dev(xd), dev(abd), dev(p["A_log"]), dev(p["dt_bias"]),
+                dev(p["conv_w"]), yd)
+    # oracle: sequential prefill per sequence from zero state
+    D = conv_dim(Hk, Hv)
+    st_ref = np.zeros((32, Hv, DV, DK), np.float32)
+    cs_ref = np.zeros((32, K - 1, D), np.uint16)
+    worst_y = 0.0
+    for i, L in enumerate(lens):
+        a, b = cu[i], cu[i + 1]
+        yr, cs_ref[i], st_ref[i] = O.prefill(np.zeros((K - 1, D), np.uint16),
+                                             np.zeros((Hv, DV, DK), np.float32), mixed[a:b],
+                                             ab[a:b], p["A_log"], p["dt_bias"], p["conv_w"], Hk, Hv)
+        worst_y = max(worst_y, float(np.max(np.abs(O.bf16_to_f32(y[a:b]) - O.bf16_to_f32(yr)))))
+    ydr, cs_ref[4:], st_ref[4:] = O.decode(dcs, dst, xd, abd, p["A_log"], p["dt_bias"],
+                                           p["conv_w"], Hk, Hv)
+    worst_y = max(worst_y, float(np.max(np.abs(O.bf16_to_f32(host(yd)) - O.bf16_to_f32(ydr)))))
+    gs, gc = _read(pool, 0, slots, gpu)
+    assert np.array_equal(gc, cs_ref)
+    worst_s = max(rel_l2(gs[i], st_ref[i]) for i in range(32))
+    say("config3 after prefill: worst |dy|", worst_y, "worst state relL2", worst_s)
+    assert worst_y <= Y_TOL and worst_s <= STATE_TOL
+    # hand-off: 3 decode steps over all 32 sequences
+    ydec = torch.zeros((32, Hv, DV), dtype=torch.int16, device=gpu)
+    for step in range(3):
+        x, abx = gen_tokens(rng, 32, Hk, Hv)
+        pool.decode(0, _ids(slots), dev(x), dev(abx), dev(p["A_log"]), dev(p["dt_bias"]),
+                    dev(p["conv_w"]), ydec)
+        yr, cs_ref, st_ref = O.decode(cs_ref, st_ref, x, abx, p["A_log"], p["dt_bias"],
+                                      p["conv_w"], Hk, Hv)
+        assert np.max(np.abs(O.bf16_to_f32(host(ydec)) - O.bf16_to_f32(yr))) <= Y_TOL
+    gs, gc = _read(pool, 0, slots, gpu)
+    assert np.array_equal(gc, cs_ref)
+    assert max(rel_l2(gs[i], st_ref[i]) for i in range(32)) <= STATE_TOL
+    assert pool.check() == 0
+
+
+@pytest.mark.parametrize("Hk,Hv", [(16, 32), (2, 8)])
+def test_prefill_edge_lengths_from_nonzero_state(gpu, Hk, Hv):
+    """Lengths 1, 2, 3 (conv state mixes old rows), 0 (empty sequence: slot
+    untouched), 63/64/65 around a chunk boundary; sequences continue from a
+    nonzero state (prefill of a prompt continuation)."""
+    import gdn_amd
+    lens = [1, 2, 0, 3, 64, 65, 63]
+    say("gdn_prefill_varlen", f"edge lens={lens} Hk={Hk} Hv={Hv}")
+    rng = np.random.default_rng(510 + Hv)
+    n = len(lens)
+    pool = gdn_amd.Pool(1, n + 2, Hk, Hv)
+    p = gen_layer_params(rng, Hk, Hv)
+    slots = rng.permutation(n + 2)[:n].astype(np.int32)
+    st0, cs0 = gen_states(rng, n, Hk, Hv, state_std=0.05)
+    pool.write(0, _ids(slots), dev(st0), dev(cs0))
+    mixed, ab = gen_tokens(rng, sum(lens), Hk, Hv)
+    y, cu = _run_prefill(pool, 0, slots, lens, mixed, ab, p, gpu)
+    gs, gc = _read(pool, 0, slots, gpu)
+    for i, L in enumerate(lens):
+        a, b = cu[i], cu[i + 1]
+        if L == 0:
+            assert np.array_equal(gs[i], st0[i]) and np.array_equal(gc[i], cs0[i])
+            continue
+        yr, csr, sr = O.prefill(cs0[i], st0[i], mixed[a:b], ab[a:b], p["A_log"], p["dt_bias"],
+                                p["conv_w"], Hk, Hv)
+        assert np.array_equal(gc[i], csr)
+        assert np.max(np.abs(O.bf16_to_f32(y[a:b]) - O.bf16_to_f32(yr))) <= Y_TOL
+        assert rel_l2(gs[i], sr) <= STATE_TOL
+    assert pool.check() == 0

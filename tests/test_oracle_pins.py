@@ -1,0 +1,348 @@
+"""Pins the CPU oracle (oracle/gdn_oracle.c) without the reference.
+
+The reference ships no tests or fixtures for any GDN numerics, so each oracle
+function is held to something independent of its own code: a closed form,
+an invariant of the recurrence, brute force on tiny inputs, or the float64
+restatement in another state layout (tests/gdn_testlib.py). Each check is
+chosen so that a plausible slip (swapped a/b halves, reversed conv taps, a
+transposed state, a dropped delta term, a wrong GQA map) fails it.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from gdn_testlib import (O, DK, DV, K, conv_dim, f64, gen_recurrent_inputs, gen_layer_params,
+                         gen_states, gen_tokens, np_chunked_one_head, np_conv_depthwise,
+                         np_recurrent_dkdv, rel_l2)
+
+
+# ------------------------------------------------------------------ bf16 --
+
+def test_bf16_rounding_is_rne():
+    x = np.array([1.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -9, -2.5, 0.0, -0.0, np.inf], np.float32)
+    got = O.bf16_to_f32(O.f32_to_bf16(x))
+    # 1 + 2^-8 is a tie between 1 and 1 + 2^-7: even mantissa wins (1.0)
+    exp = np.array([1.0, 1.0, 1.0 + 2 ** -7, -2.5, 0.0, -0.0, np.inf], np.float32)
+    assert np.array_equal(got, exp)
+    assert np.signbit(got[5])
+    assert np.isnan(O.bf16_to_f32(O.f32_to_bf16(np.array([np.nan], np.float32))))[0]
+
+
+# ----------------------------------------------------------------- gates --
+
+def test_beta_g_closed_form():
+    rng = np.random.default_rng(1)
+    Hv = 32
+    ab = O.f32_to_bf16(rng.standard_normal((64, 2 * Hv)).astype(np.float32) * 3)
+    A_log = rng.uniform(0, np.log(16), Hv).astype(np.float32)
+    dt = (rng.standard_normal(Hv) * 0.1).astype(np.float32)
+    beta, g = O.beta_g(ab, A_log, dt)
+    b = f64(ab[:, :Hv])
+    a = f64(ab[:, Hv:])
+    beta_ref = 1.0 / (1.0 + np.exp(-b))
+    sp = np.log1p(np.exp(a + dt.astype(np.float64)))
+    g_ref = np.exp(-np.exp(A_log.astype(np.float64)) * sp)
+    # beta: f32 sigmoid rounded to bf16 -> within one bf16 ulp of the exact value
+    assert np.all(np.abs(O.bf16_to_f32(beta) - beta_ref) <= 2 ** -8 * np.abs(beta_ref) + 1e-7)
+    assert np.allclose(g, g_ref, rtol=2e-5, atol=1e-30)
+    # the halves are not interchangeable: b drives beta, a drives g
+    beta_sw, g_sw = O.beta_g(np.concatenate([ab[:, Hv:], ab[:, :Hv]], 1), A_log, dt)
+    assert not np.array_equal(beta_sw, beta) and not np.allclose(g_sw, g)
+
+
+def test_beta_g_special_values():
+    Hv = 4
+    one = O.f32_to_bf16(np.array([0.0, 0.0, 0.0, 0.0, 0.0, 100.0, -40.0, 0.0], np.float32))
+    A_log = np.array([-np.inf, 0.0, 0.0, 0.0], np.float32)
+    dt = np.zeros(Hv, np.float32)
+    beta, g = O.beta_g(one[None, :], A_log, dt)
+    beta, g = O.bf16_to_f32(beta)[0], g[0]
+    assert np.all(beta == 0.5)                     # sigmoid(0)
+    # a = ab[:, Hv:] = [0, 100, -40, 0]
+    assert g[0] == 1.0                             # A_log = -inf: exp(-0*sp) = 1
+    assert g[1] == 0.0                             # naive softplus overflows: log(inf) -> g = 0
+    assert g[2] == 1.0                             # exp(-40)+1 == 1 in f32: softplus 0 -> g = 1
+    assert g[3] == pytest.approx(0.5, rel=1e-6)    # a = 0, A_log = 0: exp(-log 2) = 1/2
+
+
+# ------------------------------------------------------------------ conv --
+
+def test_conv_update_one_hot_taps_pick_window_rows():
+    rng = np.random.default_rng(2)
+    B, D = 3, 256
+    _, cs = gen_states(rng, B, 1, 1)  # shape [B,3,conv_dim(1,1)=384]
+    cs = cs[:, :, :D].copy()
+    x = O.f32_to_bf16(rng.standard_normal((B, D)).astype(np.float32))
+    for tap in range(K):
+        w = np.zeros((D, K), np.float32)
+        w[:, tap] = 1.0
+        new, out = O.conv_update(cs, x, O.f32_to_bf16(w))
+        window = np.concatenate([cs, x[:, None, :]], 1)   # [s0 s1 s2 x], oldest first
+        expect = O.bf16_to_f32(window[:, tap])
+        expect_silu = O.round_bf16(expect * O.round_bf16(1.0 / (1.0 + np.exp(-expect.astype(np.float64)))))
+        assert np.array_equal(new, window[:, 1:])        # bit-exact shift
+        got = O.bf16_to_f32(out)
+        assert np.allclose(got, expect_silu, rtol=2 ** -7, atol=1e-6)
+
+
+def test_conv_update_closed_form_random_weights():
+    rng = np.random.default_rng(3)
+    B, Hk, Hv = 2, 1, 2
+    D = conv_dim(Hk, Hv)
+    _, cs = gen_states(rng, B, Hk, Hv)
+    x, _ = gen_tokens(rng, B, Hk, Hv)
+    w = gen_layer_params(rng, Hk, Hv)["conv_w"]
+    _, out = O.conv_update(cs, x, w)
+    win = f64(np.concatenate([cs, x[:, None, :]], 1))
+    pre = np.einsum("bkd,dk->bd", win, f64(w))
+    ref = pre / (1 + np.exp(-pre))
+    assert np.max(np.abs(O.bf16_to_f32(out) - ref)) < 0.03 * max(1.0, np.abs(ref).max())
+
+
+def test_conv_prefill_matches_textbook_conv_and_repeated_updates():
+    rng = np.random.default_rng(4)
+    Hk, Hv = 1, 2
+    D = conv_dim(Hk, Hv)
+    _, cs = gen_states(rng, 1, Hk, Hv)
+    cs = cs[0]
+    S = 9
+    x, _ = gen_tokens(rng, S, Hk, Hv)
+    w = gen_layer_params(rng, Hk, Hv)["conv_w"]
+    new, out = O.conv_prefill(cs, x, w)
+    padded = np.concatenate([cs, x], 0)
+    assert np.array_equal(new, padded[-(K - 1):])
+    pre = np_conv_depthwise(f64(padded), f64(w))
+    ref = pre / (1 + np.exp(-pre))
+    assert np.max(np.abs(O.bf16_to_f32(out) - ref)) < 0.03 * max(1.0, np.abs(ref).max())
+    # With small-integer inputs and weights every product and sum is exact, so
+    # the prefill conv must equal S single-token updates bit for bit.
+    xi = O.f32_to_bf16(rng.integers(-3, 4, (S, D)).astype(np.float32))
+    csi = O.f32_to_bf16(rng.integers(-3, 4, (K - 1, D)).astype(np.float32))
+    wi = O.f32_to_bf16(rng.integers(-2, 3, (D, K)).astype(np.float32))
+    new_p, out_p = O.conv_prefill(csi, xi, wi)
+    st = csi[None]
+    for t in range(S):
+        st, o = O.conv_update(st, xi[t:t + 1], wi)
+        assert np.array_equal(o[0], out_p[t])
+    assert np.array_equal(st[0], new_p)
+
+
+def test_conv_prefill_short_sequence_state_mixes_old_rows():
+    rng = np.random.default_rng(5)
+    D = 384
+    cs = O.f32_to_bf16(rng.standard_normal((K - 1, D)).astype(np.float32))
+    x = O.f32_to_bf16(rng.standard_normal((1, D)).astype(np.float32))
+    w = O.f32_to_bf16(rng.standard_normal((D, K)).astype(np.float32))
+    new, _ = O.conv_prefill(cs, x, w)
+    assert np.array_equal(new, np.concatenate([cs[1:], x], 0))
+
+
+# ------------------------------------------------------------------ norm --
+
+def test_norm_weights_are_the_baked_bf16_values():
+    assert O.q_norm_weight(128) == 0.0078125
+    assert O.k_norm_weight(128) == 0.08837890625
+
+
+def test_rms_norm_closed_form():
+    rng = np.random.default_rng(6)
+    x = O.f32_to_bf16(rng.standard_normal((50, DK)).astype(np.float32) * 2)
+    xk = O.rms_norm(x, O.k_norm_weight(DK), 1e-6)
+    xq = O.rms_norm(x, O.q_norm_weight(DK), 1e-6)
+    xf = f64(x)
+    base = xf / np.sqrt((xf ** 2).sum(-1, keepdims=True) + DK * 1e-6)
+    assert np.allclose(f64(xk), base * 0.08837890625 * np.sqrt(DK), rtol=2 ** -7, atol=1e-6)
+    assert np.allclose(f64(xq), base / np.sqrt(DK), rtol=2 ** -7, atol=1e-8)
+    # |k| is 0.99989, not 1 (the bf16 weight), |q| is 1/sqrt(128)
+    assert np.allclose(np.linalg.norm(f64(xk), axis=-1), 0.08837890625 * np.sqrt(DK), rtol=5e-3)
+    # tiny inputs are dominated by eps (effective 128 * 1e-6 in sum-of-squares
+    # space): |k| = sqrt(ss / (ss + 1.28e-4)) * 0.99989, about 0.0995 here
+    tiny = O.f32_to_bf16(np.full((1, DK), 1e-4, np.float32))
+    ss = float((f64(tiny) ** 2).sum())
+    expect = math.sqrt(ss / (ss + DK * 1e-6)) * 0.08837890625 * math.sqrt(DK)
+    got = np.linalg.norm(f64(O.rms_norm(tiny, O.k_norm_weight(DK), 1e-6)))
+    assert got == pytest.approx(expect, rel=1e-2) and got < 0.11
+
+
+# ------------------------------------------------------------ recurrence --
+
+def _brute_recurrence(q, k, v, g, beta, S):
+    """Scalar loops straight from the per-row description of the kernel."""
+    B, T, Hk, Dk = q.shape
+    Hv, Dv = v.shape[2], v.shape[3]
+    S = S.astype(np.float64).copy()
+    y = np.zeros((B, T, Hv, Dv))
+    for b in range(B):
+        for h in range(Hv):
+            hk = h // (Hv // Hk)
+            for dv in range(Dv):
+                s = S[b, h, dv]
+                for t in range(T):
+                    s = s * g[b, t, h]
+                    kv = sum(s[i] * k[b, t, hk, i] for i in range(Dk))
+                    d = (v[b, t, h, dv] - kv) * beta[b, t, h]
+                    s = s + k[b, t, hk] * d
+                    y[b, t, h, dv] = sum(s[i] * q[b, t, hk, i] for i in range(Dk))
+                S[b, h, dv] = s
+    return y, S
+
+
+def test_recurrence_matches_brute_force_tiny():
+    rng = np.random.default_rng(7)
+    B, T, Hk, Hv, Dk, Dv = 1, 4, 2, 4, 32, 4
+    inp = gen_recurrent_inputs(rng, B, T, Hk, Hv, Dk, Dv, state_std=0.3)
+    y, st = O.recurrent(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], inp["state"])
+    yr, sr = _brute_recurrence(f64(inp["q"]), f64(inp["k"]), f64(inp["v"]),
+                               inp["g"].astype(np.float64), f64(inp["beta"]), inp["state"])
+    assert rel_l2(st, sr) < 1e-6
+    assert np.max(np.abs(O.bf16_to_f32(y) - yr)) <= 2 ** -8 * np.abs(yr).max() + 1e-7
+
+
+def test_recurrence_matches_dkdv_restatement_and_gqa_map():
+    rng = np.random.default_rng(8)
+    B, T, Hk, Hv = 2, 6, 2, 4
+    inp = gen_recurrent_inputs(rng, B, T, Hk, Hv, state_std=0.05)
+    y, st = O.recurrent(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], inp["state"])
+    o, s64 = np_recurrent_dkdv(f64(inp["q"]), f64(inp["k"]), f64(inp["v"]),
+                               inp["g"].astype(np.float64), f64(inp["beta"]), inp["state"])
+    assert rel_l2(st, s64) < 1e-6
+    assert np.max(np.abs(O.bf16_to_f32(y) - o)) <= 2 ** -8 * np.abs(o).max()
+    # a transposed state or a k<->q swap is caught by the same comparison
+    o_t, _ = np_recurrent_dkdv(f64(inp["q"]), f64(inp["k"]), f64(inp["v"]),
+                               inp["g"].astype(np.float64), f64(inp["beta"]),
+                               np.swapaxes(inp["state"], -1, -2))
+    assert rel_l2(O.bf16_to_f32(y), o_t) > 1e-2
+    # GQA: value heads 2j and 2j+1 read key head j (hv // 2), not hv % Hk
+    q2 = inp["q"].copy()
+    q2[:, :, 1] = inp["q"][:, :, 0]
+    k2 = inp["k"].copy()
+    k2[:, :, 1] = inp["k"][:, :, 0]
+    y2, _ = O.recurrent(q2, k2, inp["v"], inp["g"], inp["beta"], inp["state"])
+    assert np.array_equal(y2[:, :, :2], y[:, :, :2])     # heads 0,1 use key head 0
+    assert not np.array_equal(y2[:, :, 2:], y[:, :, 2:])  # heads 2,3 use key head 1
+
+
+def test_recurrence_invariants():
+    rng = np.random.default_rng(9)
+    B, T, Hk, Hv = 1, 3, 1, 2
+    inp = gen_recurrent_inputs(rng, B, T, Hk, Hv, state_std=0.1)
+    q, k, v, st0 = inp["q"], inp["k"], inp["v"], inp["state"]
+    zero_beta = np.zeros_like(inp["beta"])
+    one_g = np.ones_like(inp["g"])
+    # (i) beta = 0: pure decay, y_t = (prod g) S0 q_t
+    y, st = O.recurrent(q, k, v, inp["g"], zero_beta, st0)
+    gp = np.cumprod(inp["g"][0].astype(np.float64), axis=0)      # [T, Hv]
+    for t in range(T):
+        for h in range(Hv):
+            ref = gp[t, h] * st0[0, h].astype(np.float64) @ f64(q[0, t, 0])
+            assert np.allclose(f64(y[0, t, h]), ref, rtol=2 ** -7, atol=1e-7)
+    assert np.allclose(st, st0 * gp[-1][None, :, None, None], rtol=1e-5)
+    # (ii) g = 1, beta = 0: state bit-identical
+    _, st = O.recurrent(q, k, v, one_g, zero_beta, st0)
+    assert np.array_equal(st, st0)
+    # (iii) delta-rule write: g = 1, beta = 1, k = e_j  =>  S_new[:, :, j] = v
+    kj = np.zeros_like(k)
+    kj[..., 5] = O.f32_to_bf16(np.float32(1.0))
+    one_beta = O.f32_to_bf16(np.ones(inp["beta"].shape, np.float32))
+    _, st = O.recurrent(q[:, :1], kj[:, :1], v[:, :1], one_g[:, :1], one_beta[:, :1], st0)
+    assert np.allclose(st[0, :, :, 5], f64(v[0, 0]), rtol=0, atol=1e-6)
+    others = [i for i in range(DK) if i != 5]
+    assert np.array_equal(st[0][:, :, others], st0[0][:, :, others])
+
+
+def test_recurrence_batch_permutation_equivariance():
+    rng = np.random.default_rng(10)
+    B, T, Hk, Hv = 4, 2, 2, 4
+    inp = gen_recurrent_inputs(rng, B, T, Hk, Hv)
+    y, st = O.recurrent(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], inp["state"])
+    p = rng.permutation(B)
+    yp, stp = O.recurrent(inp["q"][p], inp["k"][p], inp["v"][p], inp["g"][p], inp["beta"][p],
+                          inp["state"][p])
+    assert np.array_equal(yp, y[p]) and np.array_equal(stp, st[p])
+
+
+def test_recurrence_f32_tracks_f64_over_256_steps():
+    rng = np.random.default_rng(11)
+    B, T, Hk, Hv = 1, 256, 1, 2
+    inp = gen_recurrent_inputs(rng, B, T, Hk, Hv)
+    y, st = O.recurrent(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], inp["state"])
+    y64b, y64, st64 = O.recurrent_f64(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"],
+                                      inp["state"])
+    assert rel_l2(st, st64) < 1e-5
+    assert np.max(np.abs(O.bf16_to_f32(y) - y64)) < 2e-2
+
+
+# --------------------------------------------------------- chunked form --
+
+@pytest.mark.parametrize("T", [1, 40, 64, 130])
+def test_chunked_wy_form_equals_sequential_recurrence(T):
+    """The chunked algorithm the prefill kernel implements reproduces the
+    token-by-token recurrence, including a partial last chunk."""
+    rng = np.random.default_rng(12 + T)
+    inp = gen_recurrent_inputs(rng, 1, T, 1, 1, state_std=0.05)
+    q, k, v = f64(inp["q"][0, :, 0]), f64(inp["k"][0, :, 0]), f64(inp["v"][0, :, 0])
+    g = inp["g"][0, :, 0].astype(np.float64)
+    beta = f64(inp["beta"][0, :, 0])
+    S0 = inp["state"][0, 0].astype(np.float64)          # [Dv, Dk]
+    o, S = np_chunked_one_head(q, k, v, np.log(g), beta, S0.T)
+    y, st = O.recurrent(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], inp["state"])
+    _, y64, st64 = O.recurrent_f64(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"],
+                                   inp["state"])
+    assert rel_l2(S.T, st64[0, 0]) < 1e-7        # st64 is stored rounded to f32
+    assert np.max(np.abs(o - y64[0, :, 0])) < 1e-9
+    assert np.max(np.abs(O.bf16_to_f32(y[0, :, 0]) - o)) < 2e-2
+
+
+# ------------------------------------------------------- composed layer --
+
+def test_decode_equals_composition_of_steps():
+    rng = np.random.default_rng(13)
+    B, Hk, Hv = 2, 2, 4
+    D = conv_dim(Hk, Hv)
+    p = gen_layer_params(rng, Hk, Hv)
+    st, cs = gen_states(rng, B, Hk, Hv)
+    x, ab = gen_tokens(rng, B, Hk, Hv)
+    y, cs2, st2 = O.decode(cs, st, x, ab, p["A_log"], p["dt_bias"], p["conv_w"], Hk, Hv)
+    cs_ref, xc = O.conv_update(cs, x, p["conv_w"])
+    q, k, v = O.split_qkv(xc, Hk, Hv, DK, DV)
+    q = O.rms_norm(q, O.q_norm_weight(DK))
+    k = O.rms_norm(k, O.k_norm_weight(DK))
+    beta, g = O.beta_g(ab, p["A_log"], p["dt_bias"])
+    yr, str_ = O.recurrent(q[:, None], k[:, None], v[:, None], g[:, None], beta[:, None], st)
+    assert np.array_equal(cs2, cs_ref)
+    assert np.array_equal(y, yr[:, 0]) and np.array_equal(st2, str_)
+    assert D == 1024
+
+
+def test_prefill_equals_token_by_token_decode_within_rounding():
+    """Prefill (conv1d, f32 accumulation) vs S decode steps (bf16 products):
+    same mathematics, different MLX rounding, so equal to tolerance."""
+    rng = np.random.default_rng(14)
+    Hk, Hv, S = 1, 2, 12
+    p = gen_layer_params(rng, Hk, Hv)
+    st, cs = gen_states(rng, 1, Hk, Hv)
+    x, ab = gen_tokens(rng, S, Hk, Hv)
+    y, cs_p, st_p = O.prefill(cs[0], st[0], x, ab, p["A_log"], p["dt_bias"], p["conv_w"], Hk, Hv)
+    cs_d, st_d = cs, st
+    ys = []
+    for t in range(S):
+        yt, cs_d, st_d = O.decode(cs_d, st_d, x[t:t + 1], ab[t:t + 1], p["A_log"], p["dt_bias"],
+                                  p["conv_w"], Hk, Hv)
+        ys.append(yt[0])
+    assert np.array_equal(cs_p, cs_d[0])
+    assert np.max(np.abs(O.bf16_to_f32(y) - O.bf16_to_f32(np.stack(ys)))) < 2e-2
+    assert rel_l2(st_p, st_d[0]) < 2e-2
+
+
+def test_stack_unstack_are_gather_scatter():
+    rng = np.random.default_rng(15)
+    pool = rng.standard_normal((10, 3, 4)).astype(np.float32)
+    ids = np.array([7, 2, 9], np.int32)
+    batched = O.stack(pool, ids)
+    assert np.array_equal(batched, pool[[7, 2, 9]])
+    new = pool.copy()
+    O.unstack(new, ids, batched * 2)
+    assert np.array_equal(new[[7, 2, 9]], pool[[7, 2, 9]] * 2)
+    untouched = [i for i in range(10) if i not in (7, 2, 9)]
+    assert np.array_equal(new[untouched], pool[untouched])
