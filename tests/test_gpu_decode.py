@@ -126,10 +126,12 @@ def test_recurrent_matches_oracle(gpu, B, T):
     got_s = torch.empty((B, 32, DV, DK), dtype=torch.float32, device=gpu)
     pool.read(0, _ids(slots), got_s, None)
     yr, sr = O.recurrent(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], inp["state"])
-    dy = np.abs(O.bf16_to_f32(host(y)) - O.bf16_to_f32(yr))
-    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(O.bf16_to_f32(yr)), 1e-30))) - 7)
+    yo = O.bf16_to_f32(yr)
+    dy = np.abs(O.bf16_to_f32(host(y)) - yo)
+    say("gdn_recurrent worst |dy|", float(dy.max()), "of max |y|", float(np.abs(yo).max()))
     assert dy.max() <= Y_TOL
-    assert np.all(dy <= ulp + 1e-12)              # at most one bf16 ulp apart
+    # one bf16 ulp of the value, plus an f32 summation-order floor for y near 0
+    assert np.all(dy <= 2.0 ** -7 * np.abs(yo) + 1e-5 * np.abs(yo).max())
     assert rel_l2(host(got_s), sr) < 1e-5
     assert pool.check() == 0
 
@@ -157,8 +159,10 @@ def test_decode_fused_matches_oracle_config0(gpu):
     pool.read(0, _ids([2]), gs, gc)
     yr, cr, sr = O.decode(conv, state, x, ab, p["A_log"], p["dt_bias"], p["conv_w"], Hk, Hv)
     assert np.array_equal(host(gc), cr)           # rolling conv state: bit-exact shift
-    assert np.max(np.abs(O.bf16_to_f32(host(y)) - O.bf16_to_f32(yr))) <= Y_TOL
-    assert rel_l2(host(gs), sr) < 1e-4
+    dy = float(np.max(np.abs(O.bf16_to_f32(host(y)) - O.bf16_to_f32(yr))))
+    ds = rel_l2(host(gs), sr)
+    say("gdn_decode config0 |dy|", dy, "state relL2", ds)
+    assert dy <= Y_TOL and ds <= STATE_TOL
     assert pool.check() == 0
 
 
@@ -183,8 +187,10 @@ def test_decode_fused_other_head_ratios(gpu, Hk, Hv):
     pool.read(0, _ids(slots), gs, gc)
     yr, cr, sr = O.decode(cs, st, x, ab, p["A_log"], p["dt_bias"], p["conv_w"], Hk, Hv)
     assert np.array_equal(host(gc), cr)
-    assert np.max(np.abs(O.bf16_to_f32(host(y)) - O.bf16_to_f32(yr))) <= Y_TOL
-    assert rel_l2(host(gs), sr) < 1e-4
+    dy = float(np.max(np.abs(O.bf16_to_f32(host(y)) - O.bf16_to_f32(yr))))
+    ds = rel_l2(host(gs), sr)
+    say("gdn_decode worst |dy|", dy, "state relL2", ds)
+    assert dy <= Y_TOL and ds <= STATE_TOL
 
 
 def test_decode_chained_config1(gpu):
