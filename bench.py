@@ -52,13 +52,14 @@ def parse_args(argv=None):
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--churn-every", type=int, default=16)
     ap.add_argument("--churn", type=int, default=8)
-    ap.add_argument("--timing-steps", type=int, default=16,
-                    help="steps of the per-launch event timing pass")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target duration of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (PMC byte-count calibration)")
+    ap.add_argument("--rmw-ceiling", action="store_true",
+                    help="only time a plain in-place multiply over 30 x 128 MiB buffers "
+                         "(the decode's per-launch state bytes, read + write)")
     ap.add_argument("--seed", type=int, default=0)
     return ap.parse_args(argv)
 
@@ -73,6 +74,28 @@ def copy_calibration(mib: int):
     torch.cuda.synchronize()
     print(json.dumps({"copy_calibration_bytes_read": n * 4, "copy_calibration_bytes_written": n * 4,
                       "launches": 5}), flush=True)
+
+
+def rmw_ceiling(layers: int = 30, mib: int = 128, reps: int = 8):
+    """Reference rate of a plain streaming read-modify-write of the same bytes
+    per launch as the decode kernel's state traffic (torch's in-place multiply,
+    cycling `layers` buffers so nothing stays in the 256 MB memory-side cache)."""
+    import torch
+    bufs = [torch.zeros(mib * (1 << 20) // 4, device="cuda:0") for _ in range(layers)]
+    for b in bufs:
+        b.mul_(0.999)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        for b in bufs:
+            b.mul_(0.999)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * layers)
+    nbytes = 2 * mib * (1 << 20)
+    print(json.dumps({"rmw_ceiling_us_per_launch": round(us, 2), "bytes_per_launch": nbytes,
+                      "GBps": round(nbytes / us * 1e-3, 1)}), flush=True)
 
 
 class Workload:
@@ -132,14 +155,16 @@ class Workload:
         self.d_ids.copy_(self.torch.from_numpy(np.asarray(self.active, np.int32)))
 
     def step(self, events=None):
+        """One decode step: L back-to-back gdn_decode launches (bracketed by the
+        event pair `events` on the launch stream when given), then churn."""
         k = self.step_no % self.nsets
+        if events is not None:
+            events[0].record()
         for l in range(self.L):
-            if events is not None:
-                events[l][0].record()
             self.pool.decode(l, self.d_ids, self.mixed[k, l], self.ab[k, l], self.A_log[l],
                              self.dt_bias[l], self.conv_w[l], self.y[l])
-            if events is not None:
-                events[l][1].record()
+        if events is not None:
+            events[1].record()
         self.step_no += 1
         if self.args.churn_every > 0 and self.step_no % self.args.churn_every == 0:
             self.churn()
@@ -182,26 +207,25 @@ def main(argv=None):
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
         return 0
+    if args.rmw_ceiling:
+        rmw_ceiling()
+        return 0
     w = Workload(args)
     for _ in range(args.warmup):
         w.step()
+    # HIP events on the stream the kernels are launched on (torch's current
+    # stream, which the binding passes to libgdn) bracket each step's L
+    # back-to-back gdn_decode launches; slot churn runs outside the brackets.
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        w.step()
+    for i in range(args.steps):
+        w.step(ev[i])
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     tok_s = args.batch * args.steps / elapsed
-
-    # per-launch duration of the dominant kernel, HIP events on the launch stream
-    ev = [[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
-          for _ in range(args.layers)]
-    durs = []
-    for _ in range(args.timing_steps):
-        w.step(ev)
-        torch.cuda.synchronize()
-        durs += [a.elapsed_time(b) for a, b in ev]
-    avg_ms = sum(durs) / len(durs)
+    avg_ms = sum(a.elapsed_time(b) for a, b in ev) / (args.steps * args.layers)
     launch_bytes = args.batch * STATE_BYTES
     achieved = launch_bytes / (avg_ms * 1e-3) / 1e9
     traffic = None
@@ -243,6 +267,7 @@ def main(argv=None):
             "traffic": traffic,
             "kernel": "gdn_decode (decode_fused_kernel<2>)",
             "kernel_avg_us": round(avg_ms * 1e3, 2),
+            "kernel_timing": "HIP events around each step's back-to-back launches / launches",
             "algorithmic_bytes_per_launch": launch_bytes,
         },
         "state_traffic_gbs_whole_step": round(args.batch * args.layers * STATE_BYTES /

@@ -76,6 +76,25 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Work-group barrier that orders LDS only. Global loads issued before it stay
+// in flight (a plain __syncthreads() would wait for every outstanding vector
+// memory operation). Use it only where threads communicate through LDS.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// A pointer that is the same in every lane of the wave, moved to SGPRs so that
+// loads can use scalar-base + 32-bit lane-offset addressing.
+template <typename T>
+__device__ __forceinline__ T* wave_uniform(T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
+}
+
 __device__ __forceinline__ void flag_status(uint32_t* status, uint32_t bit) {
   if (status) atomicOr(status, bit);
 }

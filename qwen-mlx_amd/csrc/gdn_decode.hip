@@ -52,46 +52,42 @@ __device__ __forceinline__ float dot4(const v4f& a, const v4f& b) {
   return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
 }
 
-// One token on the register tile. kk/qq: this thread's 16 k / q values;
-// vrow[i]: v at row grp+32i; kq = k.q over all of Dk. yrow[i] gets the output
-// of row grp+32i (identical in the 8 lanes of a row group).
-__device__ __forceinline__ void tile_step(TileRegs& t, const v4f kk[4], const v4f qq[4],
+// One token on the register tile. kl/ql: k and q of the token in LDS (Dk
+// floats each); vrow[i]: v at row grp+32i; kq = k.q over all of Dk. yrow[i]
+// gets the output of row grp+32i (identical in the 8 lanes of a row group).
+// k/q are read from LDS per column block (j outer) so that only 8 of them are
+// live at a time; the compiler barrier between the passes makes the second
+// pass re-read k instead of keeping 16 registers alive across the reduction.
+__device__ __forceinline__ void tile_step(TileRegs& t, const float* kl, const float* ql, int sub,
                                           const float vrow[4], float g, float beta, float kq,
                                           float yrow[4]) {
-  float kd[4], qd[4];
+  float kd[4] = {0.f, 0.f, 0.f, 0.f}, qd[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float a = 0.0f, c = 0.0f;
+  for (int j = 0; j < 4; ++j) {
+    const v4f kj = *reinterpret_cast<const v4f*>(kl + 4 * (sub + 8 * j));
+    const v4f qj = *reinterpret_cast<const v4f*>(ql + 4 * (sub + 8 * j));
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      v4f s = t.s[i][j];
-      s.x *= g;
-      s.y *= g;
-      s.z *= g;
-      s.w *= g;
-      a += dot4(s, kk[j]);
-      c += dot4(s, qq[j]);
-      t.s[i][j] = s;
+    for (int i = 0; i < 4; ++i) {
+      const v4f sv = t.s[i][j] * g;
+      kd[i] += dot4(sv, kj);
+      qd[i] += dot4(sv, qj);
+      t.s[i][j] = sv;
     }
-    kd[i] = a;
-    qd[i] = c;
   }
+  float delta[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     kd[i] = sum8(kd[i]);
     qd[i] = sum8(qd[i]);
+    delta[i] = (vrow[i] - kd[i]) * beta;
+    yrow[i] = qd[i] + delta[i] * kq;
   }
+  asm volatile("" ::: "memory");
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float delta = (vrow[i] - kd[i]) * beta;
-    yrow[i] = qd[i] + delta * kq;
+  for (int j = 0; j < 4; ++j) {
+    const v4f kj = *reinterpret_cast<const v4f*>(kl + 4 * (sub + 8 * j));
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      t.s[i][j].x += kk[j].x * delta;
-      t.s[i][j].y += kk[j].y * delta;
-      t.s[i][j].z += kk[j].z * delta;
-      t.s[i][j].w += kk[j].w * delta;
-    }
+    for (int i = 0; i < 4; ++i) t.s[i][j] += kj * delta[i];
   }
 }
 
@@ -103,14 +99,23 @@ constexpr float kNormEps = 1e-6f;
 // -------------------------------------------------------------------------
 // Fused S=1 decode: conv update + silu + split + q/k rms-norm + gates +
 // recurrence. grid (Hk, B), block 256*R.
+//
+// Load order: the small conv/gate inputs first, then the 64 KiB state tile.
+// Waiting for the conv inputs leaves the state loads in flight through the
+// conv and norm phases, whose barriers order LDS only (lds_barrier). At most
+// 128 VGPRs (4 waves per SIMD) lets two 512-thread groups share a CU, so one
+// group's state stores overlap the other's loads.
 template <int R>
-__global__ __launch_bounds__(256 * R) void decode_fused_kernel(
-    float* __restrict__ state, uint16_t* __restrict__ conv, const int32_t* __restrict__ slot_ids,
-    int num_slots, int Hk, const uint16_t* __restrict__ mixed, const uint16_t* __restrict__ ab,
-    const float* __restrict__ A_log, const float* __restrict__ dt_bias,
-    const uint16_t* __restrict__ conv_w, uint16_t* __restrict__ y, uint32_t* __restrict__ status) {
+__global__ __launch_bounds__(256 * R) __attribute__((amdgpu_waves_per_eu(4))) void
+decode_fused_kernel(float* __restrict__ state, uint16_t* __restrict__ conv,
+                    const int32_t* __restrict__ slot_ids, int num_slots, int Hk,
+                    const uint16_t* __restrict__ mixed, const uint16_t* __restrict__ ab,
+                    const float* __restrict__ A_log, const float* __restrict__ dt_bias,
+                    const uint16_t* __restrict__ conv_w, uint16_t* __restrict__ y,
+                    uint32_t* __restrict__ status) {
   constexpr int NT = 256 * R;
   constexpr int NCH = (2 + R) * kDk;  // q, k of hk + v of R value heads
+  constexpr int CPT = (NCH + NT - 1) / NT;
   const int hk = blockIdx.x, b = blockIdx.y;
   const int Hv = Hk * R;
   const int D = 2 * Hk * kDk + Hv * kDv;
@@ -126,7 +131,39 @@ __global__ __launch_bounds__(256 * R) void decode_fused_kernel(
   __shared__ __align__(16) float kn[kDk];
   __shared__ float red[8];
   __shared__ float gate_g[R], gate_beta[R];
+  __shared__ uint16_t win_next[kConvK - 1][NCH];  // shifted conv window, stored at the end
 
+  // global conv channel of the group's local channel c (q | k | v blocks)
+  auto chan = [&](int c) {
+    return c < kDk ? hk * kDk + c
+                   : (c < 2 * kDk ? Hk * kDk + hk * kDk + (c - kDk)
+                                  : 2 * Hk * kDk + hk * R * kDv + (c - 2 * kDk));
+  };
+
+  // 1. conv window, weights and gate inputs of the channels this thread owns
+  uint16_t* cs = conv + (size_t)slot * (kConvK - 1) * D;
+  uint16_t cwin[CPT][kConvK];
+  uint2 cwt[CPT];
+#pragma unroll
+  for (int u = 0; u < CPT; ++u) {
+    const int c = tid + u * NT;
+    const int gc = chan(c < NCH ? c : 0);
+    cwt[u] = *reinterpret_cast<const uint2*>(conv_w + (size_t)gc * kConvK);
+    cwin[u][0] = cs[gc];
+    cwin[u][1] = cs[D + gc];
+    cwin[u][2] = cs[2 * D + gc];
+    cwin[u][3] = mixed[(size_t)b * D + gc];
+  }
+  float braw = 0.f, araw = 0.f, alog = 0.f, dtb = 0.f;
+  if (tid < R) {
+    const int h = hk * R + tid;
+    braw = bf2f(ab[(size_t)b * 2 * Hv + h]);
+    araw = bf2f(ab[(size_t)b * 2 * Hv + Hv + h]);
+    alog = A_log[h];
+    dtb = dt_bias[h];
+  }
+
+  // 2. the state tile of value head hv (stays in flight until tile_step)
   const int r = tid >> 8;
   const int lt = tid & 255, grp = lt >> 3, sub = lt & 7;
   const int hv = hk * R + r;
@@ -134,44 +171,39 @@ __global__ __launch_bounds__(256 * R) void decode_fused_kernel(
   TileRegs t;
   tile_load(t, tile, grp, sub);
 
-  // Conv window [s0 s1 s2 x] . w (qwen3_5.rs:602-610): bf16 products, f32 sum,
-  // silu; shift the window in place (this group owns these channels).
-  uint16_t* cs = conv + (size_t)slot * (kConvK - 1) * D;
-  for (int c = tid; c < NCH; c += NT) {
-    const int gc = c < kDk ? hk * kDk + c
-                           : (c < 2 * kDk ? Hk * kDk + hk * kDk + (c - kDk)
-                                          : 2 * Hk * kDk + hk * R * kDv + (c - 2 * kDk));
-    const uint2 wv = *reinterpret_cast<const uint2*>(conv_w + (size_t)gc * kConvK);
-    const uint16_t p0 = cs[gc], p1 = cs[D + gc], p2 = cs[2 * D + gc];
-    const uint16_t x = mixed[(size_t)b * D + gc];
-    float acc = rbf(bf2f(p0) * bf2f((uint16_t)(wv.x & 0xffffu)));
-    acc += rbf(bf2f(p1) * bf2f((uint16_t)(wv.x >> 16)));
-    acc += rbf(bf2f(p2) * bf2f((uint16_t)(wv.y & 0xffffu)));
-    acc += rbf(bf2f(x) * bf2f((uint16_t)(wv.y >> 16)));
-    xs[c] = silu_bf16(rbf(acc));
-    cs[gc] = p1;
-    cs[D + gc] = p2;
-    cs[2 * D + gc] = x;
+  // 3. conv (qwen3_5.rs:602-610): bf16 products, f32 sum, silu. The shifted
+  // window goes to LDS and is stored at the end of the kernel: a store issued
+  // here would sit behind the state loads in the in-order vmcnt counter and
+  // force waits on them.
+#pragma unroll
+  for (int u = 0; u < CPT; ++u) {
+    const int c = tid + u * NT;
+    if (c < NCH) {
+      float acc = rbf(bf2f(cwin[u][0]) * bf2f((uint16_t)(cwt[u].x & 0xffffu)));
+      acc += rbf(bf2f(cwin[u][1]) * bf2f((uint16_t)(cwt[u].x >> 16)));
+      acc += rbf(bf2f(cwin[u][2]) * bf2f((uint16_t)(cwt[u].y & 0xffffu)));
+      acc += rbf(bf2f(cwin[u][3]) * bf2f((uint16_t)(cwt[u].y >> 16)));
+      xs[c] = silu_bf16(rbf(acc));
+#pragma unroll
+      for (int k = 0; k < kConvK - 1; ++k) win_next[k][c] = cwin[u][k + 1];
+    }
   }
-  // Gates (compiled_ops.rs:30-43) on ab = [b | a].
+  // gates (compiled_ops.rs:30-43) on ab = [b | a]
   if (tid < R) {
-    const int h = hk * R + tid;
-    const float braw = bf2f(ab[(size_t)b * 2 * Hv + h]);
-    const float araw = bf2f(ab[(size_t)b * 2 * Hv + Hv + h]);
     gate_beta[tid] = rbf(sigmoid_f32(braw));
-    const float sp = logf(expf(araw + dt_bias[h]) + 1.0f);
-    gate_g[tid] = expf(-(expf(A_log[h]) * sp));
+    const float sp = logf(expf(araw + dtb) + 1.0f);
+    gate_g[tid] = expf(-(expf(alog) * sp));
   }
-  __syncthreads();
+  lds_barrier();
 
-  // q/k rms-norm (qwen3_5.rs:638-639): waves 0-1 hold q, waves 2-3 hold k.
+  // 4. q/k rms-norm (qwen3_5.rs:638-639): waves 0-1 hold q, waves 2-3 hold k.
   const int wave = tid >> 6, lane = tid & 63;
   if (tid < 2 * kDk) {
     const float v = xs[tid];
     const float ss = wave_sum(v * v);
     if (lane == 0) red[wave] = ss;
   }
-  __syncthreads();
+  lds_barrier();
   if (tid < kDk) {
     const float rq = 1.0f / sqrtf((red[0] + red[1]) / (float)kDk + kNormEps);
     const float rk = 1.0f / sqrtf((red[2] + red[3]) / (float)kDk + kNormEps);
@@ -182,24 +214,30 @@ __global__ __launch_bounds__(256 * R) void decode_fused_kernel(
     const float p = wave_sum(qv * kv);
     if (lane == 0) red[4 + wave] = p;
   }
-  __syncthreads();
+  lds_barrier();
   const float kq = red[4] + red[5];
 
-  v4f kk[4], qq[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    kk[j] = *reinterpret_cast<const v4f*>(&kn[4 * (sub + 8 * j)]);
-    qq[j] = *reinterpret_cast<const v4f*>(&qn[4 * (sub + 8 * j)]);
-  }
+  // 5. recurrence on the tile
   float vrow[4], yrow[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) vrow[i] = xs[2 * kDk + r * kDv + grp + 32 * i];
-  tile_step(t, kk, qq, vrow, gate_g[r], gate_beta[r], kq, yrow);
+  tile_step(t, kn, qn, sub, vrow, gate_g[r], gate_beta[r], kq, yrow);
   tile_store(t, tile, grp, sub);
   uint16_t* yo = y + ((size_t)b * Hv + hv) * kDv;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     if (sub == i) yo[grp + 32 * i] = f2bf(yrow[i]);
+  // 6. rolling conv state: window [s0 s1 s2 x] -> [s1 s2 x] in place (this
+  // group is the only one touching these channels of the slot)
+#pragma unroll
+  for (int u = 0; u < CPT; ++u) {
+    const int c = tid + u * NT;
+    if (c < NCH) {
+      const int gc = chan(c);
+#pragma unroll
+      for (int k = 0; k < kConvK - 1; ++k) cs[(size_t)k * D + gc] = win_next[k][c];
+    }
+  }
 }
 
 // -------------------------------------------------------------------------
@@ -252,16 +290,10 @@ __global__ __launch_bounds__(256 * R) void recurrent_kernel(
     }
     __syncthreads();
     const float kq = red[0] + red[1];
-    v4f kk[4], qq[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      kk[j] = *reinterpret_cast<const v4f*>(&ks[4 * (sub + 8 * j)]);
-      qq[j] = *reinterpret_cast<const v4f*>(&qs[4 * (sub + 8 * j)]);
-    }
     float vrow[4], yrow[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) vrow[i] = vs[r * kDv + grp + 32 * i];
-    tile_step(t, kk, qq, vrow, gg[r], bb[r], kq, yrow);
+    tile_step(t, ks, qs, sub, vrow, gg[r], bb[r], kq, yrow);
     uint16_t* yo = y + (tok * Hv + hv) * kDv;
 #pragma unroll
     for (int i = 0; i < 4; ++i)

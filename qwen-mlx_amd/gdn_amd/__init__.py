@@ -80,6 +80,13 @@ def load(path: str = LIB_PATH):
         return _lib
     if not os.path.exists(path):
         raise FileNotFoundError(f"{path} is not built; run __graft_entry__.build()")
+    # torch ships its own HIP runtime; loading it first makes libgdn bind to the
+    # same runtime instance, so device pointers from torch's allocator and its
+    # streams are valid inside the library.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(path)
     for name, (args, res) in SIGNATURES.items():
         fn = getattr(lib, name)
