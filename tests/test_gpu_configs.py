@@ -1,0 +1,196 @@
+"""GPU parity at the full sizes of the large-decode and long-context
+workloads. All layers run on the GPU; the CPU oracle tracks a subset of
+layers / sequences token by token (layers are independent, and the same
+kernels serve every layer), and every layer is checked through
+size-independent properties: untouched slots bit-exact, admitted slots read
+back as exact zeros, the rolling conv state equal to the last K-1 inputs,
+finite states."""
+import numpy as np
+import pytest
+
+from gdn_testlib import O, DK, DV, K, conv_dim, dev, host, rel_l2, say
+
+pytestmark = pytest.mark.gpu
+
+Y_TOL = 2e-2
+STATE_TOL = 1e-3
+HK, HV = 16, 32
+D = conv_dim(HK, HV)
+
+
+def _ids(lst):
+    return dev(np.asarray(lst, np.int32))
+
+
+def _layer_params(torch, gen, gpu, L):
+    bf = torch.bfloat16
+    conv_w = [(torch.randn((D, K), generator=gen, device=gpu) * 0.25).to(bf) for _ in range(L)]
+    A_log = [torch.rand(HV, generator=gen, device=gpu) * float(np.log(16.0)) for _ in range(L)]
+    dt_bias = [torch.randn(HV, generator=gen, device=gpu) * 0.1 for _ in range(L)]
+    return conv_w, A_log, dt_bias
+
+
+def _np_params(conv_w, A_log, dt_bias, l):
+    return (host(conv_w[l].view(__import__("torch").int16)), host(A_log[l]), host(dt_bias[l]))
+
+
+def test_config2_large_ragged_decode_with_churn(gpu):
+    """30 layers x 1024 slots, B=64 at scattered slots, 256 steps; every 16
+    steps 8 sequences retire and 8 are admitted into the freed slots with
+    zeroed state. Layers 0 and 29 are tracked by the oracle."""
+    import torch
+    import gdn_amd
+    L, S, B, steps = 30, 1024, 64, 256
+    tracked = (0, 29)
+    say("config2", f"L={L} S={S} B={B} steps={steps} tracked layers={tracked}")
+    rng = np.random.default_rng(600)
+    gen = torch.Generator(device=gpu).manual_seed(600)
+    pool = gdn_amd.Pool(L, S, HK, HV)
+    conv_w, A_log, dt_bias = _layer_params(torch, gen, gpu, L)
+    # seeded random states in every slot of every layer
+    ids_all = _ids(np.arange(S))
+    chunk = 128
+    st_chunk = torch.empty((chunk, HV, DV, DK), dtype=torch.float32, device=gpu)
+    cs_chunk = torch.empty((chunk, K - 1, D), dtype=torch.bfloat16, device=gpu)
+    for l in range(L):
+        for s0 in range(0, S, chunk):
+            st_chunk.normal_(0.0, 0.01, generator=gen)
+            cs_chunk.normal_(0.0, 1.0, generator=gen)
+            pool.write(l, ids_all[s0:s0 + chunk], st_chunk, cs_chunk)
+    active = [int(s) for s in rng.choice(S, B, replace=False)]
+    ever = set(active)
+    # oracle copies of the tracked layers' active slots
+    buf_s = torch.empty((B, HV, DV, DK), dtype=torch.float32, device=gpu)
+    buf_c = torch.empty((B, K - 1, D), dtype=torch.int16, device=gpu)
+    ost, ocs = {}, {}
+    for l in tracked:
+        pool.read(l, _ids(active), buf_s, buf_c)
+        ost[l], ocs[l] = host(buf_s), host(buf_c)
+    # a full copy of one untracked layer, to check untouched slots bit-exact
+    probe_layer = 15
+    before_s = torch.empty((S, HV, DV, DK), dtype=torch.float32, device=gpu)
+    before_c = torch.empty((S, K - 1, D), dtype=torch.int16, device=gpu)
+    pool.read(probe_layer, ids_all, before_s, before_c)
+    params_np = {l: _np_params(conv_w, A_log, dt_bias, l) for l in tracked}
+    y = torch.empty((L, B, HV, DV), dtype=torch.bfloat16, device=gpu)
+    worst_y = 0.0
+    d_ids = _ids(active)
+    for step in range(steps):
+        x = (torch.randn((L, B, D), generator=gen, device=gpu)).to(torch.bfloat16)
+        ab = (torch.randn((L, B, 2 * HV), generator=gen, device=gpu)).to(torch.bfloat16)
+        for l in range(L):
+            pool.decode(l, d_ids, x[l], ab[l], A_log[l], dt_bias[l], conv_w[l], y[l])
+        for l in tracked:
+            w, al, dtb = params_np[l]
+            yr, ocs[l], ost[l] = O.decode(ocs[l], ost[l], host(x[l].view(torch.int16)),
+                                          host(ab[l].view(torch.int16)), al, dtb, w, HK, HV)
+            dy = np.abs(O.bf16_to_f32(host(y[l].view(torch.int16))) - O.bf16_to_f32(yr))
+            worst_y = max(worst_y, float(dy.max()))
+        if (step + 1) % 16 == 0:
+            pos = sorted(int(p) for p in rng.choice(B, 8, replace=False))
+            freed = [active[p] for p in pos]
+            keep = [i for i in range(B) if i not in pos]
+            active = [active[i] for i in keep] + freed
+            pool.zero(-1, _ids(freed))
+            pool.read(7, _ids(freed), buf_s[:8], buf_c[:8])
+            assert not host(buf_s[:8]).any() and not host(buf_c[:8]).any(), "admitted slot not zero"
+            for l in tracked:
+                ost[l] = np.concatenate([ost[l][keep], np.zeros((8, HV, DV, DK), np.float32)])
+                ocs[l] = np.concatenate([ocs[l][keep], np.zeros((8, K - 1, D), np.uint16)])
+            d_ids = _ids(active)
+    assert worst_y <= Y_TOL
+    worst_s = 0.0
+    for l in tracked:
+        pool.read(l, d_ids, buf_s, buf_c)
+        assert np.array_equal(host(buf_c), ocs[l])
+        worst_s = max(worst_s, max(rel_l2(host(buf_s)[i], ost[l][i]) for i in range(B)))
+    after_s = torch.empty_like(before_s)
+    after_c = torch.empty_like(before_c)
+    pool.read(probe_layer, ids_all, after_s, after_c)
+    untouched = torch.tensor(sorted(set(range(S)) - ever), device=gpu)
+    assert torch.equal(after_s[untouched], before_s[untouched])
+    assert torch.equal(after_c[untouched], before_c[untouched])
+    assert torch.isfinite(after_s).all()
+    say("config2 worst |dy|", worst_y, "worst state relL2", worst_s)
+    assert worst_s <= STATE_TOL
+    assert pool.check() == 0
+
+
+def test_config4_long_context(gpu):
+    """30 layers; 8 sequences each a single 16384-token prefill (1% of tokens
+    with k scaled x8 before the norm), then 512 decode steps at B=8. Layer 0,
+    sequences 0 and 5, are checked after the prefill and every 128 steps."""
+    import torch
+    import gdn_amd
+    L, nseq, P, steps = 30, 8, 16384, 512
+    chk_layer, chk_seqs = 0, (0, 5)
+    say("config4", f"L={L} nseq={nseq} prefill={P} decode={steps} check layer={chk_layer} "
+        f"seqs={chk_seqs}")
+    gen = torch.Generator(device=gpu).manual_seed(700)
+    pool = gdn_amd.Pool(L, 12, HK, HV)
+    conv_w, A_log, dt_bias = _layer_params(torch, gen, gpu, L)
+    slots = [3, 7, 1, 10, 0, 5, 11, 8]
+    d_ids = _ids(slots)
+    pool.zero(-1, d_ids)
+    cu = dev(np.arange(nseq + 1, dtype=np.int32) * P)
+    total = nseq * P
+    y = torch.empty((total, HV, DV), dtype=torch.bfloat16, device=gpu)
+    w_np, al_np, dtb_np = _np_params(conv_w, A_log, dt_bias, chk_layer)
+    ref_cs, ref_st = {}, {}
+    for l in range(L):
+        x = torch.randn((total, D), generator=gen, device=gpu)
+        outl = torch.rand(total, generator=gen, device=gpu) < 0.01
+        x[:, HK * DK:2 * HK * DK] *= torch.where(outl, 8.0, 1.0)[:, None]
+        x = x.to(torch.bfloat16)
+        ab = torch.randn((total, 2 * HV), generator=gen, device=gpu).to(torch.bfloat16)
+        pool.prefill(l, d_ids, cu, total, x, ab, A_log[l], dt_bias[l], conv_w[l], y)
+        if l == chk_layer:
+            torch.cuda.synchronize()
+            xn, abn, yn = host(x.view(torch.int16)), host(ab.view(torch.int16)), host(y.view(torch.int16))
+            worst = 0.0
+            for sq in chk_seqs:
+                a, b = sq * P, (sq + 1) * P
+                say("config4 oracle prefill", f"seq {sq}")
+                yr, ref_cs[sq], ref_st[sq] = O.prefill(np.zeros((K - 1, D), np.uint16),
+                                                       np.zeros((HV, DV, DK), np.float32),
+                                                       xn[a:b], abn[a:b], al_np, dtb_np, w_np,
+                                                       HK, HV)
+                worst = max(worst, float(np.max(np.abs(O.bf16_to_f32(yn[a:b]) - O.bf16_to_f32(yr)))))
+            assert np.all(np.isfinite(O.bf16_to_f32(yn)))
+            say("config4 after prefill: worst |dy|", worst)
+            assert worst <= Y_TOL
+    buf_s = torch.empty((nseq, HV, DV, DK), dtype=torch.float32, device=gpu)
+    buf_c = torch.empty((nseq, K - 1, D), dtype=torch.int16, device=gpu)
+
+    def check_states(tag):
+        pool.read(chk_layer, d_ids, buf_s, buf_c)
+        gs, gc = host(buf_s), host(buf_c)
+        worst = 0.0
+        for sq in chk_seqs:
+            assert np.array_equal(gc[sq], ref_cs[sq])
+            worst = max(worst, rel_l2(gs[sq], ref_st[sq]))
+        assert np.all(np.isfinite(gs))
+        say(f"config4 {tag}: worst state relL2", worst)
+        assert worst <= STATE_TOL
+
+    check_states("after prefill")
+    yd = torch.empty((nseq, HV, DV), dtype=torch.bfloat16, device=gpu)
+    worst_y = 0.0
+    for step in range(steps):
+        for l in range(L):
+            x = torch.randn((nseq, D), generator=gen, device=gpu).to(torch.bfloat16)
+            ab = torch.randn((nseq, 2 * HV), generator=gen, device=gpu).to(torch.bfloat16)
+            pool.decode(l, d_ids, x, ab, A_log[l], dt_bias[l], conv_w[l], yd)
+            if l == chk_layer:
+                xn, abn = host(x.view(torch.int16)), host(ab.view(torch.int16))
+                ydn = O.bf16_to_f32(host(yd.view(torch.int16)))
+                for sq in chk_seqs:
+                    yr, c1, s1 = O.decode(ref_cs[sq][None], ref_st[sq][None], xn[sq:sq + 1],
+                                          abn[sq:sq + 1], al_np, dtb_np, w_np, HK, HV)
+                    ref_cs[sq], ref_st[sq] = c1[0], s1[0]
+                    worst_y = max(worst_y, float(np.max(np.abs(ydn[sq] - O.bf16_to_f32(yr[0])))))
+        if (step + 1) % 128 == 0:
+            check_states(f"after {step + 1} decode steps")
+            say("config4 decode worst |dy| so far", worst_y)
+            assert worst_y <= Y_TOL
+    assert pool.check() == 0
