@@ -57,6 +57,11 @@ def parse_args(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (PMC byte-count calibration)")
+    ap.add_argument("--prefill", action="store_true",
+                    help="measure the chunked varlen prefill instead: 8 sequences x 16384 "
+                         "tokens per layer over --layers layers")
+    ap.add_argument("--prefill-seqs", type=int, default=8)
+    ap.add_argument("--prefill-len", type=int, default=16384)
     ap.add_argument("--rmw-ceiling", action="store_true",
                     help="only time a plain in-place multiply over 30 x 128 MiB buffers "
                          "(the decode's per-launch state bytes, read + write)")
@@ -96,6 +101,78 @@ def rmw_ceiling(layers: int = 30, mib: int = 128, reps: int = 8):
     nbytes = 2 * mib * (1 << 20)
     print(json.dumps({"rmw_ceiling_us_per_launch": round(us, 2), "bytes_per_launch": nbytes,
                       "GBps": round(nbytes / us * 1e-3, 1)}), flush=True)
+
+
+# Algorithmic FLOPs of the chunked (WY form, chunk C) prefill per (token,
+# value head): 12*C*Dk + 6*Dk^2 + C^2/3 = 197,973 at C=64, Dk=128.
+PREFILL_CHUNK = 64
+PREFILL_FLOP_PER_TOKEN_HEAD = 12 * PREFILL_CHUNK * DK + 6 * DK * DK + PREFILL_CHUNK ** 2 / 3
+PEAK_BF16_TFLOPS = 2500.0
+
+
+def prefill_bench(args):
+    """Chunked varlen prefill: `prefill_seqs` sequences of `prefill_len`
+    tokens packed in one gdn_prefill_varlen call per layer, from zeroed slots,
+    inputs resident in HBM. Prints one JSON line."""
+    import torch
+
+    import gdn_amd
+    dev = torch.device("cuda:0")
+    L, n, P = args.layers, args.prefill_seqs, args.prefill_len
+    total = n * P
+    pool = gdn_amd.Pool(L, n, HK, HV)
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    bf = torch.bfloat16
+    conv_w = [(torch.randn((D, KW), generator=gen, device=dev) * 0.25).to(bf) for _ in range(L)]
+    A_log = [torch.rand(HV, generator=gen, device=dev) * math.log(16.0) for _ in range(L)]
+    dt_bias = [torch.randn(HV, generator=gen, device=dev) * 0.1 for _ in range(L)]
+    nsets = 2
+    x = [torch.randn((total, D), generator=gen, device=dev).to(bf) for _ in range(nsets)]
+    ab = [torch.randn((total, 2 * HV), generator=gen, device=dev).to(bf) for _ in range(nsets)]
+    y = torch.empty((total, HV, DV), dtype=bf, device=dev)
+    ids = torch.arange(n, dtype=torch.int32, device=dev)
+    cu = torch.arange(n + 1, dtype=torch.int32, device=dev) * P
+
+    def run_layers():
+        pool.zero(-1, ids)
+        for l in range(L):
+            pool.prefill(l, ids, cu, total, x[l % nsets], ab[l % nsets], A_log[l], dt_bias[l],
+                         conv_w[l], y)
+
+    run_layers()  # warmup (also grows the workspace)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record()
+    run_layers()
+    e1.record()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    gpu_s = e0.elapsed_time(e1) * 1e-3
+    flops = PREFILL_FLOP_PER_TOKEN_HEAD * total * HV * L
+    tflops = flops / gpu_s / 1e12
+    out = {
+        "metric": "GDN chunked prefill tokens/s (packed varlen, all layers)",
+        "value": round(total / elapsed, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "ms_per_step": round(elapsed * 1e3, 3),
+        "higher_is_better": True,
+        "dtype": "bf16 MFMA products, f32 state",
+        "data": "synthetic",
+        "config": {"workload": f"{n} x {P}-token prefills per layer, {L} layers, chunk 64",
+                   "layers": L, "sequences": n, "tokens_per_sequence": P},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                     "flop_per_token_head": PREFILL_FLOP_PER_TOKEN_HEAD,
+                     "note": "all prefill launches (conv, norm/gates, chunk recurrence)"},
+    }
+    flags = pool.check()
+    if flags:
+        print(f"pool status flags 0x{flags:x}", file=sys.stderr)
+        return 1
+    print(json.dumps(out), flush=True)
+    return 0
 
 
 class Workload:
@@ -210,6 +287,8 @@ def main(argv=None):
     if args.rmw_ceiling:
         rmw_ceiling()
         return 0
+    if args.prefill:
+        return prefill_bench(args)
     w = Workload(args)
     for _ in range(args.warmup):
         w.step()
