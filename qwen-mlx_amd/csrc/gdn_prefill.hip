@@ -157,366 +157,341 @@ __global__ __launch_bounds__(256) void prefill_prep_kernel(
   }
 }
 
-// 4. Chunked (WY form) recurrence, one work-group of 256 threads per
-// (sequence, value head, 64-row block of Dv), walking the sequence's chunks
-// of kC = 64 tokens. With G the cumulative log decay inside a chunk, the
-// chunk start state S ([Dv, Dk]) and T = (I + L)^-1,
+// 4. Chunked (WY form) recurrence, one work-group of 512 threads (8 waves) per
+// (sequence, value head), walking the sequence's chunks of kC = 64 tokens. With G the cumulative log decay inside a chunk and S
+// ([Dv, Dk]) the state at the chunk start:
 //   L_ij = beta_i (k_i.k_j) exp(G_i - G_j)   (j < i)
 //   P_ij = (q_i.k_j) exp(G_i - G_j)          (j <= i)
 //   R    = beta * (V - exp(G) * (K S^T))      per token row
-//   V'   = T R
+//   (I + L) V' = R                            (block forward substitution)
 //   O    = exp(G) * (Q S^T) + P V'
 //   S^T <- exp(G_C) S^T + K^T (exp(G_C - G) * V')
 // which equals the token-by-token recurrence of metal_gdn.rs:37-62.
-// Products use v_mfma_f32_16x16x32_bf16: k and q are bf16 already (exact);
-// f32 operands on the state path (S, T, R, V') are split into bf16 hi + lo
-// parts so they carry ~16 mantissa bits. The state lives in MFMA
-// accumulators (S^T tiles) across chunks, with an f32 copy in LDS as the B
-// operand of K S^T and Q S^T. Padded rows of a partial chunk have k = q =
-// v = beta = 0 and log decay 0, so they leave every result unchanged.
+//
+// Work split: waves 0-3 form K K^T (token row block w) and invert its
+// diagonal block, waves 4-7 form Q K^T; every other step runs wave-locally on
+// the wave's own 16 state rows (dv block w), so a chunk needs three
+// work-group barriers. The triangular solve works on V'
+// directly, 16-token blocks: V'_I = D_I (R_I - sum_{j<I} L_Ij V'_j) with
+// D_I = (I + L_II)^-1, on v_mfma_f32_16x16x16_bf16, whose accumulator layout
+// is its B-operand layout, so V' blocks feed the next products without data
+// movement. K K^T and Q K^T use v_mfma_f32_16x16x32_bf16. k and q are bf16
+// (exact operands); f32 operands on the state path (S, L, D, R, V') are split
+// into bf16 hi + lo parts (~16 mantissa bits). The state lives in MFMA
+// accumulators (S^T tiles) across chunks; split into hi/lo they are directly
+// the B operands of K S^T and Q S^T. The next chunk's inputs are loaded into
+// registers while the current chunk computes. Padded rows of a
+// partial chunk have k = q = v = beta = 0 and log decay 0, so they change
+// nothing.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 namespace {
 constexpr int kC = 64;
-constexpr int kDVB = 64;
-constexpr int kLdK = kDk + 8;   // bf16 [64][128] rows (272 B)
-constexpr int kLdT = kC + 8;    // bf16 [*][64] rows (144 B)
-constexpr int kLdF = kC + 4;    // f32 [*][64] rows (272 B)
-constexpr int kLdS = kDk + 4;   // f32 [64][128] rows (528 B)
+constexpr int kLdK = kDk + 8;  // bf16 [64][128] rows (272 B)
+constexpr int kLdT = kC + 8;   // bf16 [*][64] rows (144 B)
+constexpr int kLdD = 24;       // bf16 [16][16] blocks (48 B rows)
 
 struct ChunkSmem {
-  uint16_t K[kC][kLdK];    // k, token-major
-  uint16_t KT[kDk][kLdT];  // k, dk-major
-  uint16_t Q[kC][kLdK];    // q, token-major
-  uint16_t V[kC][kLdT];    // v of this Dv block, token-major
-  uint16_t P[kC][kLdT];    // masked, decayed q.k
-  float Tm[kC][kLdF];      // L, then T = (I + L)^-1
-  float RV[kDVB][kLdF];    // R^T, then V'^T ([dv][token])
-  float S[kDVB][kLdS];     // state block [dv][dk] (chunk start)
-  float X[4][16][16];      // per-wave block scratch of the solve
+  uint16_t K[kC][kLdK];      // k, token-major
+  uint16_t KT[kDk][kLdT];    // k, dk-major
+  uint16_t Q[kC][kLdK];      // q, token-major
+  uint16_t V[kC][kLdK];      // v of the head, token-major
+  uint16_t P[kC][kLdT];      // masked, decayed q.k
+  uint16_t NLh[kC][kLdT];    // -L, bf16 hi part
+  uint16_t NLl[kC][kLdT];    // -L, bf16 lo part
+  float Ld[4][16][17];       // diagonal 16x16 blocks of L (f32)
+  uint16_t Dh[4][16][kLdD];  // D_I = (I + L_II)^-1, hi
+  uint16_t Dl[4][16][kLdD];  // lo
   float beta[kC], G[kC], eG[kC], dec_end[kC];
 };
 
-__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+__device__ __forceinline__ f32x4 mfma32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
+__device__ __forceinline__ f32x4 mfma16(s16x4 a, s16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
 
-// Operand fragment of a 16x32 (rows x k) block whose k runs contiguous in
-// memory: lane l takes row r0 + l%16, k = k0 + 8*(l/16) .. +7. It serves as
-// the A operand (rows = output rows) and as the B operand (rows = output
-// columns) of v_mfma_f32_16x16x32_bf16.
-__device__ __forceinline__ bf16x8 frag(const uint16_t* base, int ld, int r0, int k0, int lane) {
+// Operand fragments whose k runs contiguous in memory; they serve as A
+// operands (rows = output rows) and as B operands (rows = output columns).
+//   16x16x32: lane l takes row r0 + l%16, k = k0 + 8*(l/16) .. +7
+//   16x16x16: lane l takes row r0 + l%16, k = k0 + 4*(l/16) .. +3
+// A 16x16 accumulator tile holds row 4*(l/16) + r, column l%16 in register r,
+// which is exactly a 16x16x16 B operand.
+__device__ __forceinline__ bf16x8 frag32(const uint16_t* base, int ld, int r0, int k0, int lane) {
   return *reinterpret_cast<const bf16x8*>(base + (r0 + (lane & 15)) * ld + k0 + (lane >> 4) * 8);
 }
-
-__device__ __forceinline__ void split8(const float (&x)[8], bf16x8& hi, bf16x8& lo) {
-#pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const __bf16 h = (__bf16)x[u];
-    hi[u] = h;
-    lo[u] = (__bf16)(x[u] - (float)h);
-  }
+__device__ __forceinline__ s16x4 frag16(const uint16_t* base, int ld, int r0, int k0, int lane) {
+  return *reinterpret_cast<const s16x4*>(base + (r0 + (lane & 15)) * ld + k0 + (lane >> 4) * 4);
 }
 
-// The same fragment taken from f32 storage and split into hi + lo; `scale`
-// (indexed by k) multiplies the values first when given.
-__device__ __forceinline__ void frag_split(const float* base, int ld, int r0, int k0, int lane,
-                                           const float* scale, bf16x8& hi, bf16x8& lo) {
-  const int k = k0 + (lane >> 4) * 8;
-  const float* p = base + (r0 + (lane & 15)) * ld + k;
-  const f32x4 a = *reinterpret_cast<const f32x4*>(p);
-  const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
-  float x[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-  if (scale) {
+__device__ __forceinline__ short bfbits(float x) { return (short)f2bf(x); }
+
+// f32 tile -> bf16 hi + lo (hi + lo carries ~16 mantissa bits of x)
+__device__ __forceinline__ void split4(const f32x4& x, s16x4& hi, s16x4& lo) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) x[u] *= scale[k + u];
+  for (int u = 0; u < 4; ++u) {
+    const uint16_t h = f2bf(x[u]);
+    hi[u] = (short)h;
+    lo[u] = bfbits(x[u] - bf2f(h));
   }
-  split8(x, hi, lo);
 }
 }  // namespace
 
 template <int R>
-__global__ __launch_bounds__(256) void prefill_chunk_kernel(
+__global__ __launch_bounds__(512) void prefill_chunk_kernel(
     float* __restrict__ state, const int32_t* __restrict__ slot_ids,
     const int32_t* __restrict__ cu, int num_slots, int Hk, int D, int T,
     const uint16_t* __restrict__ qn, const uint16_t* __restrict__ kn,
     const uint16_t* __restrict__ xc, const float* __restrict__ lgv,
     const uint16_t* __restrict__ betav, uint16_t* __restrict__ y, uint32_t* __restrict__ status) {
+  constexpr int NT = 512;
   __shared__ ChunkSmem sm;
-  const int dvb = blockIdx.x, hv = blockIdx.y, s = blockIdx.z;
+  const int hv = blockIdx.x, s = blockIdx.y;
   const int Hv = Hk * R, hk = hv / R;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane0 = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, scalar
   const int slot = slot_ids[s];
   if ((unsigned)slot >= (unsigned)num_slots) {
-    if (tid == 0 && dvb == 0 && hv == 0) flag_status(status, GDN_FLAG_BAD_SLOT);
+    if (tid == 0 && hv == 0) flag_status(status, GDN_FLAG_BAD_SLOT);
     return;
   }
   const int st = min(max(cu[s], 0), T), en = min(max(cu[s + 1], st), T);
   if (en <= st) return;
-  const int dv0 = dvb * kDVB;
-  float* gstate = state + ((size_t)slot * Hv + hv) * kTileElems;  // [Dv][Dk]
-  const int lr = (lane >> 4) * 4, lc = lane & 15;  // accumulator row base / column
+  // this lane's state row (accumulator column) and 4-row group
+  float* gstate = state + ((size_t)slot * Hv + hv) * kTileElems + (size_t)(16 * w + (lane0 & 15)) * kDk +
+                  4 * (lane0 >> 4);
 
-  // state accumulators: S^T tiles, dk block 2*wave + a, dv block J
-  f32x4 acc[2][4];
+  // state accumulators: S^T tiles (dk block a, this wave's 16 state rows)
+  f32x4 acc[8];
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < 8; ++a)
+    acc[a] = *reinterpret_cast<const f32x4*>(gstate + 16 * a);
+
+  // chunk inputs in registers (prefetched one chunk ahead)
+  const size_t vcol = 2 * (size_t)Hk * kDk + (size_t)hv * kDv;
+  uint4 kv[2], qv[2], vv[2];
+  float pb = 0.f, pl = 0.f;
+  auto load_inputs = [&](int c0) {
+    const int n = min(kC, en - c0);
 #pragma unroll
-    for (int J = 0; J < 4; ++J) {
-      const int dk = 16 * (2 * wave + a) + lr, dv = 16 * J + lc;
-      acc[a][J] = *reinterpret_cast<const f32x4*>(gstate + (size_t)(dv0 + dv) * kDk + dk);
-      *reinterpret_cast<f32x4*>(&sm.S[dv][dk]) = acc[a][J];
+    for (int u = 0; u < 2; ++u) {
+      const int e = tid + NT * u, i = e >> 4, c = (e & 15) * 8;
+      kv[u] = make_uint4(0u, 0u, 0u, 0u);
+      qv[u] = kv[u];
+      vv[u] = kv[u];
+      if (i < n) {
+        const size_t off = ((size_t)(c0 + i) * Hk + hk) * kDk + c;
+        kv[u] = *reinterpret_cast<const uint4*>(kn + off);
+        qv[u] = *reinterpret_cast<const uint4*>(qn + off);
+        vv[u] = *reinterpret_cast<const uint4*>(xc + (size_t)(c0 + i) * D + vcol + c);
+      }
     }
+    pb = 0.f;
+    pl = 0.f;
+    if (w == 0 && lane0 < n) {
+      pb = bf2f(betav[(size_t)(c0 + lane0) * Hv + hv]);
+      pl = lgv[(size_t)(c0 + lane0) * Hv + hv];
+    }
+  };
+  auto store_inputs = [&]() {
+    // Opaque to the compiler until here, so it cannot unpack the prefetched
+    // words (and wait for the loads) right after issuing them.
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      asm volatile("" : "+v"(kv[u].x), "+v"(kv[u].y), "+v"(kv[u].z), "+v"(kv[u].w),
+                   "+v"(qv[u].x), "+v"(qv[u].y), "+v"(qv[u].z), "+v"(qv[u].w),
+                   "+v"(vv[u].x), "+v"(vv[u].y), "+v"(vv[u].z), "+v"(vv[u].w));
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int e = tid + NT * u, i = e >> 4, c = (e & 15) * 8;
+      *reinterpret_cast<uint4*>(&sm.K[i][c]) = kv[u];
+      *reinterpret_cast<uint4*>(&sm.Q[i][c]) = qv[u];
+      *reinterpret_cast<uint4*>(&sm.V[i][c]) = vv[u];
+      const uint16_t* kb = reinterpret_cast<const uint16_t*>(&kv[u]);
+#pragma unroll
+      for (int x = 0; x < 8; ++x) sm.KT[c + x][i] = kb[x];
+    }
+    if (w == 0) {  // inclusive prefix sum of the log decay
+      float gsum = pl;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float t = __shfl_up(gsum, off, 64);
+        if (lane0 >= off) gsum += t;
+      }
+      const float gC = __shfl(gsum, 63, 64);
+      sm.beta[lane0] = pb;
+      sm.G[lane0] = gsum;
+      sm.eG[lane0] = expf(gsum);
+      sm.dec_end[lane0] = expf(gC - gsum);
+    }
+  };
 
-  const size_t vcol = 2 * (size_t)Hk * kDk + (size_t)hv * kDv + dv0;
+  load_inputs(st);
   for (int c0 = st; c0 < en; c0 += kC) {
     const int n = min(kC, en - c0);
-    // (a) chunk inputs -> LDS; rows >= n are zero
-    {
-      uint4 kv[4], qv[4], vv[2];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int e = tid + 256 * u, i = e >> 4, c = (e & 15) * 8;
-        kv[u] = make_uint4(0u, 0u, 0u, 0u);
-        qv[u] = kv[u];
-        if (i < n) {
-          const size_t off = ((size_t)(c0 + i) * Hk + hk) * kDk + c;
-          kv[u] = *reinterpret_cast<const uint4*>(kn + off);
-          qv[u] = *reinterpret_cast<const uint4*>(qn + off);
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int e = tid + 256 * u, i = e >> 3, c = (e & 7) * 8;
-        vv[u] = make_uint4(0u, 0u, 0u, 0u);
-        if (i < n) vv[u] = *reinterpret_cast<const uint4*>(xc + (size_t)(c0 + i) * D + vcol + c);
-      }
-      float b = 0.f, l = 0.f;
-      if (wave == 0 && lane < n) {
-        b = bf2f(betav[(size_t)(c0 + lane) * Hv + hv]);
-        l = lgv[(size_t)(c0 + lane) * Hv + hv];
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int e = tid + 256 * u, i = e >> 4, c = (e & 15) * 8;
-        *reinterpret_cast<uint4*>(&sm.K[i][c]) = kv[u];
-        *reinterpret_cast<uint4*>(&sm.Q[i][c]) = qv[u];
-        const uint16_t* kb = reinterpret_cast<const uint16_t*>(&kv[u]);
-#pragma unroll
-        for (int w = 0; w < 8; ++w) sm.KT[c + w][i] = kb[w];
-      }
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int e = tid + 256 * u, i = e >> 3, c = (e & 7) * 8;
-        *reinterpret_cast<uint4*>(&sm.V[i][c]) = vv[u];
-      }
-      if (wave == 0) {  // inclusive prefix sum of the log decay
-        float gsum = l;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-          const float t = __shfl_up(gsum, off, 64);
-          if (lane >= off) gsum += t;
-        }
-        const float gC = __shfl(gsum, 63, 64);
-        sm.beta[lane] = b;
-        sm.G[lane] = gsum;
-        sm.eG[lane] = expf(gsum);
-        sm.dec_end[lane] = expf(gC - gsum);
-      }
-    }
+    // Lane-derived LDS addresses are recomputed in every chunk (a few VALU
+    // ops) instead of being held in registers across the loop.
+    int lane = lane0;
+    asm volatile("" : "+v"(lane));
+    const int lq = lane >> 4, lc = lane & 15;
+    const int drow = 16 * w + lc;
+    store_inputs();
     __syncthreads();
+    if (c0 + kC < en) load_inputs(c0 + kC);
 
-    // (b) K K^T, Q K^T -> L (Tm, f32) and P (bf16); wave owns row block `wave`
+    // (b) waves 0-3: K K^T for token rows 16w.. -> -L (hi/lo) and its f32
+    // diagonal block; waves 4-7: Q K^T for token rows 16(w-4).. -> P. Column
+    // blocks above the row block are zero and skipped.
     {
-      f32x4 akk[4], aqk[4];
+      const int I = w & 3;
+      const bool isq = w >= 4;
+      const uint16_t* A = isq ? &sm.Q[0][0] : &sm.K[0][0];
 #pragma unroll
       for (int J = 0; J < 4; ++J) {
-        akk[J] = f32x4{0.f, 0.f, 0.f, 0.f};
-        aqk[J] = akk[J];
-      }
+        if (J > I) continue;
+        f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const bf16x8 ak = frag(&sm.K[0][0], kLdK, 16 * wave, 32 * ks, lane);
-        const bf16x8 aq = frag(&sm.Q[0][0], kLdK, 16 * wave, 32 * ks, lane);
-#pragma unroll
-        for (int J = 0; J < 4; ++J) {
-          const bf16x8 bk = frag(&sm.K[0][0], kLdK, 16 * J, 32 * ks, lane);
-          akk[J] = mfma16(ak, bk, akk[J]);
-          aqk[J] = mfma16(aq, bk, aqk[J]);
-        }
-      }
-#pragma unroll
-      for (int J = 0; J < 4; ++J)
+        for (int ks = 0; ks < 4; ++ks)
+          c = mfma32(frag32(A, kLdK, 16 * I, 32 * ks, lane),
+                     frag32(&sm.K[0][0], kLdK, 16 * J, 32 * ks, lane), c);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int i = 16 * wave + lr + r, j = 16 * J + lc;
+          const int i = 16 * I + 4 * lq + r, j = 16 * J + lc;
           const float d = expf(fminf(sm.G[i] - sm.G[j], 0.f));
-          sm.Tm[i][j] = j < i ? sm.beta[i] * akk[J][r] * d : 0.f;
-          sm.P[i][j] = f2bf(j <= i ? aqk[J][r] * d : 0.f);
+          if (isq) {
+            sm.P[i][j] = f2bf(j <= i ? c[r] * d : 0.f);
+          } else {
+            const float lv = j < i ? sm.beta[i] * c[r] * d : 0.f;
+            const uint16_t nh = f2bf(-lv);
+            sm.NLh[i][j] = nh;
+            sm.NLl[i][j] = f2bf(-lv - bf2f(nh));
+            if (J == I) sm.Ld[I][4 * lq + r][lc] = lv;
+          }
         }
-    }
-
-    // (d) K S^T and Q S^T for this wave's token rows (independent of (c))
-    f32x4 yk[4], zq[4];
-#pragma unroll
-    for (int J = 0; J < 4; ++J) {
-      yk[J] = f32x4{0.f, 0.f, 0.f, 0.f};
-      zq[J] = yk[J];
-    }
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const bf16x8 ak = frag(&sm.K[0][0], kLdK, 16 * wave, 32 * ks, lane);
-      const bf16x8 aq = frag(&sm.Q[0][0], kLdK, 16 * wave, 32 * ks, lane);
-#pragma unroll
-      for (int J = 0; J < 4; ++J) {
-        bf16x8 sh, sl;
-        frag_split(&sm.S[0][0], kLdS, 16 * J, 32 * ks, lane, nullptr, sh, sl);
-        yk[J] = mfma16(ak, sh, yk[J]);
-        yk[J] = mfma16(ak, sl, yk[J]);
-        zq[J] = mfma16(aq, sh, zq[J]);
-        zq[J] = mfma16(aq, sl, zq[J]);
       }
     }
-    __syncthreads();
-
-    // (c) T = (I + L)^-1 in place: 16x16 diagonal blocks by forward
-    // substitution (wave b, lanes = columns), then block rows 1..3 with
-    // T_ij = -D_i sum_{k=j}^{i-1} L_ik T_kj (all X_ij read L before any T_ij
-    // overwrites it).
-    if (lane < 16) {
-      const int b0 = 16 * wave, j = lane;
+    // (c) waves 0-3: D_w = (I + L_ww)^-1 by forward substitution (lanes 0..15
+    // = columns)
+    if (w < 4 && lane < 16) {
+      const int j = lane;
       float t[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
+        asm volatile("" ::: "memory");  // bound live ranges: one row of L at a time
         float a = i == j ? 1.f : 0.f;
 #pragma unroll
-        for (int k = 0; k < i; ++k) a -= sm.Tm[b0 + i][b0 + k] * t[k];
+        for (int k = 0; k < i; ++k) a -= sm.Ld[w][i][k] * t[k];
         t[i] = a;
       }
 #pragma unroll
-      for (int i = 0; i < 16; ++i) sm.Tm[b0 + i][b0 + j] = t[i];
-    }
-    __syncthreads();
-    {
-      const int rr = lane >> 2, cq = (lane & 3) * 4;
-      for (int bi = 1; bi < 4; ++bi) {
-        if (wave < bi) {
-          f32x4 x = {0.f, 0.f, 0.f, 0.f};
-          for (int kb = wave; kb < bi; ++kb)
-#pragma unroll
-            for (int m = 0; m < 16; ++m)
-              x += sm.Tm[16 * bi + rr][16 * kb + m] *
-                   *reinterpret_cast<const f32x4*>(&sm.Tm[16 * kb + m][16 * wave + cq]);
-          *reinterpret_cast<f32x4*>(&sm.X[wave][rr][cq]) = x;
-        }
-        __syncthreads();
-        if (wave < bi) {
-          f32x4 t = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int m = 0; m < 16; ++m)
-            t += sm.Tm[16 * bi + rr][16 * bi + m] *
-                 *reinterpret_cast<const f32x4*>(&sm.X[wave][m][cq]);
-          *reinterpret_cast<f32x4*>(&sm.Tm[16 * bi + rr][16 * wave + cq]) = -t;
-        }
-        __syncthreads();
+      for (int i = 0; i < 16; ++i) {
+        const uint16_t h = f2bf(t[i]);
+        sm.Dh[w][i][j] = h;
+        sm.Dl[w][i][j] = f2bf(t[i] - bf2f(h));
       }
     }
-
-    // (e) R = beta * (V - exp(G) * K S^T), stored transposed [dv][token]
+    // (d) Y_I = K_I S^T and Z_I = Q_I S^T for this wave's 16 state rows; the
+    // hi/lo split of the S^T accumulator tiles is the B operand
+    f32x4 yk[4], zq[4];
 #pragma unroll
-    for (int J = 0; J < 4; ++J)
+    for (int I = 0; I < 4; ++I) {
+      yk[I] = f32x4{0.f, 0.f, 0.f, 0.f};
+      zq[I] = yk[I];
+    }
+#pragma unroll
+    for (int a = 0; a < 8; ++a) {
+      asm volatile("" ::: "memory");  // bound live ranges: one dk block at a time
+      s16x4 sh, sl;
+      split4(acc[a], sh, sl);
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        const s16x4 ak = frag16(&sm.K[0][0], kLdK, 16 * I, 16 * a, lane);
+        const s16x4 aq = frag16(&sm.Q[0][0], kLdK, 16 * I, 16 * a, lane);
+        yk[I] = mfma16(ak, sh, yk[I]);
+        yk[I] = mfma16(ak, sl, yk[I]);
+        zq[I] = mfma16(aq, sh, zq[I]);
+        zq[I] = mfma16(aq, sl, zq[I]);
+      }
+    }
+    __syncthreads();
+
+    // (e, f) R_I, then V'_I = D_I (R_I - sum_{j<I} L_Ij V'_j)
+    s16x4 vph[4], vpl[4];
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      f32x4 x;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int i = 16 * wave + lr + r, dv = 16 * J + lc;
-        sm.RV[dv][i] = sm.beta[i] * (bf2f(sm.V[i][dv]) - sm.eG[i] * yk[J][r]);
+        const int i = 16 * I + 4 * lq + r;
+        x[r] = sm.beta[i] * (bf2f(sm.V[i][drow]) - sm.eG[i] * yk[I][r]);
       }
-    __syncthreads();
-
-    // (f) V' = T R (T lower triangular: k blocks above the row block are 0)
-    f32x4 vp[4];
 #pragma unroll
-    for (int J = 0; J < 4; ++J) vp[J] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      if (32 * ks > 16 * wave + 15) continue;
-      bf16x8 th, tl;
-      frag_split(&sm.Tm[0][0], kLdF, 16 * wave, 32 * ks, lane, nullptr, th, tl);
-#pragma unroll
-      for (int J = 0; J < 4; ++J) {
-        bf16x8 rh, rl;
-        frag_split(&sm.RV[0][0], kLdF, 16 * J, 32 * ks, lane, nullptr, rh, rl);
-        vp[J] = mfma16(th, rh, vp[J]);
-        vp[J] = mfma16(th, rl, vp[J]);
-        vp[J] = mfma16(tl, rh, vp[J]);
+      for (int j = 0; j < 4; ++j) {
+        if (j >= I) continue;
+        const s16x4 lh = frag16(&sm.NLh[0][0], kLdT, 16 * I, 16 * j, lane);
+        const s16x4 ll = frag16(&sm.NLl[0][0], kLdT, 16 * I, 16 * j, lane);
+        x = mfma16(lh, vph[j], x);
+        x = mfma16(lh, vpl[j], x);
+        x = mfma16(ll, vph[j], x);
       }
+      s16x4 xh, xl;
+      split4(x, xh, xl);
+      const s16x4 dh = frag16(&sm.Dh[I][0][0], kLdD, 0, 0, lane);
+      const s16x4 dl = frag16(&sm.Dl[I][0][0], kLdD, 0, 0, lane);
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+      v = mfma16(dh, xh, v);
+      v = mfma16(dh, xl, v);
+      v = mfma16(dl, xh, v);
+      split4(v, vph[I], vpl[I]);
     }
-    __syncthreads();
+    // (g) O_I = exp(G) * Z_I + sum_{j<=I} P_Ij V'_j
 #pragma unroll
-    for (int J = 0; J < 4; ++J)
+    for (int I = 0; I < 4; ++I) {
+      f32x4 o;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sm.RV[16 * J + lc][16 * wave + lr + r] = vp[J][r];
-    __syncthreads();
-
-    // (g) O = exp(G) * Q S^T + P V'
+      for (int r = 0; r < 4; ++r) o[r] = zq[I][r] * sm.eG[16 * I + 4 * lq + r];
 #pragma unroll
-    for (int J = 0; J < 4; ++J)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) zq[J][r] *= sm.eG[16 * wave + lr + r];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      if (32 * ks > 16 * wave + 15) continue;
-      const bf16x8 ap = frag(&sm.P[0][0], kLdT, 16 * wave, 32 * ks, lane);
-#pragma unroll
-      for (int J = 0; J < 4; ++J) {
-        bf16x8 vh, vl;
-        frag_split(&sm.RV[0][0], kLdF, 16 * J, 32 * ks, lane, nullptr, vh, vl);
-        zq[J] = mfma16(ap, vh, zq[J]);
-        zq[J] = mfma16(ap, vl, zq[J]);
+      for (int j = 0; j < 4; ++j) {
+        if (j > I) continue;
+        const s16x4 ph = frag16(&sm.P[0][0], kLdT, 16 * I, 16 * j, lane);
+        o = mfma16(ph, vph[j], o);
+        o = mfma16(ph, vpl[j], o);
       }
-    }
-#pragma unroll
-    for (int J = 0; J < 4; ++J)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int i = 16 * wave + lr + r;
-        if (i < n) y[((size_t)(c0 + i) * Hv + hv) * kDv + dv0 + 16 * J + lc] = f2bf(zq[J][r]);
+        const int i = 16 * I + 4 * lq + r;
+        if (i < n) y[((size_t)(c0 + i) * Hv + hv) * kDv + drow] = f2bf(o[r]);
       }
-
+    }
     // (h) S^T <- exp(G_C) S^T + K^T (exp(G_C - G) * V')
     const float eC = sm.eG[kC - 1];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < 8; ++a) acc[a] *= eC;
 #pragma unroll
-      for (int J = 0; J < 4; ++J) acc[a][J] *= eC;
+    for (int j = 0; j < 4; ++j) {
+      asm volatile("" ::: "memory");  // bound live ranges: one token block at a time
+      f32x4 vt;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+      for (int r = 0; r < 4; ++r)
+        vt[r] = (bf2f((uint16_t)vph[j][r]) + bf2f((uint16_t)vpl[j][r])) *
+                sm.dec_end[16 * j + 4 * lq + r];
+      s16x4 th, tl;
+      split4(vt, th, tl);
 #pragma unroll
-      for (int a = 0; a < 2; ++a) {
-        const bf16x8 ak = frag(&sm.KT[0][0], kLdT, 16 * (2 * wave + a), 32 * ks, lane);
-#pragma unroll
-        for (int J = 0; J < 4; ++J) {
-          bf16x8 vh, vl;
-          frag_split(&sm.RV[0][0], kLdF, 16 * J, 32 * ks, lane, sm.dec_end, vh, vl);
-          acc[a][J] = mfma16(ak, vh, acc[a][J]);
-          acc[a][J] = mfma16(ak, vl, acc[a][J]);
-        }
+      for (int a = 0; a < 8; ++a) {
+        const s16x4 kt = frag16(&sm.KT[0][0], kLdT, 16 * a, 16 * j, lane);
+        acc[a] = mfma16(kt, th, acc[a]);
+        acc[a] = mfma16(kt, tl, acc[a]);
       }
     }
     __syncthreads();
-#pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-      for (int J = 0; J < 4; ++J)
-        *reinterpret_cast<f32x4*>(&sm.S[16 * J + lc][16 * (2 * wave + a) + lr]) = acc[a][J];
-    __syncthreads();
   }
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
-#pragma unroll
-    for (int J = 0; J < 4; ++J)
-      *reinterpret_cast<f32x4*>(gstate + (size_t)(dv0 + 16 * J + lc) * kDk + 16 * (2 * wave + a) +
-                                lr) = acc[a][J];
+  for (int a = 0; a < 8; ++a)
+    *reinterpret_cast<f32x4*>(gstate + 16 * a) = acc[a];
 }
 
 size_t prefill_workspace_bytes(int R, int Hk, int total_tokens) {
@@ -548,7 +523,7 @@ static hipError_t launch_prefill_r(const PrefillArgs& a) {
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(prefill_chunk_kernel<R>, dim3(kDv / kDVB, Hv, a.nseq), dim3(256), 0,
+  hipLaunchKernelGGL(prefill_chunk_kernel<R>, dim3(Hv, a.nseq), dim3(512), 0,
                      a.stream, a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk, D,
                      a.total_tokens, ws.qn, ws.kn, ws.xc, ws.lg, ws.beta, a.y, a.status);
   return hipGetLastError();
