@@ -5,12 +5,11 @@
 // over [conv_state | x], silu, split, q/k rms-norm, gates, and one
 // gated_delta_kernel launch with T=S (metal_gdn.rs:37). Here any number of
 // sequences share the launches, each addressed by its slot:
-//   1. conv_kernel       (token, channel) parallel conv + silu -> xc
+//   1. qkv_kernel        conv + silu, q/k rms-norm -> qn/kn/vc, gates -> beta, lg
 //   2. conv_state_kernel last K-1 rows of [conv_state | x] -> slot
-//   3. prep_kernel       q/k rms-norm -> qn/kn, gates -> beta, g
-//   4. chunk_kernel      chunked WY-form recurrence on bf16 MFMA
+//   3. chunk_kernel      chunked WY-form recurrence on bf16 MFMA
 // Workspace layout (each region 256-byte aligned):
-//   xc [T,D] bf16 | qn [T,Hk,Dk] bf16 | kn [T,Hk,Dk] bf16 | beta [T,Hv] bf16 | lg [T,Hv] f32
+//   qn [T,Hk,Dk] bf16 | kn [T,Hk,Dk] bf16 | vc [T,Hv,Dv] bf16 | beta [T,Hv] bf16 | lg [T,Hv] f32
 
 #include "gdn_common.h"
 
@@ -21,20 +20,20 @@ namespace {
 constexpr float kQNormW = 0.0078125f;
 constexpr float kKNormW = 0.08837890625f;
 constexpr float kNormEps = 1e-6f;
+constexpr int kTT = 64;  // tokens per qkv_kernel work-group
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct Workspace {
-  uint16_t* xc;
   uint16_t* qn;
   uint16_t* kn;
+  uint16_t* vc;
   uint16_t* beta;
   float* lg;
 };
 
 size_t carve(void* base, int R, int Hk, int T, Workspace* w) {
   const int Hv = Hk * R;
-  const size_t D = 2 * (size_t)Hk * kDk + (size_t)Hv * kDv;
   size_t off = 0;
   char* p = static_cast<char*>(base);
   auto take = [&](size_t bytes) {
@@ -43,9 +42,9 @@ size_t carve(void* base, int R, int Hk, int T, Workspace* w) {
     return r;
   };
   Workspace ws;
-  ws.xc = static_cast<uint16_t*>(take((size_t)T * D * 2));
   ws.qn = static_cast<uint16_t*>(take((size_t)T * Hk * kDk * 2));
   ws.kn = static_cast<uint16_t*>(take((size_t)T * Hk * kDk * 2));
+  ws.vc = static_cast<uint16_t*>(take((size_t)T * Hv * kDv * 2));
   ws.beta = static_cast<uint16_t*>(take((size_t)T * Hv * 2));
   ws.lg = static_cast<float*>(take((size_t)T * Hv * 4));
   if (w) *w = ws;
@@ -62,37 +61,166 @@ __device__ __forceinline__ int seq_of(const int32_t* __restrict__ cu, int nseq, 
   return lo;
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// The sigmoid of the conv activations on the hardware exp2 and reciprocal
+// (v_exp_f32, v_rcp_f32; ~2 ulp instead of the ~1 ulp of expf and an IEEE
+// divide). Its result is rounded to bf16 next, so the two forms differ only
+// where the exact value lies within a few f32 ulp of a bf16 rounding
+// boundary, by one bf16 ulp.
+__device__ __forceinline__ float sigmoid_fast(float x) {
+  const float e = __builtin_amdgcn_exp2f(-fabsf(x) * 1.4426950408889634f);
+  const float y = __builtin_amdgcn_rcpf(1.0f + e);
+  return x < 0.0f ? 1.0f - y : y;
+}
+
 }  // namespace
 
-// 1. conv1d + silu (qwen3_5.rs:617-623): out[t,ch] = silu(sum_k padded[t+k,ch] w[ch,k])
-// with padded = [slot conv state (K-1 rows) | x of the sequence]; f32
-// accumulation, one rounding to bf16. grid (T, D/256), block 256.
-__global__ __launch_bounds__(256) void prefill_conv_kernel(
+// 1. Per (64-token tile, 128-channel head) of mixed_qkv; heads 0..Hk-1 are q,
+// Hk..2Hk-1 are k, the rest v (the channel order of the qkv projection):
+//   conv1d + silu (qwen3_5.rs:617-623): c[t,ch] = silu(sum_k padded[t+k,ch] w[ch,k])
+//     with padded = [slot conv state (K-1 rows) | x of the sequence]; f32
+//     accumulation, one rounding to bf16;
+//   q/k heads: rms-norm with the baked weights (qwen3_5.rs:627-633) -> qn, kn;
+//   v heads: c -> vc, and the gates of that head (compiled_ops.rs:68-94):
+//     beta = sigmoid(b), lg = log g = -exp(A_log) softplus(a + dt_bias).
+// The 64 + K-1 input rows of the tile are staged in LDS once (one HBM read per
+// element plus a 3-row halo); lane l of a 16-lane group owns channels 8l..8l+7
+// of one token. grid (2Hk+Hv, ceil(T/64)), block 256.
+template <int R>
+__global__ __launch_bounds__(256) void prefill_qkv_kernel(
     const uint16_t* __restrict__ conv, const int32_t* __restrict__ slot_ids,
-    const int32_t* __restrict__ cu, int nseq, int num_slots, int D,
+    const int32_t* __restrict__ cu, int nseq, int num_slots, int Hk, int T,
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ conv_w,
-    uint16_t* __restrict__ xc) {
-  const int t = blockIdx.x;
-  const int ch = blockIdx.y * 256 + threadIdx.x;
-  if (ch >= D) return;
-  const int s = seq_of(cu, nseq, t);
-  const int slot = slot_ids[s];
-  if ((unsigned)slot >= (unsigned)num_slots) return;  // flagged by the recurrence kernel
-  // seq_of gives cu[s] <= t for a well-formed cu_seqlens; the clamp keeps the
-  // conv-state row index in [0, K-1) for any input.
-  const int st = min(max(cu[s], 0), t);
-  const uint16_t* cs = conv + (size_t)slot * (kConvK - 1) * D;
-  const uint2 wv = *reinterpret_cast<const uint2*>(conv_w + (size_t)ch * kConvK);
-  const uint16_t wk[4] = {(uint16_t)(wv.x & 0xffffu), (uint16_t)(wv.x >> 16),
-                          (uint16_t)(wv.y & 0xffffu), (uint16_t)(wv.y >> 16)};
-  float acc = 0.0f;
-#pragma unroll
-  for (int k = 0; k < kConvK; ++k) {
-    const int u = t + k - (kConvK - 1);  // source token
-    const uint16_t p = u >= st ? x[(size_t)u * D + ch] : cs[(size_t)(u - st + kConvK - 1) * D + ch];
-    acc += bf2f(p) * bf2f(wk[k]);
+    const uint16_t* __restrict__ ab, const float* __restrict__ A_log,
+    const float* __restrict__ dt_bias, uint16_t* __restrict__ qn, uint16_t* __restrict__ kn,
+    uint16_t* __restrict__ vc, uint16_t* __restrict__ beta, float* __restrict__ lg) {
+  constexpr int KH = kConvK - 1;
+  __shared__ uint4 tile[kTT + KH][16];
+  __shared__ int tok_st[kTT];    // first token of the token's sequence (clamped <= t)
+  __shared__ int tok_slot[kTT];  // slot of that sequence, -1 if invalid
+  const int head = blockIdx.x, t0 = blockIdx.y * kTT;
+  const int Hv = Hk * R;
+  const int D = (2 * Hk + Hv) * kDk;
+  const int tid = threadIdx.x;
+  const size_t hcol = (size_t)head * kDk;
+  for (int e = tid; e < (kTT + KH) * 16; e += 256) {
+    const int r = e >> 4, c = e & 15, u = t0 - KH + r;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (u >= 0 && u < T)
+      v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + (size_t)u * D + hcol) + c);
+    tile[r][c] = make_uint4(v.x, v.y, v.z, v.w);
   }
-  xc[(size_t)t * D + ch] = f2bf(silu_bf16(rbf(acc)));
+  if (tid < kTT) {
+    const int t = t0 + tid;
+    int st = t, sl = -1;
+    if (t < T) {
+      const int s = seq_of(cu, nseq, t);
+      st = min(max(cu[s], 0), t);
+      sl = slot_ids[s];
+      if ((unsigned)sl >= (unsigned)num_slots) sl = -1;  // flagged by the chunk kernel
+    }
+    tok_st[tid] = st;
+    tok_slot[tid] = sl;
+  }
+  const int l = tid & 15;
+  // conv weights of channels 8l..8l+7: [8][K] bf16 = 4 x uint4
+  float wk[8][kConvK];
+  {
+    const uint4* wp = reinterpret_cast<const uint4*>(conv_w + (hcol + 8 * l) * kConvK);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint4 v = wp[q];
+      const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        wk[2 * q + h][0] = bf_lo(wd[2 * h]);
+        wk[2 * q + h][1] = bf_hi(wd[2 * h]);
+        wk[2 * q + h][2] = bf_lo(wd[2 * h + 1]);
+        wk[2 * q + h][3] = bf_hi(wd[2 * h + 1]);
+      }
+    }
+  }
+  __syncthreads();
+  const bool isq = head < Hk, isk = !isq && head < 2 * Hk;
+#pragma unroll
+  for (int it = 0; it < kTT / 16; ++it) {
+    const int i = (tid >> 4) + 16 * it, t = t0 + i;
+    const int st = tok_st[i];
+    uint32_t win[kConvK][4];  // taps t-K+1..t, channels 8l..8l+7 as bf16 pairs
+    if (t - KH >= st) {
+#pragma unroll
+      for (int k = 0; k < kConvK; ++k) {
+        const uint4 v = tile[i + k][l];
+        win[k][0] = v.x; win[k][1] = v.y; win[k][2] = v.z; win[k][3] = v.w;
+      }
+    } else {  // within K-1 tokens of the sequence start: taps before it come from the conv state
+      const int sl = tok_slot[i];
+#pragma unroll
+      for (int k = 0; k < kConvK; ++k) {
+        const int u = t + k - KH;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (u >= st)
+          v = tile[i + k][l];
+        else if (sl >= 0)  // conv state row u - st + K-1
+          v = *reinterpret_cast<const uint4*>(conv + ((size_t)sl * KH + (u - st + KH)) * D + hcol + 8 * l);
+        win[k][0] = v.x; win[k][1] = v.y; win[k][2] = v.z; win[k][3] = v.w;
+      }
+    }
+    // bf16 x bf16 products are exact in f32, so the fused multiply-adds equal
+    // the sequential f32 accumulation of the products.
+    float cv[8];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+      for (int k = 0; k < kConvK; ++k) {
+        a0 = fmaf(bf_lo(win[k][h]), wk[2 * h][k], a0);
+        a1 = fmaf(bf_hi(win[k][h]), wk[2 * h + 1][k], a1);
+      }
+      rbf2(a0, a1);
+      float s0 = sigmoid_fast(a0), s1 = sigmoid_fast(a1);
+      rbf2(s0, s1);
+      float c0 = a0 * s0, c1 = a1 * s1;
+      rbf2(c0, c1);
+      cv[2 * h] = c0;
+      cv[2 * h + 1] = c1;
+    }
+    uint32_t o[4];
+    uint16_t* dst;
+    if (isq || isk) {
+      float ss = 0.f;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) ss = fmaf(cv[c], cv[c], ss);
+#pragma unroll
+      for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, 64);
+      const float rn = 1.0f / sqrtf(ss / (float)kDk + kNormEps);
+      const float wn = isq ? kQNormW : kKNormW;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        float n0 = cv[2 * h] * rn, n1 = cv[2 * h + 1] * rn;
+        rbf2(n0, n1);
+        o[h] = f2bf2(wn * n0, wn * n1);
+      }
+      dst = (isq ? qn : kn) + ((size_t)t * Hk + (isq ? head : head - Hk)) * kDk;
+    } else {
+#pragma unroll
+      for (int h = 0; h < 4; ++h) o[h] = f2bf2(cv[2 * h], cv[2 * h + 1]);
+      dst = vc + ((size_t)t * Hv + (head - 2 * Hk)) * kDv;
+    }
+    if (t < T) reinterpret_cast<uint4*>(dst)[l] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+  if (!isq && !isk && tid < kTT && t0 + tid < T) {
+    const int t = t0 + tid, h = head - 2 * Hk;
+    const float braw = bf2f(ab[(size_t)t * 2 * Hv + h]);
+    const float araw = bf2f(ab[(size_t)t * 2 * Hv + Hv + h]);
+    beta[(size_t)t * Hv + h] = f2bf(sigmoid_f32(braw));
+    // log of the decay multiplier g = exp(lg) (compiled_ops.rs:36-43); the
+    // naive softplus overflows to inf for a+dt_bias >~ 88 (g = 0), clamped so
+    // that differences of cumulative sums stay finite (exp(-1e4) == 0 in f32)
+    const float sp = logf(expf(araw + dt_bias[h]) + 1.0f);
+    lg[(size_t)t * Hv + h] = fmaxf(-(expf(A_log[h]) * sp), -1.0e4f);
+  }
 }
 
 // 2. new conv state = last K-1 rows of padded (qwen3_5.rs:618-619).
@@ -121,43 +249,7 @@ __global__ __launch_bounds__(256) void prefill_conv_state_kernel(
   }
 }
 
-// 3. q/k rms-norm with the baked weights and the gates (beta, log decay), per
-// (token, hk).
-// grid (T, Hk), block 256: threads 0..127 q, 128..255 k.
-template <int R>
-__global__ __launch_bounds__(256) void prefill_prep_kernel(
-    int Hk, int D, const uint16_t* __restrict__ xc, const uint16_t* __restrict__ ab,
-    const float* __restrict__ A_log, const float* __restrict__ dt_bias,
-    uint16_t* __restrict__ qn, uint16_t* __restrict__ kn, uint16_t* __restrict__ beta,
-    float* __restrict__ lg) {
-  const int t = blockIdx.x, hk = blockIdx.y;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int Hv = Hk * R;
-  __shared__ float red[4];
-  const int isk = tid >> 7, d = tid & 127;
-  const float xv = bf2f(xc[(size_t)t * D + (size_t)isk * Hk * kDk + hk * kDk + d]);
-  const float ss = wave_sum(xv * xv);
-  if (lane == 0) red[wave] = ss;
-  __syncthreads();
-  const float sum = isk ? red[2] + red[3] : red[0] + red[1];
-  const float rn = 1.0f / sqrtf(sum / (float)kDk + kNormEps);
-  const float w = isk ? kKNormW : kQNormW;
-  uint16_t* dst = isk ? kn : qn;
-  dst[((size_t)t * Hk + hk) * kDk + d] = f2bf(w * rbf(xv * rn));
-  if (tid < R) {
-    const int h = hk * R + tid;
-    const float braw = bf2f(ab[(size_t)t * 2 * Hv + h]);
-    const float araw = bf2f(ab[(size_t)t * 2 * Hv + Hv + h]);
-    beta[(size_t)t * Hv + h] = f2bf(sigmoid_f32(braw));
-    // log of the decay multiplier g = exp(lg) (compiled_ops.rs:36-43); the
-    // naive softplus overflows to inf for a+dt_bias >~ 88 (g = 0), clamped so
-    // that differences of cumulative sums stay finite (exp(-1e4) == 0 in f32)
-    const float sp = logf(expf(araw + dt_bias[h]) + 1.0f);
-    lg[(size_t)t * Hv + h] = fmaxf(-(expf(A_log[h]) * sp), -1.0e4f);
-  }
-}
-
-// 4. Chunked (WY form) recurrence, one work-group of 512 threads (8 waves) per
+// 3. Chunked (WY form) recurrence, one work-group of 512 threads (8 waves) per
 // (sequence, value head), walking the sequence's chunks of kC = 64 tokens. With G the cumulative log decay inside a chunk and S
 // ([Dv, Dk]) the state at the chunk start:
 //   L_ij = beta_i (k_i.k_j) exp(G_i - G_j)   (j < i)
@@ -243,9 +335,9 @@ __device__ __forceinline__ void split4(const f32x4& x, s16x4& hi, s16x4& lo) {
 template <int R>
 __global__ __launch_bounds__(512) void prefill_chunk_kernel(
     float* __restrict__ state, const int32_t* __restrict__ slot_ids,
-    const int32_t* __restrict__ cu, int num_slots, int Hk, int D, int T,
+    const int32_t* __restrict__ cu, int num_slots, int Hk, int T,
     const uint16_t* __restrict__ qn, const uint16_t* __restrict__ kn,
-    const uint16_t* __restrict__ xc, const float* __restrict__ lgv,
+    const uint16_t* __restrict__ vc, const float* __restrict__ lgv,
     const uint16_t* __restrict__ betav, uint16_t* __restrict__ y, uint32_t* __restrict__ status) {
   constexpr int NT = 512;
   __shared__ ChunkSmem sm;
@@ -271,7 +363,6 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
     acc[a] = *reinterpret_cast<const f32x4*>(gstate + 16 * a);
 
   // chunk inputs in registers (prefetched one chunk ahead)
-  const size_t vcol = 2 * (size_t)Hk * kDk + (size_t)hv * kDv;
   uint4 kv[2], qv[2], vv[2];
   float pb = 0.f, pl = 0.f;
   auto load_inputs = [&](int c0) {
@@ -286,7 +377,7 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
         const size_t off = ((size_t)(c0 + i) * Hk + hk) * kDk + c;
         kv[u] = *reinterpret_cast<const uint4*>(kn + off);
         qv[u] = *reinterpret_cast<const uint4*>(qn + off);
-        vv[u] = *reinterpret_cast<const uint4*>(xc + (size_t)(c0 + i) * D + vcol + c);
+        vv[u] = *reinterpret_cast<const uint4*>(vc + ((size_t)(c0 + i) * Hv + hv) * kDv + c);
       }
     }
     pb = 0.f;
@@ -505,9 +596,10 @@ static hipError_t launch_prefill_r(const PrefillArgs& a) {
   Workspace ws;
   carve(a.workspace, R, a.Hk, a.total_tokens, &ws);
   if (a.total_tokens > 0) {
-    hipLaunchKernelGGL(prefill_conv_kernel, dim3(a.total_tokens, (D + 255) / 256), dim3(256), 0,
-                       a.stream, a.conv, a.slot_ids, a.cu_seqlens, a.nseq, a.num_slots, D,
-                       a.mixed, a.conv_w, ws.xc);
+    hipLaunchKernelGGL(prefill_qkv_kernel<R>, dim3(2 * a.Hk + Hv, (a.total_tokens + kTT - 1) / kTT),
+                       dim3(256), 0, a.stream, a.conv, a.slot_ids, a.cu_seqlens, a.nseq,
+                       a.num_slots, a.Hk, a.total_tokens, a.mixed, a.conv_w, a.ab, a.A_log,
+                       a.dt_bias, ws.qn, ws.kn, ws.vc, ws.beta, ws.lg);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -516,16 +608,9 @@ static hipError_t launch_prefill_r(const PrefillArgs& a) {
                      a.mixed);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (a.total_tokens > 0) {
-    hipLaunchKernelGGL(prefill_prep_kernel<R>, dim3(a.total_tokens, a.Hk), dim3(256), 0,
-                       a.stream, a.Hk, D, ws.xc, a.ab, a.A_log, a.dt_bias, ws.qn, ws.kn,
-                       ws.beta, ws.lg);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-  }
   hipLaunchKernelGGL(prefill_chunk_kernel<R>, dim3(Hv, a.nseq), dim3(512), 0,
-                     a.stream, a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk, D,
-                     a.total_tokens, ws.qn, ws.kn, ws.xc, ws.lg, ws.beta, a.y, a.status);
+                     a.stream, a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk,
+                     a.total_tokens, ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, a.y, a.status);
   return hipGetLastError();
 }
 
