@@ -344,7 +344,7 @@ def main(argv=None):
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": traffic,
-            "kernel": "gdn_decode (decode_fused_kernel<2>)",
+            "kernel": "gdn_decode (decode_kernel<2>)",
             "kernel_avg_us": round(avg_ms * 1e3, 2),
             "kernel_timing": "HIP events around each step's back-to-back launches / launches",
             "algorithmic_bytes_per_launch": launch_bytes,

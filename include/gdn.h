@@ -31,7 +31,11 @@
  *   - Slot ids within one call must be distinct: two work-groups updating the
  *     same slot in one launch race. gdn_slots_validate() checks this on demand.
  *   - One pool is not reentrant: calls that touch the same slots must be
- *     ordered on one stream by the caller.
+ *     ordered on one stream by the caller. gdn_prefill_varlen uses a device
+ *     workspace held by the pool, so its calls on a pool must be ordered on
+ *     one stream; a call with a new maximum total_tokens synchronizes its
+ *     stream and reallocates it, later calls at or below that size allocate
+ *     nothing. gdn_decode allocates nothing.
  *   - Model shape limits: head_k_dim == head_v_dim == 128, conv_kernel == 4,
  *     num_v_heads / num_k_heads in {1, 2, 4}.
  *
@@ -158,7 +162,7 @@ gdn_status gdn_recurrent(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
  *   baked weights bf16(1/Dk), bf16(1/sqrt(Dk)), eps 1e-6 -> beta = sigmoid(b),
  *   g = exp(-exp(A_log) * log(exp(a+dt_bias)+1)) -> recurrence -> y.
  * The rolling conv state and the recurrent state of each slot are updated in
- * place. mixed_qkv [B,D], ab [B,2Hv], y [B,Hv,Dv]. */
+ * place. mixed_qkv [B,D], ab [B,2Hv], y [B,Hv,Dv]; B <= num_slots. */
 gdn_status gdn_decode(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
                       int32_t B, const uint16_t* mixed_qkv, const uint16_t* ab,
                       const float* A_log, const float* dt_bias,

@@ -329,6 +329,26 @@ gdn_status gdn_recurrent(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
   return GDN_OK;
 }
 
+// Grows the pool's prefill workspace to at least `need` bytes. Growing waits
+// for the stream, so work still reading the old buffer has finished.
+static gdn_status ensure_workspace(gdn_pool* pool, size_t need, void* stream, const char* what) {
+  if (need <= pool->workspace_bytes) return GDN_OK;
+  if (pool->workspace) {
+    hipError_t e = hipStreamSynchronize(as_stream(stream));
+    if (e != hipSuccess) return hip_fail(e, "workspace grow sync");
+    (void)hipFree(pool->workspace);
+    pool->workspace = nullptr;
+    pool->workspace_bytes = 0;
+  }
+  if (hipMalloc(&pool->workspace, need) != hipSuccess) {
+    (void)hipGetLastError();
+    pool->workspace = nullptr;
+    return fail(GDN_ERR_OOM, "%s workspace of %zu bytes", what, need);
+  }
+  pool->workspace_bytes = need;
+  return GDN_OK;
+}
+
 gdn_status gdn_decode(gdn_pool* pool, int32_t layer, const int32_t* slot_ids, int32_t B,
                       const uint16_t* mixed_qkv, const uint16_t* ab, const float* A_log,
                       const float* dt_bias, const uint16_t* conv_w, uint16_t* y, void* stream) {
@@ -337,6 +357,9 @@ gdn_status gdn_decode(gdn_pool* pool, int32_t layer, const int32_t* slot_ids, in
   if (B < 0) return fail(GDN_ERR_INVALID, "B = %d < 0", B);
   if (B == 0) return GDN_OK;
   if (B > 65535) return fail(GDN_ERR_INVALID, "B = %d > 65535", B);
+  if (B > pool->d.num_slots)
+    return fail(GDN_ERR_INVALID, "B = %d > num_slots = %d (slot ids must be distinct)", B,
+                pool->d.num_slots);
   if (!slot_ids || !mixed_qkv || !ab || !A_log || !dt_bias || !conv_w || !y)
     return fail(GDN_ERR_INVALID, "gdn_decode: NULL tensor pointer");
   if (reinterpret_cast<uintptr_t>(conv_w) % 8 != 0)
@@ -381,23 +404,9 @@ gdn_status gdn_prefill_varlen(gdn_pool* pool, int32_t layer, const int32_t* slot
   if (reinterpret_cast<uintptr_t>(conv_w) % 8 != 0)
     return fail(GDN_ERR_INVALID, "gdn_prefill_varlen: conv_w must be 8-byte aligned");
   DeviceGuard guard(pool->d.device);
-  const size_t need = gdn::prefill_workspace_bytes(pool->R, pool->d.num_k_heads, total_tokens);
-  if (need > pool->workspace_bytes) {
-    hipError_t e;
-    if (pool->workspace) {
-      if ((e = hipStreamSynchronize(as_stream(stream))) != hipSuccess)
-        return hip_fail(e, "workspace grow sync");
-      (void)hipFree(pool->workspace);
-      pool->workspace = nullptr;
-      pool->workspace_bytes = 0;
-    }
-    if (hipMalloc(&pool->workspace, need) != hipSuccess) {
-      (void)hipGetLastError();
-      pool->workspace = nullptr;
-      return fail(GDN_ERR_OOM, "prefill workspace of %zu bytes", need);
-    }
-    pool->workspace_bytes = need;
-  }
+  st = ensure_workspace(pool, gdn::prefill_workspace_bytes(pool->R, pool->d.num_k_heads, total_tokens),
+                        stream, "prefill");
+  if (st) return st;
   gdn::PrefillArgs a{};
   a.R = pool->R;
   a.Hk = pool->d.num_k_heads;

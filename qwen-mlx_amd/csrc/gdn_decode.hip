@@ -2,18 +2,19 @@
 //
 // Work decomposition: one work-group per (sequence, key head hk). The group
 // owns the R = Hv/Hk value heads hv = hk*R + r that share hk's q/k (the GQA
-// map hk = hv / (Hv/Hk) of metal_gdn.rs:14), so the fused kernel computes the
-// q/k conv channels once and is the only writer of every conv channel it
-// reads: no two work-groups touch the same conv-state bytes of a slot.
+// map hk = hv / (Hv/Hk) of metal_gdn.rs:14), so the fused decode kernel
+// computes the q/k conv channels once and is the only writer of every conv
+// channel it reads: no two work-groups touch the same conv-state bytes of a
+// slot.
 //
-// Each 128x128 f32 tile (one slot, one value head) is held in VGPRs by a
-// "tile team" of 256 threads (4 waves), 64 floats per thread:
+// The recurrence kernel (prepared q/k/v, T tokens) holds each 128x128 f32
+// tile in a "tile team" of 256 threads, 64 floats per thread:
 //   lt = thread index in the team, grp = lt >> 3 (0..31), sub = lt & 7;
 //   rows  dv = grp + 32*i            (i = 0..3)
 //   cols  dk = 4*(sub + 8*j) + e     (j = 0..3, e = 0..3)
-// A load instruction of one wave reads 8 rows x 128 contiguous bytes, so every
-// fetched cache line is fully used; the dk-reductions of a row stay inside 8
-// aligned lanes and are done with three DPP adds (sum8).
+// and reduces over dk inside 8 aligned lanes (three DPP adds, sum8). The
+// fused decode kernel uses a row layout with 16 lanes per row instead (see
+// decode_kernel).
 //
 // Arithmetic (metal_gdn.rs:37-62): s *= g; kv = s.k; d = (v - kv)*beta;
 // s += k d; y = s.q. The readout is taken from the decayed state in the same
@@ -50,6 +51,12 @@ __device__ __forceinline__ void tile_store(const TileRegs& t, float* __restrict_
 
 __device__ __forceinline__ float dot4(const v4f& a, const v4f& b) {
   return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+}
+
+// Sum over the 16 lanes of a DPP row (every lane receives the sum).
+__device__ __forceinline__ float sum16(float v) {
+  v = sum8(v);
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
 }
 
 // One token on the register tile. kl/ql: k and q of the token in LDS (Dk
@@ -95,150 +102,6 @@ __device__ __forceinline__ void tile_step(TileRegs& t, const float* kl, const fl
 constexpr float kQNormW = 0.0078125f;
 constexpr float kKNormW = 0.08837890625f;
 constexpr float kNormEps = 1e-6f;
-
-// -------------------------------------------------------------------------
-// Fused S=1 decode: conv update + silu + split + q/k rms-norm + gates +
-// recurrence. grid (Hk, B), block 256*R.
-//
-// Load order: the small conv/gate inputs first, then the 64 KiB state tile.
-// Waiting for the conv inputs leaves the state loads in flight through the
-// conv and norm phases, whose barriers order LDS only (lds_barrier). At most
-// 128 VGPRs (4 waves per SIMD) lets two 512-thread groups share a CU, so one
-// group's state stores overlap the other's loads.
-template <int R>
-__global__ __launch_bounds__(256 * R) __attribute__((amdgpu_waves_per_eu(4))) void
-decode_fused_kernel(float* __restrict__ state, uint16_t* __restrict__ conv,
-                    const int32_t* __restrict__ slot_ids, int num_slots, int Hk,
-                    const uint16_t* __restrict__ mixed, const uint16_t* __restrict__ ab,
-                    const float* __restrict__ A_log, const float* __restrict__ dt_bias,
-                    const uint16_t* __restrict__ conv_w, uint16_t* __restrict__ y,
-                    uint32_t* __restrict__ status) {
-  constexpr int NT = 256 * R;
-  constexpr int NCH = (2 + R) * kDk;  // q, k of hk + v of R value heads
-  constexpr int CPT = (NCH + NT - 1) / NT;
-  const int hk = blockIdx.x, b = blockIdx.y;
-  const int Hv = Hk * R;
-  const int D = 2 * Hk * kDk + Hv * kDv;
-  const int tid = threadIdx.x;
-  const int slot = slot_ids[b];
-  if ((unsigned)slot >= (unsigned)num_slots) {
-    if (tid == 0) flag_status(status, GDN_FLAG_BAD_SLOT);
-    return;
-  }
-
-  __shared__ float xs[NCH];
-  __shared__ __align__(16) float qn[kDk];
-  __shared__ __align__(16) float kn[kDk];
-  __shared__ float red[8];
-  __shared__ float gate_g[R], gate_beta[R];
-  __shared__ uint16_t win_next[kConvK - 1][NCH];  // shifted conv window, stored at the end
-
-  // global conv channel of the group's local channel c (q | k | v blocks)
-  auto chan = [&](int c) {
-    return c < kDk ? hk * kDk + c
-                   : (c < 2 * kDk ? Hk * kDk + hk * kDk + (c - kDk)
-                                  : 2 * Hk * kDk + hk * R * kDv + (c - 2 * kDk));
-  };
-
-  // 1. conv window, weights and gate inputs of the channels this thread owns
-  uint16_t* cs = conv + (size_t)slot * (kConvK - 1) * D;
-  uint16_t cwin[CPT][kConvK];
-  uint2 cwt[CPT];
-#pragma unroll
-  for (int u = 0; u < CPT; ++u) {
-    const int c = tid + u * NT;
-    const int gc = chan(c < NCH ? c : 0);
-    cwt[u] = *reinterpret_cast<const uint2*>(conv_w + (size_t)gc * kConvK);
-    cwin[u][0] = cs[gc];
-    cwin[u][1] = cs[D + gc];
-    cwin[u][2] = cs[2 * D + gc];
-    cwin[u][3] = mixed[(size_t)b * D + gc];
-  }
-  float braw = 0.f, araw = 0.f, alog = 0.f, dtb = 0.f;
-  if (tid < R) {
-    const int h = hk * R + tid;
-    braw = bf2f(ab[(size_t)b * 2 * Hv + h]);
-    araw = bf2f(ab[(size_t)b * 2 * Hv + Hv + h]);
-    alog = A_log[h];
-    dtb = dt_bias[h];
-  }
-
-  // 2. the state tile of value head hv (stays in flight until tile_step)
-  const int r = tid >> 8;
-  const int lt = tid & 255, grp = lt >> 3, sub = lt & 7;
-  const int hv = hk * R + r;
-  float* tile = state + ((size_t)slot * Hv + hv) * kTileElems;
-  TileRegs t;
-  tile_load(t, tile, grp, sub);
-
-  // 3. conv (qwen3_5.rs:602-610): bf16 products, f32 sum, silu. The shifted
-  // window goes to LDS and is stored at the end of the kernel: a store issued
-  // here would sit behind the state loads in the in-order vmcnt counter and
-  // force waits on them.
-#pragma unroll
-  for (int u = 0; u < CPT; ++u) {
-    const int c = tid + u * NT;
-    if (c < NCH) {
-      float acc = rbf(bf2f(cwin[u][0]) * bf2f((uint16_t)(cwt[u].x & 0xffffu)));
-      acc += rbf(bf2f(cwin[u][1]) * bf2f((uint16_t)(cwt[u].x >> 16)));
-      acc += rbf(bf2f(cwin[u][2]) * bf2f((uint16_t)(cwt[u].y & 0xffffu)));
-      acc += rbf(bf2f(cwin[u][3]) * bf2f((uint16_t)(cwt[u].y >> 16)));
-      xs[c] = silu_bf16(rbf(acc));
-#pragma unroll
-      for (int k = 0; k < kConvK - 1; ++k) win_next[k][c] = cwin[u][k + 1];
-    }
-  }
-  // gates (compiled_ops.rs:30-43) on ab = [b | a]
-  if (tid < R) {
-    gate_beta[tid] = rbf(sigmoid_f32(braw));
-    const float sp = logf(expf(araw + dtb) + 1.0f);
-    gate_g[tid] = expf(-(expf(alog) * sp));
-  }
-  lds_barrier();
-
-  // 4. q/k rms-norm (qwen3_5.rs:638-639): waves 0-1 hold q, waves 2-3 hold k.
-  const int wave = tid >> 6, lane = tid & 63;
-  if (tid < 2 * kDk) {
-    const float v = xs[tid];
-    const float ss = wave_sum(v * v);
-    if (lane == 0) red[wave] = ss;
-  }
-  lds_barrier();
-  if (tid < kDk) {
-    const float rq = 1.0f / sqrtf((red[0] + red[1]) / (float)kDk + kNormEps);
-    const float rk = 1.0f / sqrtf((red[2] + red[3]) / (float)kDk + kNormEps);
-    const float qv = rbf(kQNormW * rbf(xs[tid] * rq));
-    const float kv = rbf(kKNormW * rbf(xs[kDk + tid] * rk));
-    qn[tid] = qv;
-    kn[tid] = kv;
-    const float p = wave_sum(qv * kv);
-    if (lane == 0) red[4 + wave] = p;
-  }
-  lds_barrier();
-  const float kq = red[4] + red[5];
-
-  // 5. recurrence on the tile
-  float vrow[4], yrow[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) vrow[i] = xs[2 * kDk + r * kDv + grp + 32 * i];
-  tile_step(t, kn, qn, sub, vrow, gate_g[r], gate_beta[r], kq, yrow);
-  tile_store(t, tile, grp, sub);
-  uint16_t* yo = y + ((size_t)b * Hv + hv) * kDv;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    if (sub == i) yo[grp + 32 * i] = f2bf(yrow[i]);
-  // 6. rolling conv state: window [s0 s1 s2 x] -> [s1 s2 x] in place (this
-  // group is the only one touching these channels of the slot)
-#pragma unroll
-  for (int u = 0; u < CPT; ++u) {
-    const int c = tid + u * NT;
-    if (c < NCH) {
-      const int gc = chan(c);
-#pragma unroll
-      for (int k = 0; k < kConvK - 1; ++k) cs[(size_t)k * D + gc] = win_next[k][c];
-    }
-  }
-}
 
 // -------------------------------------------------------------------------
 // Recurrence on prepared q/k/v/g/beta for T tokens per sequence (the
@@ -303,14 +166,139 @@ __global__ __launch_bounds__(256 * R) void recurrent_kernel(
   tile_store(t, tile, grp, sub);
 }
 
+// -------------------------------------------------------------------------
+// Fused S=1 decode (conv update + silu + split + q/k rms-norm + gates +
+// recurrence), one launch. grid (Hk, B), block 256*R.
+//
+// The group of (b, hk) owns the q/k conv channels of hk and the v channels of
+// its R value heads, so it is the only reader and writer of those conv-state
+// bytes of the slot. Waves 4r..4r+3 hold the state tile of value head
+// hv = hk*R + r in registers, 16 float4 per thread: lanes 16q..16q+15 of wave
+// 4r+w own rows 32w + 4j + q (j = 0..7); lane l holds columns 4l..4l+3 and
+// 64+4l..64+4l+3 of each. A load instruction of a wave thus reads four rows x
+// 256 contiguous bytes, and every dk-reduction is a 16-lane DPP sum.
+//
+// Load order: the conv window, weights and gate inputs first, then the state
+// rows. Waiting for the conv inputs then leaves the state loads in flight
+// (vmcnt counts in issue order) through the conv, gate and norm phases, whose
+// barriers order LDS only. Results used by only some lanes are computed by
+// all of them (or written to LDS by all of them): a value consumed only
+// inside a divergent branch drags its loads, and their wait, into the branch
+// behind the state loads.
+__device__ __forceinline__ float conv1(uint16_t c0, uint16_t c1, uint16_t c2, uint16_t x, uint2 w) {
+  float acc = rbf(bf2f(c0) * bf_lo(w.x));
+  acc += rbf(bf2f(c1) * bf_hi(w.x));
+  acc += rbf(bf2f(c2) * bf_lo(w.y));
+  acc += rbf(bf2f(x) * bf_hi(w.y));
+  return silu_bf16(rbf(acc));
+}
+
+template <int R>
+__global__ __launch_bounds__(256 * R) void decode_kernel(
+    float* __restrict__ state, uint16_t* __restrict__ conv, const int32_t* __restrict__ slot_ids,
+    int num_slots, int Hk, const uint16_t* __restrict__ mixed, const uint16_t* __restrict__ ab,
+    const float* __restrict__ A_log, const float* __restrict__ dt_bias,
+    const uint16_t* __restrict__ conv_w, uint16_t* __restrict__ y, uint32_t* __restrict__ status) {
+  constexpr int NT = 256 * R;
+  constexpr int NCH = (2 + R) * kDk;
+  constexpr int CPT = (NCH + NT - 1) / NT;
+  const int hk = blockIdx.x, b = blockIdx.y;
+  const int Hv = Hk * R;
+  const int D = 2 * Hk * kDk + Hv * kDv;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l = lane & 15;
+  const int slot = slot_ids[b];
+  if ((unsigned)slot >= (unsigned)num_slots) {
+    if (tid == 0) flag_status(status, GDN_FLAG_BAD_SLOT);
+    return;
+  }
+  __shared__ float xs[CPT * NT];
+  __shared__ __align__(16) float qk[2][kDk];
+  __shared__ float red[8];
+  __shared__ float gsh[R][2];
+  auto chan = [&](int c) {
+    return c < kDk ? hk * kDk + c
+                   : (c < 2 * kDk ? Hk * kDk + hk * kDk + (c - kDk)
+                                  : 2 * Hk * kDk + hk * R * kDv + (c - 2 * kDk));
+  };
+  uint16_t* cs = conv + (size_t)slot * (kConvK - 1) * D;
+  uint2 cw[CPT];
+  uint16_t c0[CPT], c1[CPT], c2[CPT], cx[CPT];
+#pragma unroll
+  for (int u = 0; u < CPT; ++u) {
+    const int c = tid + u * NT;
+    const int gc = chan(c < NCH ? c : 0);
+    cw[u] = *reinterpret_cast<const uint2*>(conv_w + (size_t)gc * kConvK);
+    c0[u] = cs[gc]; c1[u] = cs[D + gc]; c2[u] = cs[2 * D + gc];
+    cx[u] = mixed[(size_t)b * D + gc];
+  }
+  const int gr = tid & (R - 1), gh = hk * R + gr;
+  const float alog = A_log[gh], dtb = dt_bias[gh];
+  const uint16_t braw = ab[(size_t)b * 2 * Hv + gh], araw = ab[(size_t)b * 2 * Hv + Hv + gh];
+  __builtin_amdgcn_sched_barrier(0);
+  const int r = wave >> 2, wt = wave & 3;
+  const int hv = hk * R + r;
+  float* tile = state + ((size_t)slot * Hv + hv) * kTileElems;
+  float* base = tile + (size_t)(32 * wt + (lane >> 4)) * kDk;
+  v4f s[8][2];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    s[j][0] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(base + 4 * j * kDk + 4 * l));
+    s[j][1] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(base + 4 * j * kDk + 64 + 4 * l));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < CPT; ++u) xs[tid + u * NT] = conv1(c0[u], c1[u], c2[u], cx[u], cw[u]);
+  {
+    const float sp = logf(expf(bf2f(araw) + dtb) + 1.0f);
+    gsh[gr][0] = expf(-(expf(alog) * sp));
+    gsh[gr][1] = rbf(sigmoid_f32(bf2f(braw)));
+  }
+  lds_barrier();
+  if (tid < 2 * kDk) {
+    const float v = xs[tid];
+    const float ss = wave_sum(v * v);
+    if (lane == 0) red[wave] = ss;
+  }
+  lds_barrier();
+  if (tid < 2 * kDk) {
+    const float rn = 1.0f / sqrtf((wave < 2 ? red[0] + red[1] : red[2] + red[3]) / (float)kDk + kNormEps);
+    qk[tid >> 7][tid & (kDk - 1)] = rbf((tid < kDk ? kQNormW : kKNormW) * rbf(xs[tid] * rn));
+  }
+  lds_barrier();
+  const v4f qa = *reinterpret_cast<const v4f*>(&qk[0][4 * l]);
+  const v4f qb = *reinterpret_cast<const v4f*>(&qk[0][64 + 4 * l]);
+  const v4f ka = *reinterpret_cast<const v4f*>(&qk[1][4 * l]);
+  const v4f kb = *reinterpret_cast<const v4f*>(&qk[1][64 + 4 * l]);
+  const float kq = sum16(dot4(ka, qa) + dot4(kb, qb));
+  const float g = gsh[r][0], beta = gsh[r][1];
+  const float* vrow = &xs[2 * kDk + r * kDv + 32 * wt + (lane >> 4)];
+  uint16_t* yo = y + ((size_t)b * Hv + hv) * kDv + 32 * wt + (lane >> 4);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const v4f a0 = s[j][0] * g, a1 = s[j][1] * g;
+    const float kd = sum16(dot4(a0, ka) + dot4(a1, kb));
+    const float qd = sum16(dot4(a0, qa) + dot4(a1, qb));
+    const float d = (vrow[4 * j] - kd) * beta;
+    __builtin_nontemporal_store(a0 + ka * d, reinterpret_cast<v4f*>(base + 4 * j * kDk + 4 * l));
+    __builtin_nontemporal_store(a1 + kb * d, reinterpret_cast<v4f*>(base + 4 * j * kDk + 64 + 4 * l));
+    if (l == 0) yo[4 * j] = f2bf(qd + d * kq);
+  }
+#pragma unroll
+  for (int u = 0; u < CPT; ++u) {
+    const int c = tid + u * NT;
+    if (c < NCH) {
+      const int gc = chan(c);
+      cs[gc] = c1[u]; cs[D + gc] = c2[u]; cs[2 * D + gc] = cx[u];
+    }
+  }
+}
 // ------------------------------------------------------------ launchers --
 
 template <int R>
 static hipError_t launch_decode_r(const DecodeArgs& a) {
-  dim3 grid(a.Hk, a.B);
-  hipLaunchKernelGGL(decode_fused_kernel<R>, grid, dim3(256 * R), 0, a.stream, a.state, a.conv,
-                     a.slot_ids, a.num_slots, a.Hk, a.mixed, a.ab, a.A_log, a.dt_bias, a.conv_w,
-                     a.y, a.status);
+  hipLaunchKernelGGL(decode_kernel<R>, dim3(a.Hk, a.B), dim3(256 * R), 0, a.stream, a.state,
+                     a.conv, a.slot_ids, a.num_slots, a.Hk, a.mixed, a.ab, a.A_log, a.dt_bias,
+                     a.conv_w, a.y, a.status);
   return hipGetLastError();
 }
 
