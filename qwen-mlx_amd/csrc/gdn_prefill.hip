@@ -265,13 +265,17 @@ __global__ __launch_bounds__(256) void prefill_conv_state_kernel(
 // the wave's own 16 state rows (dv block w), so a chunk needs three
 // work-group barriers. The triangular solve works on V'
 // directly, 16-token blocks: V'_I = D_I (R_I - sum_{j<I} L_Ij V'_j) with
-// D_I = (I + L_II)^-1, on v_mfma_f32_16x16x16_bf16, whose accumulator layout
-// is its B-operand layout, so V' blocks feed the next products without data
-// movement. K K^T and Q K^T use v_mfma_f32_16x16x32_bf16. k and q are bf16
-// (exact operands); f32 operands on the state path (S, L, D, R, V') are split
-// into bf16 hi + lo parts (~16 mantissa bits). The state lives in MFMA
-// accumulators (S^T tiles) across chunks; split into hi/lo they are directly
-// the B operands of K S^T and Q S^T. The next chunk's inputs are loaded into
+// D_I = (I + L_II)^-1. A 16x16 MFMA accumulator holds row 4*(l/16) + r,
+// column l%16 of its tile in register r of lane l, which is the B-operand
+// layout of a 16-deep product: V' blocks and state tiles feed the next
+// products without data movement. k and q are bf16 (exact operands); f32
+// operands on the state path (S, L, D, R, V') are split into bf16 hi + lo
+// parts (~16 mantissa bits). A product with a split operand, X.Bh + X.Bl, is
+// one v_mfma_f32_16x16x32_bf16 whose 32-deep k axis holds, in each lane
+// group's 8 slots, 4 k of the hi part then the same 4 k of the lo part, with
+// the A fragment repeated (cat): the accumulator-layout registers are the B
+// operand as they are. The state lives in MFMA accumulators (S^T tiles)
+// across chunks. The next chunk's inputs are loaded into
 // registers while the current chunk computes. Padded rows of a
 // partial chunk have k = q = v = beta = 0 and log decay 0, so they change
 // nothing.
@@ -296,22 +300,19 @@ struct ChunkSmem {
   float Ld[4][16][17];       // diagonal 16x16 blocks of L (f32)
   uint16_t Dh[4][16][kLdD];  // D_I = (I + L_II)^-1, hi
   uint16_t Dl[4][16][kLdD];  // lo
-  float beta[kC], G[kC], eG[kC], dec_end[kC];
+  float beta[kC], G[kC], eG[kC], dec_end[kC];  // G: cumulative log2 decay
 };
 
 __device__ __forceinline__ f32x4 mfma32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ f32x4 mfma16(s16x4 a, s16x4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
-}
 
 // Operand fragments whose k runs contiguous in memory; they serve as A
 // operands (rows = output rows) and as B operands (rows = output columns).
-//   16x16x32: lane l takes row r0 + l%16, k = k0 + 8*(l/16) .. +7
-//   16x16x16: lane l takes row r0 + l%16, k = k0 + 4*(l/16) .. +3
-// A 16x16 accumulator tile holds row 4*(l/16) + r, column l%16 in register r,
-// which is exactly a 16x16x16 B operand.
+//   frag32: lane l takes row r0 + l%16, k = k0 + 8*(l/16) .. +7
+//   frag16: lane l takes row r0 + l%16, k = k0 + 4*(l/16) .. +3
+// A 16x16 accumulator tile holds row 4*(l/16) + r, column l%16 in register r:
+// the frag16 layout of its transpose, i.e. a B operand with k = row.
 __device__ __forceinline__ bf16x8 frag32(const uint16_t* base, int ld, int r0, int k0, int lane) {
   return *reinterpret_cast<const bf16x8*>(base + (r0 + (lane & 15)) * ld + k0 + (lane >> 4) * 8);
 }
@@ -320,6 +321,26 @@ __device__ __forceinline__ s16x4 frag16(const uint16_t* base, int ld, int r0, in
 }
 
 __device__ __forceinline__ short bfbits(float x) { return (short)f2bf(x); }
+
+// Two 4-element fragments as one 8-element MFMA operand. Every product of
+// the kernel is a v_mfma_f32_16x16x32_bf16, a lone 16-deep term padded with
+// zeros: accumulation chains that mixed it with v_mfma_f32_16x16x16_bf16
+// (the result of one feeding the accumulator of the other) gave wrong results
+// in testing, so no accumulator is ever shared between the two opcodes.
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+constexpr s16x4 kZero4 = {0, 0, 0, 0};
+__device__ __forceinline__ bf16x8 cat(s16x4 a, s16x4 b) {
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// K^T is stored with its token column XOR-swizzled by 8 * ((dk >> 3) & 7):
+// the transposing 2-byte stores of one wave (16 dk rows 8 apart) then spread
+// over the LDS banks, and a 4-token group stays contiguous and 8-byte aligned.
+__device__ __forceinline__ int kt_col(int dk, int tok) { return tok ^ (((dk >> 3) & 7) << 3); }
+__device__ __forceinline__ s16x4 frag16_kt(const uint16_t (*KT)[kC + 8], int r0, int k0, int lane) {
+  const int row = r0 + (lane & 15);
+  return *reinterpret_cast<const s16x4*>(&KT[row][kt_col(row, k0 + (lane >> 4) * 4)]);
+}
 
 // f32 tile -> bf16 hi + lo (hi + lo carries ~16 mantissa bits of x)
 __device__ __forceinline__ void split4(const f32x4& x, s16x4& hi, s16x4& lo) {
@@ -403,10 +424,10 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
       *reinterpret_cast<uint4*>(&sm.V[i][c]) = vv[u];
       const uint16_t* kb = reinterpret_cast<const uint16_t*>(&kv[u]);
 #pragma unroll
-      for (int x = 0; x < 8; ++x) sm.KT[c + x][i] = kb[x];
+      for (int x = 0; x < 8; ++x) sm.KT[c + x][kt_col(c + x, i)] = kb[x];
     }
-    if (w == 0) {  // inclusive prefix sum of the log decay
-      float gsum = pl;
+    if (w == 0) {  // inclusive prefix sum of the log decay, in log2 units
+      float gsum = pl * 1.4426950408889634f;
 #pragma unroll
       for (int off = 1; off < 64; off <<= 1) {
         const float t = __shfl_up(gsum, off, 64);
@@ -415,8 +436,8 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
       const float gC = __shfl(gsum, 63, 64);
       sm.beta[lane0] = pb;
       sm.G[lane0] = gsum;
-      sm.eG[lane0] = expf(gsum);
-      sm.dec_end[lane0] = expf(gC - gsum);
+      sm.eG[lane0] = __builtin_amdgcn_exp2f(gsum);
+      sm.dec_end[lane0] = __builtin_amdgcn_exp2f(gC - gsum);
     }
   };
 
@@ -451,7 +472,7 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int i = 16 * I + 4 * lq + r, j = 16 * J + lc;
-          const float d = expf(fminf(sm.G[i] - sm.G[j], 0.f));
+          const float d = __builtin_amdgcn_exp2f(fminf(sm.G[i] - sm.G[j], 0.f));
           if (isq) {
             sm.P[i][j] = f2bf(j <= i ? c[r] * d : 0.f);
           } else {
@@ -497,14 +518,13 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
       asm volatile("" ::: "memory");  // bound live ranges: one dk block at a time
       s16x4 sh, sl;
       split4(acc[a], sh, sl);
+      const bf16x8 bs = cat(sh, sl);
 #pragma unroll
       for (int I = 0; I < 4; ++I) {
         const s16x4 ak = frag16(&sm.K[0][0], kLdK, 16 * I, 16 * a, lane);
         const s16x4 aq = frag16(&sm.Q[0][0], kLdK, 16 * I, 16 * a, lane);
-        yk[I] = mfma16(ak, sh, yk[I]);
-        yk[I] = mfma16(ak, sl, yk[I]);
-        zq[I] = mfma16(aq, sh, zq[I]);
-        zq[I] = mfma16(aq, sl, zq[I]);
+        yk[I] = mfma32(cat(ak, ak), bs, yk[I]);
+        zq[I] = mfma32(cat(aq, aq), bs, zq[I]);
       }
     }
     __syncthreads();
@@ -524,18 +544,16 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
         if (j >= I) continue;
         const s16x4 lh = frag16(&sm.NLh[0][0], kLdT, 16 * I, 16 * j, lane);
         const s16x4 ll = frag16(&sm.NLl[0][0], kLdT, 16 * I, 16 * j, lane);
-        x = mfma16(lh, vph[j], x);
-        x = mfma16(lh, vpl[j], x);
-        x = mfma16(ll, vph[j], x);
+        x = mfma32(cat(lh, ll), cat(vph[j], vph[j]), x);  // lh.vph + ll.vph
+        x = mfma32(cat(lh, kZero4), cat(vpl[j], vpl[j]), x);  // lh.vpl
       }
       s16x4 xh, xl;
       split4(x, xh, xl);
       const s16x4 dh = frag16(&sm.Dh[I][0][0], kLdD, 0, 0, lane);
       const s16x4 dl = frag16(&sm.Dl[I][0][0], kLdD, 0, 0, lane);
       f32x4 v = {0.f, 0.f, 0.f, 0.f};
-      v = mfma16(dh, xh, v);
-      v = mfma16(dh, xl, v);
-      v = mfma16(dl, xh, v);
+      v = mfma32(cat(dh, dl), cat(xh, xh), v);      // dh.xh + dl.xh
+      v = mfma32(cat(dh, kZero4), cat(xl, xl), v);  // dh.xl
       split4(v, vph[I], vpl[I]);
     }
     // (g) O_I = exp(G) * Z_I + sum_{j<=I} P_Ij V'_j
@@ -548,8 +566,7 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
       for (int j = 0; j < 4; ++j) {
         if (j > I) continue;
         const s16x4 ph = frag16(&sm.P[0][0], kLdT, 16 * I, 16 * j, lane);
-        o = mfma16(ph, vph[j], o);
-        o = mfma16(ph, vpl[j], o);
+        o = mfma32(cat(ph, ph), cat(vph[j], vpl[j]), o);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -571,11 +588,11 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
                 sm.dec_end[16 * j + 4 * lq + r];
       s16x4 th, tl;
       split4(vt, th, tl);
+      const bf16x8 bt = cat(th, tl);
 #pragma unroll
       for (int a = 0; a < 8; ++a) {
-        const s16x4 kt = frag16(&sm.KT[0][0], kLdT, 16 * a, 16 * j, lane);
-        acc[a] = mfma16(kt, th, acc[a]);
-        acc[a] = mfma16(kt, tl, acc[a]);
+        const s16x4 kt = frag16_kt(sm.KT, 16 * a, 16 * j, lane);
+        acc[a] = mfma32(cat(kt, kt), bt, acc[a]);
       }
     }
     __syncthreads();
