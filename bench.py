@@ -104,9 +104,15 @@ def rmw_ceiling(layers: int = 30, mib: int = 128, reps: int = 8):
 
 
 # Algorithmic FLOPs of the chunked (WY form, chunk C) prefill per (token,
-# value head): 12*C*Dk + 6*Dk^2 + C^2/3 = 197,973 at C=64, Dk=128.
+# value head), d = Dk = Dv, triangular products counted at their half:
+#   K K^T and Q K^T (lower triangles)          2 C^2 d per chunk
+#   K S^T, Q S^T                               4 C d^2
+#   (I + L)^-1 solve and P V' (lower triangles) 2 C^2 d
+#   S^T update K^T W                           2 C d^2
+# = (4 C d + 6 d^2) per token = 131,072 at C = 64, d = 128 (the 16x16
+# diagonal inverses add ~0.1% and are left out).
 PREFILL_CHUNK = 64
-PREFILL_FLOP_PER_TOKEN_HEAD = 12 * PREFILL_CHUNK * DK + 6 * DK * DK + PREFILL_CHUNK ** 2 / 3
+PREFILL_FLOP_PER_TOKEN_HEAD = 4 * PREFILL_CHUNK * DK + 6 * DK * DK
 PEAK_BF16_TFLOPS = 2500.0
 
 
