@@ -104,15 +104,18 @@ def rmw_ceiling(layers: int = 30, mib: int = 128, reps: int = 8):
 
 
 # Algorithmic FLOPs of the chunked (WY form, chunk C) prefill per (token,
-# value head), d = Dk = Dv, triangular products counted at their half:
-#   K K^T and Q K^T (lower triangles)          2 C^2 d per chunk
-#   K S^T, Q S^T                               4 C d^2
-#   (I + L)^-1 solve and P V' (lower triangles) 2 C^2 d
-#   S^T update K^T W                           2 C d^2
-# = (4 C d + 6 d^2) per token = 131,072 at C = 64, d = 128 (the 16x16
-# diagonal inverses add ~0.1% and are left out).
+# value head), d = Dk = Dv, the contract's count (WY factors W = T(beta K)
+# and U = T(beta V) formed explicitly, C x C products counted in full):
+#   12 C d + 6 d^2 + C^2/3 = 197,973 at C = 64, d = 128.
+# Two further counts are reported beside it:
+#   products this kernel needs, triangles at half (no explicit W, U):
+#     K K^T, Q K^T 2 C^2 d; K S^T, Q S^T 4 C d^2; solve and P V' 2 C^2 d;
+#     S^T update 2 C d^2 -> 4 C d + 6 d^2 = 131,072 per token
+#   the sequential recurrence: 7 d^2 = 114,688 per token.
 PREFILL_CHUNK = 64
-PREFILL_FLOP_PER_TOKEN_HEAD = 4 * PREFILL_CHUNK * DK + 6 * DK * DK
+PREFILL_FLOP_PER_TOKEN_HEAD = 12 * PREFILL_CHUNK * DK + 6 * DK * DK + PREFILL_CHUNK ** 2 / 3
+PREFILL_FLOP_PER_TOKEN_HEAD_MIN = 4 * PREFILL_CHUNK * DK + 6 * DK * DK
+PREFILL_FLOP_PER_TOKEN_HEAD_SEQ = 7 * DK * DK
 PEAK_BF16_TFLOPS = 2500.0
 
 
@@ -171,6 +174,10 @@ def prefill_bench(args):
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
                      "flop_per_token_head": PREFILL_FLOP_PER_TOKEN_HEAD,
+                     "achieved_min_count": round(tflops * PREFILL_FLOP_PER_TOKEN_HEAD_MIN
+                                                 / PREFILL_FLOP_PER_TOKEN_HEAD, 2),
+                     "flop_per_token_head_min": PREFILL_FLOP_PER_TOKEN_HEAD_MIN,
+                     "flop_per_token_head_sequential": PREFILL_FLOP_PER_TOKEN_HEAD_SEQ,
                      "note": "all prefill launches (conv, norm/gates, chunk recurrence)"},
     }
     flags = pool.check()
@@ -253,11 +260,23 @@ class Workload:
             self.churn()
 
 
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(seconds: float):
     """Oracle restatement of the reference step (stack copy, out-of-place
-    kernel, unstack as views) over 30 layers, timed on this host."""
+    kernel, unstack as views) on the measured shape -- B=64, 30 layers --
+    timed on this host for a bounded number of steps."""
     from oracle import oracle as O
-    Bc = 16
+    Bc = 64
     bs = O.BaselineStep(30, Bc, HK, HV, DK, DV, KW, seed=1)
     bs.step()  # first touch of the output buffers
     n, t0 = 0, time.perf_counter()
@@ -269,8 +288,9 @@ def cpu_baseline(seconds: float):
             break
     return {"value": round(Bc * n / el, 2), "unit": "tokens/s", "cores": O.num_threads(),
             "kind": "port",
-            "sample": f"B={Bc} sequences x 30 GDN layers x {n} decode steps "
-                      f"({el:.1f} s), OpenMP over (b, hv)"}
+            "sample": f"B={Bc} sequences x 30 GDN layers x {n} decode steps ({el:.1f} s), "
+                      f"OpenMP over (b, hv), {O.num_threads()} threads of {os.cpu_count()} "
+                      f"logical CPUs, {_cpu_model()}"}
 
 
 def main(argv=None):
