@@ -65,6 +65,9 @@ def parse_args(argv=None):
     ap.add_argument("--rmw-ceiling", action="store_true",
                     help="only time a plain in-place multiply over 30 x 128 MiB buffers "
                          "(the decode's per-launch state bytes, read + write)")
+    ap.add_argument("--gated", action="store_true",
+                    help="decode through gdn_decode_gated (RMSNormGated epilogue, merged "
+                         "qkvz rows) instead of gdn_decode")
     ap.add_argument("--seed", type=int, default=0)
     return ap.parse_args(argv)
 
@@ -209,7 +212,15 @@ class Workload:
                       for _ in range(L)]
         self.dt_bias = [torch.randn(HV, generator=gen, device=self.dev) * 0.1 for _ in range(L)]
         self.nsets = 4
-        self.mixed = torch.randn((self.nsets, L, B, D), generator=gen, device=self.dev).to(bf)
+        if args.gated:
+            # merged projection rows: q|k|v then z (qwen3_5.rs:572-577)
+            self.qkvz = torch.randn((self.nsets, L, B, D + HV * DV), generator=gen,
+                                    device=self.dev).to(bf)
+            self.norm_w = [(1.0 + 0.1 * torch.randn(DV, generator=gen, device=self.dev)).to(bf)
+                           for _ in range(L)]
+            self.out = torch.empty((L, B, HV, DV), dtype=bf, device=self.dev)
+        else:
+            self.mixed = torch.randn((self.nsets, L, B, D), generator=gen, device=self.dev).to(bf)
         self.ab = torch.randn((self.nsets, L, B, 2 * HV), generator=gen, device=self.dev).to(bf)
         self.y = torch.empty((L, B, HV, DV), dtype=bf, device=self.dev)
         # initial states: every slot of every layer seeded random (state ~N(0,0.01),
@@ -250,9 +261,15 @@ class Workload:
         k = self.step_no % self.nsets
         if events is not None:
             events[0].record()
-        for l in range(self.L):
-            self.pool.decode(l, self.d_ids, self.mixed[k, l], self.ab[k, l], self.A_log[l],
-                             self.dt_bias[l], self.conv_w[l], self.y[l])
+        if self.args.gated:
+            for l in range(self.L):
+                self.pool.decode_gated(l, self.d_ids, self.qkvz[k, l], self.ab[k, l],
+                                       self.A_log[l], self.dt_bias[l], self.conv_w[l],
+                                       self.norm_w[l], 1e-6, self.out[l])
+        else:
+            for l in range(self.L):
+                self.pool.decode(l, self.d_ids, self.mixed[k, l], self.ab[k, l], self.A_log[l],
+                                 self.dt_bias[l], self.conv_w[l], self.y[l])
         if events is not None:
             events[1].record()
         self.step_no += 1
@@ -337,7 +354,7 @@ def main(argv=None):
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
             tr = json.load(f)
-        if tr.get("batch") == args.batch:
+        if tr.get("batch") == args.batch and not args.gated:
             traffic = tr.get("hbm_bytes_per_launch")
     flags = w.pool.check()
     if flags:
@@ -362,6 +379,7 @@ def main(argv=None):
             "layers": args.layers, "slots": args.slots, "batch": args.batch,
             "heads_k": HK, "heads_v": HV, "head_dim": DK, "conv_channels": D, "conv_width": KW,
             "io": "bf16 activations, f32 recurrent state, bf16 conv state",
+            "epilogue": "RMSNormGated (gdn_decode_gated)" if args.gated else "none (gdn_decode)",
         },
         "roofline": {
             "bound": "hbm",
@@ -370,7 +388,8 @@ def main(argv=None):
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": traffic,
-            "kernel": "gdn_decode (decode_kernel<2>)",
+            "kernel": ("gdn_decode_gated (decode_kernel<2, true>)" if args.gated
+                       else "gdn_decode (decode_kernel<2, false>)"),
             "kernel_avg_us": round(avg_ms * 1e3, 2),
             "kernel_timing": "HIP events around each step's back-to-back launches / launches",
             "algorithmic_bytes_per_launch": launch_bytes,

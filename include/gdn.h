@@ -168,6 +168,23 @@ gdn_status gdn_decode(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
                       const float* A_log, const float* dt_bias,
                       const uint16_t* conv_w, uint16_t* y, void* stream);
 
+/* gdn_decode with the RMSNormGated epilogue fused into the readout
+ * (qwen3_5.rs:660-665, norm_gate_fn in compiled_ops.rs:247-263): per
+ * (sequence, value head), out = silu(z) * rms_norm(y, norm_w, norm_eps) over
+ * the Dv outputs of the recurrence, each elementwise op rounded to bf16. It
+ * reads the merged projection rows as the reference produces them
+ * (qwen3_5.rs:572-577): qkvz [B, row_stride] bf16 holds q|k|v in columns
+ * [0, D) and z in columns [D, D + Hv*Dv), row_stride >= D + Hv*Dv, so no copy
+ * of either part is needed. norm_w [Dv] bf16 (the layer's norm.weight),
+ * norm_eps the model's rms_norm_eps. out [B, Hv, Dv] bf16 is the out_proj
+ * input; y [B, Hv, Dv] (the ungated recurrence output) may be NULL. Same state
+ * updates as gdn_decode. */
+gdn_status gdn_decode_gated(gdn_pool* pool, int32_t layer, const int32_t* slot_ids, int32_t B,
+                            const uint16_t* qkvz, int64_t row_stride, const uint16_t* ab,
+                            const float* A_log, const float* dt_bias, const uint16_t* conv_w,
+                            const uint16_t* norm_w, float norm_eps, uint16_t* out, uint16_t* y,
+                            void* stream);
+
 /* Varlen prefill of nseq sequences packed along the token axis
  * (qwen3_5.rs:611-658 with S>1; the reference runs them one at a time, B=1):
  * sequence i owns tokens [cu_seqlens[i], cu_seqlens[i+1]) of mixed_qkv / ab / y

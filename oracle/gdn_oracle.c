@@ -177,6 +177,32 @@ void orc_rms_norm(const uint16_t* x, int64_t rows, int dim, float w, float eps, 
   }
 }
 
+/*
+ * RMSNormGated epilogue (src/models/qwen3_5.rs:660-665; the same math as
+ * norm_gate_fn, src/models/compiled_ops.rs:247-263):
+ *   out = silu(z) * rms_norm(y, w, eps) on rows of dim (= Dv) elements:
+ *   r = 1/sqrt(sum(y^2)/dim + eps) (f32), normed_i = bf16(w_i * bf16(y_i * r)),
+ *   silu on bf16 z with each op rounded, the product rounded to bf16.
+ * y, z, out: [rows, dim] bf16 (out may alias y); w: [dim] bf16.
+ */
+void orc_norm_gate(const uint16_t* y, const uint16_t* z, const uint16_t* w, int64_t rows, int dim,
+                   float eps, uint16_t* out) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const uint16_t* yr = y + r * dim;
+    const uint16_t* zr = z + r * dim;
+    float ss = 0.0f;
+    for (int i = 0; i < dim; ++i) {
+      const float v = bf2f(yr[i]);
+      ss += v * v;
+    }
+    const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+    for (int i = 0; i < dim; ++i) {
+      const float normed = rbf(bf2f(w[i]) * rbf(bf2f(yr[i]) * inv));
+      out[r * dim + i] = f2bf(silu_bf16(bf2f(zr[i])) * normed);
+    }
+  }
+}
+
 float orc_q_norm_weight(int dk) { return rbf(1.0f / (float)dk); }
 float orc_k_norm_weight(int dk) { return rbf(powf((float)dk, -0.5f)); }
 

@@ -44,6 +44,7 @@ def lib():
     L.orc_conv_update.argtypes = [_u16p, _u16p, _u16p, _c_int, _c_int, _c_int, _u16p, _u16p]
     L.orc_conv_prefill.argtypes = [_u16p, _u16p, _u16p, _c_int, _c_int, _c_int, _u16p, _u16p]
     L.orc_rms_norm.argtypes = [_u16p, _c_i64, _c_int, _c_float, _c_float, _u16p]
+    L.orc_norm_gate.argtypes = [_u16p, _u16p, _u16p, _c_i64, _c_int, _c_float, _u16p]
     L.orc_q_norm_weight.argtypes = [_c_int]
     L.orc_q_norm_weight.restype = _c_float
     L.orc_k_norm_weight.argtypes = [_c_int]
@@ -131,6 +132,19 @@ def rms_norm(x, w: float, eps: float = 1e-6):
     dim = x.shape[-1]
     out = np.empty_like(x)
     lib().orc_rms_norm(x, x.size // dim, dim, w, eps, out)
+    return out
+
+
+def norm_gate(y, z, w, eps: float = 1e-6):
+    """RMSNormGated: silu(z) * rms_norm(y, w, eps) over the last axis.
+    y, z bf16 [..., dim]; w bf16 [dim] -> bf16 [..., dim]."""
+    y = _c(y, np.uint16)
+    z = _c(z, np.uint16)
+    w = _c(w, np.uint16)
+    dim = y.shape[-1]
+    assert z.shape == y.shape and w.shape == (dim,)
+    out = np.empty_like(y)
+    lib().orc_norm_gate(y, z, w, y.size // dim, dim, eps, out)
     return out
 
 

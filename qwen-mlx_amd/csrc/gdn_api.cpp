@@ -349,21 +349,24 @@ static gdn_status ensure_workspace(gdn_pool* pool, size_t need, void* stream, co
   return GDN_OK;
 }
 
-gdn_status gdn_decode(gdn_pool* pool, int32_t layer, const int32_t* slot_ids, int32_t B,
-                      const uint16_t* mixed_qkv, const uint16_t* ab, const float* A_log,
-                      const float* dt_bias, const uint16_t* conv_w, uint16_t* y, void* stream) {
+// Shared checks and launch of the fused decode (gdn_decode, gdn_decode_gated).
+static gdn_status decode_common(gdn_pool* pool, int32_t layer, const int32_t* slot_ids, int32_t B,
+                                const uint16_t* qkv, int64_t xstride, const uint16_t* ab,
+                                const float* A_log, const float* dt_bias, const uint16_t* conv_w,
+                                uint16_t* y, const uint16_t* norm_w, float norm_eps, uint16_t* out,
+                                void* stream, const char* who) {
   gdn_status st = check_layer(pool, layer, false);
   if (st) return st;
-  if (B < 0) return fail(GDN_ERR_INVALID, "B = %d < 0", B);
+  if (B < 0) return fail(GDN_ERR_INVALID, "%s: B = %d < 0", who, B);
   if (B == 0) return GDN_OK;
-  if (B > 65535) return fail(GDN_ERR_INVALID, "B = %d > 65535", B);
+  if (B > 65535) return fail(GDN_ERR_INVALID, "%s: B = %d > 65535", who, B);
   if (B > pool->d.num_slots)
-    return fail(GDN_ERR_INVALID, "B = %d > num_slots = %d (slot ids must be distinct)", B,
+    return fail(GDN_ERR_INVALID, "%s: B = %d > num_slots = %d (slot ids must be distinct)", who, B,
                 pool->d.num_slots);
-  if (!slot_ids || !mixed_qkv || !ab || !A_log || !dt_bias || !conv_w || !y)
-    return fail(GDN_ERR_INVALID, "gdn_decode: NULL tensor pointer");
+  if (!slot_ids || !qkv || !ab || !A_log || !dt_bias || !conv_w)
+    return fail(GDN_ERR_INVALID, "%s: NULL tensor pointer", who);
   if (reinterpret_cast<uintptr_t>(conv_w) % 8 != 0)
-    return fail(GDN_ERR_INVALID, "gdn_decode: conv_w must be 8-byte aligned");
+    return fail(GDN_ERR_INVALID, "%s: conv_w must be 8-byte aligned", who);
   DeviceGuard guard(pool->d.device);
   gdn::DecodeArgs a{};
   a.R = pool->R;
@@ -373,17 +376,48 @@ gdn_status gdn_decode(gdn_pool* pool, int32_t layer, const int32_t* slot_ids, in
   a.state = pool->state[layer];
   a.conv = pool->conv[layer];
   a.slot_ids = slot_ids;
-  a.mixed = mixed_qkv;
+  a.mixed = qkv;
+  a.xstride = xstride;
   a.ab = ab;
   a.A_log = A_log;
   a.dt_bias = dt_bias;
   a.conv_w = conv_w;
   a.y = y;
+  a.norm_w = norm_w;
+  a.norm_eps = norm_eps;
+  a.out = out;
   a.status = pool->d_status;
   a.stream = as_stream(stream);
   hipError_t e = gdn::launch_decode(a);
-  if (e != hipSuccess) return hip_fail(e, "gdn_decode launch");
+  if (e != hipSuccess) return hip_fail(e, who);
   return GDN_OK;
+}
+
+gdn_status gdn_decode(gdn_pool* pool, int32_t layer, const int32_t* slot_ids, int32_t B,
+                      const uint16_t* mixed_qkv, const uint16_t* ab, const float* A_log,
+                      const float* dt_bias, const uint16_t* conv_w, uint16_t* y, void* stream) {
+  if (!y && B > 0) return fail(GDN_ERR_INVALID, "gdn_decode: NULL tensor pointer");
+  return decode_common(pool, layer, slot_ids, B, mixed_qkv, pool ? pool->D : 0, ab, A_log,
+                       dt_bias, conv_w, y, nullptr, 0.0f, nullptr, stream, "gdn_decode");
+}
+
+gdn_status gdn_decode_gated(gdn_pool* pool, int32_t layer, const int32_t* slot_ids, int32_t B,
+                            const uint16_t* qkvz, int64_t row_stride, const uint16_t* ab,
+                            const float* A_log, const float* dt_bias, const uint16_t* conv_w,
+                            const uint16_t* norm_w, float norm_eps, uint16_t* out, uint16_t* y,
+                            void* stream) {
+  if (pool) {
+    const int64_t need = (int64_t)pool->D + (int64_t)pool->d.num_v_heads * pool->d.head_v_dim;
+    if (row_stride < need)
+      return fail(GDN_ERR_INVALID, "gdn_decode_gated: row_stride %lld < D + Hv*Dv = %lld",
+                  (long long)row_stride, (long long)need);
+  }
+  if (B > 0 && (!norm_w || !out))
+    return fail(GDN_ERR_INVALID, "gdn_decode_gated: NULL norm_w / out");
+  if (!(norm_eps >= 0.0f))
+    return fail(GDN_ERR_INVALID, "gdn_decode_gated: norm_eps must be >= 0");
+  return decode_common(pool, layer, slot_ids, B, qkvz, row_stride, ab, A_log, dt_bias, conv_w, y,
+                       norm_w, norm_eps, out, stream, "gdn_decode_gated");
 }
 
 gdn_status gdn_prefill_varlen(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,

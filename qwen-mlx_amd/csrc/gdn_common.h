@@ -121,12 +121,16 @@ struct DecodeArgs {
   float* state;
   uint16_t* conv;
   const int32_t* slot_ids;
-  const uint16_t* mixed;
+  const uint16_t* mixed;   // [B, xstride] rows: q|k|v in the first D columns (then z if gated)
+  int64_t xstride;         // row stride of mixed in elements (D, or the merged qkvz width)
   const uint16_t* ab;
   const float* A_log;
   const float* dt_bias;
   const uint16_t* conv_w;
-  uint16_t* y;
+  uint16_t* y;             // recurrence output [B,Hv,Dv]; may be null when out is set
+  const uint16_t* norm_w;  // RMSNormGated weight [Dv] (gated only)
+  float norm_eps;
+  uint16_t* out;           // gated output [B,Hv,Dv]; null = no epilogue
   uint32_t* status;
   hipStream_t stream;
 };

@@ -168,7 +168,8 @@ __global__ __launch_bounds__(256 * R) void recurrent_kernel(
 
 // -------------------------------------------------------------------------
 // Fused S=1 decode (conv update + silu + split + q/k rms-norm + gates +
-// recurrence), one launch. grid (Hk, B), block 256*R.
+// recurrence, optionally the RMSNormGated epilogue), one launch. grid (Hk, B),
+// block 256*R.
 //
 // The group of (b, hk) owns the q/k conv channels of hk and the v channels of
 // its R value heads, so it is the only reader and writer of those conv-state
@@ -193,12 +194,14 @@ __device__ __forceinline__ float conv1(uint16_t c0, uint16_t c1, uint16_t c2, ui
   return silu_bf16(rbf(acc));
 }
 
-template <int R>
+template <int R, bool GATED>
 __global__ __launch_bounds__(256 * R) void decode_kernel(
     float* __restrict__ state, uint16_t* __restrict__ conv, const int32_t* __restrict__ slot_ids,
-    int num_slots, int Hk, const uint16_t* __restrict__ mixed, const uint16_t* __restrict__ ab,
-    const float* __restrict__ A_log, const float* __restrict__ dt_bias,
-    const uint16_t* __restrict__ conv_w, uint16_t* __restrict__ y, uint32_t* __restrict__ status) {
+    int num_slots, int Hk, const uint16_t* __restrict__ mixed, int64_t xstride,
+    const uint16_t* __restrict__ ab, const float* __restrict__ A_log,
+    const float* __restrict__ dt_bias, const uint16_t* __restrict__ conv_w,
+    uint16_t* __restrict__ y, const uint16_t* __restrict__ norm_w, float norm_eps,
+    uint16_t* __restrict__ out, uint32_t* __restrict__ status) {
   constexpr int NT = 256 * R;
   constexpr int NCH = (2 + R) * kDk;
   constexpr int CPT = (NCH + NT - 1) / NT;
@@ -215,11 +218,23 @@ __global__ __launch_bounds__(256 * R) void decode_kernel(
   __shared__ __align__(16) float qk[2][kDk];
   __shared__ float red[8];
   __shared__ float gsh[R][2];
+  // RMSNormGated staging: silu(z) and w per (head, row), y of the rows, and the
+  // per-wave sums of y^2
+  __shared__ float zsil[GATED ? R * kDv : 1], wsh[GATED ? R * kDv : 1], ysh[GATED ? R * kDv : 1];
+  __shared__ float ysq[4 * R];
   auto chan = [&](int c) {
     return c < kDk ? hk * kDk + c
                    : (c < 2 * kDk ? Hk * kDk + hk * kDk + (c - kDk)
                                   : 2 * Hk * kDk + hk * R * kDv + (c - 2 * kDk));
   };
+  // this thread's value head, and its rows 32wt + 4j + (lane >> 4), j = 0..7
+  const int r = wave >> 2, wt = wave & 3;
+  const int hv = hk * R + r;
+  const int row0 = 32 * wt + (lane >> 4);
+  const uint16_t* xrow = mixed + (size_t)b * xstride;
+
+  // 1. conv window, weights and gate inputs (and the gate's z and norm
+  // weight of the thread's rows), then the state rows
   uint16_t* cs = conv + (size_t)slot * (kConvK - 1) * D;
   uint2 cw[CPT];
   uint16_t c0[CPT], c1[CPT], c2[CPT], cx[CPT];
@@ -228,17 +243,25 @@ __global__ __launch_bounds__(256 * R) void decode_kernel(
     const int c = tid + u * NT;
     const int gc = chan(c < NCH ? c : 0);
     cw[u] = *reinterpret_cast<const uint2*>(conv_w + (size_t)gc * kConvK);
-    c0[u] = cs[gc]; c1[u] = cs[D + gc]; c2[u] = cs[2 * D + gc];
-    cx[u] = mixed[(size_t)b * D + gc];
+    c0[u] = cs[gc];
+    c1[u] = cs[D + gc];
+    c2[u] = cs[2 * D + gc];
+    cx[u] = xrow[gc];
   }
   const int gr = tid & (R - 1), gh = hk * R + gr;
   const float alog = A_log[gh], dtb = dt_bias[gh];
   const uint16_t braw = ab[(size_t)b * 2 * Hv + gh], araw = ab[(size_t)b * 2 * Hv + Hv + gh];
+  // gate inputs of (head hk*R + e/Dv, row e%Dv), e = t mod R*Dv: z follows
+  // q|k|v in the merged row, so the R heads' z are contiguous
+  uint16_t zr = 0, wr = 0;
+  if constexpr (GATED) {
+    const int e = tid & (R * kDv - 1);
+    zr = xrow[D + hk * R * kDv + e];
+    wr = norm_w[e & (kDv - 1)];
+  }
   __builtin_amdgcn_sched_barrier(0);
-  const int r = wave >> 2, wt = wave & 3;
-  const int hv = hk * R + r;
   float* tile = state + ((size_t)slot * Hv + hv) * kTileElems;
-  float* base = tile + (size_t)(32 * wt + (lane >> 4)) * kDk;
+  float* base = tile + (size_t)row0 * kDk;
   v4f s[8][2];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -246,6 +269,8 @@ __global__ __launch_bounds__(256 * R) void decode_kernel(
     s[j][1] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(base + 4 * j * kDk + 64 + 4 * l));
   }
   __builtin_amdgcn_sched_barrier(0);
+
+  // 2. conv (qwen3_5.rs:602-610), gates (compiled_ops.rs:30-43) on ab = [b | a]
 #pragma unroll
   for (int u = 0; u < CPT; ++u) xs[tid + u * NT] = conv1(c0[u], c1[u], c2[u], cx[u], cw[u]);
   {
@@ -253,7 +278,12 @@ __global__ __launch_bounds__(256 * R) void decode_kernel(
     gsh[gr][0] = expf(-(expf(alog) * sp));
     gsh[gr][1] = rbf(sigmoid_f32(bf2f(braw)));
   }
+  if constexpr (GATED) {  // threads t and t + R*Dv write the same values
+    zsil[tid & (R * kDv - 1)] = silu_bf16(bf2f(zr));
+    wsh[tid & (R * kDv - 1)] = bf2f(wr);
+  }
   lds_barrier();
+  // 3. q/k rms-norm (qwen3_5.rs:638-639): waves 0-1 hold q, waves 2-3 hold k
   if (tid < 2 * kDk) {
     const float v = xs[tid];
     const float ss = wave_sum(v * v);
@@ -261,18 +291,22 @@ __global__ __launch_bounds__(256 * R) void decode_kernel(
   }
   lds_barrier();
   if (tid < 2 * kDk) {
-    const float rn = 1.0f / sqrtf((wave < 2 ? red[0] + red[1] : red[2] + red[3]) / (float)kDk + kNormEps);
+    const float rn =
+        1.0f / sqrtf((wave < 2 ? red[0] + red[1] : red[2] + red[3]) / (float)kDk + kNormEps);
     qk[tid >> 7][tid & (kDk - 1)] = rbf((tid < kDk ? kQNormW : kKNormW) * rbf(xs[tid] * rn));
   }
   lds_barrier();
+
+  // 4. recurrence on the rows
   const v4f qa = *reinterpret_cast<const v4f*>(&qk[0][4 * l]);
   const v4f qb = *reinterpret_cast<const v4f*>(&qk[0][64 + 4 * l]);
   const v4f ka = *reinterpret_cast<const v4f*>(&qk[1][4 * l]);
   const v4f kb = *reinterpret_cast<const v4f*>(&qk[1][64 + 4 * l]);
   const float kq = sum16(dot4(ka, qa) + dot4(kb, qb));
   const float g = gsh[r][0], beta = gsh[r][1];
-  const float* vrow = &xs[2 * kDk + r * kDv + 32 * wt + (lane >> 4)];
-  uint16_t* yo = y + ((size_t)b * Hv + hv) * kDv + 32 * wt + (lane >> 4);
+  const float* vrow = &xs[2 * kDk + r * kDv + row0];
+  const size_t yoff = ((size_t)b * Hv + hv) * kDv + row0;
+  float yb[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const v4f a0 = s[j][0] * g, a1 = s[j][1] * g;
@@ -281,24 +315,61 @@ __global__ __launch_bounds__(256 * R) void decode_kernel(
     const float d = (vrow[4 * j] - kd) * beta;
     __builtin_nontemporal_store(a0 + ka * d, reinterpret_cast<v4f*>(base + 4 * j * kDk + 4 * l));
     __builtin_nontemporal_store(a1 + kb * d, reinterpret_cast<v4f*>(base + 4 * j * kDk + 64 + 4 * l));
-    if (l == 0) yo[4 * j] = f2bf(qd + d * kq);
+    yb[j] = rbf(qd + d * kq);
+    if (y != nullptr && l == 0) y[yoff + 4 * j] = f2bf(yb[j]);
   }
+
+  // 5. RMSNormGated epilogue (qwen3_5.rs:660-665): out = silu(z) *
+  // rms_norm(y, w, eps) over each head's Dv rows. Sum of y^2 per wave (8 rows
+  // per lane group, 4 groups), y staged in LDS; after the barrier thread t < R*Dv
+  // writes row t%Dv of head hk*R + t/Dv (coalesced).
+  if constexpr (GATED) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += yb[j] * yb[j];
+    ss += __shfl_xor(ss, 16, 64);
+    ss += __shfl_xor(ss, 32, 64);
+    if (lane == 0) ysq[wave] = ss;
+    if (l == 0) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ysh[r * kDv + row0 + 4 * j] = yb[j];
+    }
+    lds_barrier();
+    if (tid < R * kDv) {
+      const int h = tid / kDv;
+      const float tot = ysq[4 * h] + ysq[4 * h + 1] + ysq[4 * h + 2] + ysq[4 * h + 3];
+      const float rn = 1.0f / sqrtf(tot / (float)kDv + norm_eps);
+      const float normed = rbf(wsh[tid] * rbf(ysh[tid] * rn));
+      out[((size_t)b * Hv + hk * R) * kDv + tid] = f2bf(zsil[tid] * normed);
+    }
+  }
+
+  // 6. rolling conv state: window [s0 s1 s2 x] -> [s1 s2 x] in place (this
+  // group's channels only)
 #pragma unroll
   for (int u = 0; u < CPT; ++u) {
     const int c = tid + u * NT;
     if (c < NCH) {
       const int gc = chan(c);
-      cs[gc] = c1[u]; cs[D + gc] = c2[u]; cs[2 * D + gc] = cx[u];
+      cs[gc] = c1[u];
+      cs[D + gc] = c2[u];
+      cs[2 * D + gc] = cx[u];
     }
   }
 }
+
 // ------------------------------------------------------------ launchers --
 
 template <int R>
 static hipError_t launch_decode_r(const DecodeArgs& a) {
-  hipLaunchKernelGGL(decode_kernel<R>, dim3(a.Hk, a.B), dim3(256 * R), 0, a.stream, a.state,
-                     a.conv, a.slot_ids, a.num_slots, a.Hk, a.mixed, a.ab, a.A_log, a.dt_bias,
-                     a.conv_w, a.y, a.status);
+  if (a.out)
+    hipLaunchKernelGGL((decode_kernel<R, true>), dim3(a.Hk, a.B), dim3(256 * R), 0, a.stream,
+                       a.state, a.conv, a.slot_ids, a.num_slots, a.Hk, a.mixed, a.xstride, a.ab,
+                       a.A_log, a.dt_bias, a.conv_w, a.y, a.norm_w, a.norm_eps, a.out, a.status);
+  else
+    hipLaunchKernelGGL((decode_kernel<R, false>), dim3(a.Hk, a.B), dim3(256 * R), 0, a.stream,
+                       a.state, a.conv, a.slot_ids, a.num_slots, a.Hk, a.mixed, a.xstride, a.ab,
+                       a.A_log, a.dt_bias, a.conv_w, a.y, a.norm_w, a.norm_eps, a.out, a.status);
   return hipGetLastError();
 }
 

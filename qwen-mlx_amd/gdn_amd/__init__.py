@@ -47,6 +47,8 @@ SIGNATURES = {
     "gdn_recurrent": ([_VP, _I32, _VP, _I32, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _VP],
                       ctypes.c_int),
     "gdn_decode": ([_VP, _I32, _VP, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _VP], ctypes.c_int),
+    "gdn_decode_gated": ([_VP, _I32, _VP, _I32, _VP, ctypes.c_int64, _VP, _VP, _VP, _VP, _VP,
+                          ctypes.c_float, _VP, _VP, _VP], ctypes.c_int),
     "gdn_prefill_varlen": ([_VP, _I32, _VP, _VP, _I32, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _VP],
                            ctypes.c_int),
 }
@@ -206,6 +208,17 @@ class Pool:
         _check(self.lib.gdn_decode(self.handle, layer, _ptr(slot_ids), slot_ids.numel(),
                                    _ptr(mixed_qkv), _ptr(ab), _ptr(A_log), _ptr(dt_bias),
                                    _ptr(conv_w), _ptr(y), _stream(stream)))
+
+    def decode_gated(self, layer, slot_ids, qkvz, ab, A_log, dt_bias, conv_w, norm_w, norm_eps,
+                     out, y=None, stream=None):
+        """Decode with the RMSNormGated epilogue. qkvz: [B, row_stride] rows holding
+        q|k|v then z (the merged projection output); out (and optional y) [B,Hv,Dv]."""
+        if qkvz.dim() != 2:
+            raise ValueError("qkvz must be [B, row_stride]")
+        _check(self.lib.gdn_decode_gated(self.handle, layer, _ptr(slot_ids), slot_ids.numel(),
+                                         _ptr(qkvz), qkvz.shape[1], _ptr(ab), _ptr(A_log),
+                                         _ptr(dt_bias), _ptr(conv_w), _ptr(norm_w),
+                                         float(norm_eps), _ptr(out), _ptr(y), _stream(stream)))
 
     def prefill(self, layer, slot_ids, cu_seqlens, total_tokens, mixed_qkv, ab, A_log, dt_bias,
                 conv_w, y, stream=None):

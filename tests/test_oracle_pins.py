@@ -165,6 +165,41 @@ def test_rms_norm_closed_form():
     assert got == pytest.approx(expect, rel=1e-2) and got < 0.11
 
 
+def test_norm_gate_closed_form_and_special_values():
+    """RMSNormGated out = silu(z) * rms_norm(y, w, eps) per row of Dv."""
+    rng = np.random.default_rng(16)
+    rows = 40
+    y = O.f32_to_bf16(rng.standard_normal((rows, DV)).astype(np.float32) * 0.3)
+    z = O.f32_to_bf16(rng.standard_normal((rows, DV)).astype(np.float32))
+    w = O.f32_to_bf16((1.0 + 0.2 * rng.standard_normal(DV)).astype(np.float32))
+    eps = 1e-6
+    out = f64(O.norm_gate(y, z, w, eps))
+    yf, zf, wf = f64(y), f64(z), f64(w)
+    silu = zf / (1.0 + np.exp(-zf))
+    expect = silu * wf * yf / np.sqrt((yf ** 2).mean(-1, keepdims=True) + eps)
+    # three bf16 roundings on the way (y*r, w*., silu, product): a few ulps
+    assert np.allclose(out, expect, rtol=2 ** -6, atol=1e-6)
+    # the mean, not the sum, of squares: a dropped 1/Dv would scale by sqrt(Dv)
+    assert np.abs(np.linalg.norm(out, axis=-1) / np.linalg.norm(expect, axis=-1) - 1).max() < 1e-2
+    # z = 0 gates everything off exactly (to +-0)
+    assert not f64(O.norm_gate(y, np.zeros_like(z), w, eps)).any()
+    # rows are independent: permuting rows permutes outputs
+    perm = rng.permutation(rows)
+    assert np.array_equal(O.norm_gate(y[perm], z[perm], w, eps), O.norm_gate(y, z, w, eps)[perm])
+    # z = 16: sigmoid rounds to 1.0 in bf16 and silu(z) = 16, so out/16 is
+    # exactly the (already pinned) baked-weight rms_norm with a constant w
+    c = O.f32_to_bf16(np.array([0.75], np.float32))[0]
+    z16 = np.full_like(z, O.f32_to_bf16(np.float32(16.0)))
+    wc = np.full(DV, c, np.uint16)
+    got = f64(O.norm_gate(y, z16, wc, eps)) / 16.0
+    assert np.array_equal(got, f64(O.rms_norm(y, float(O.bf16_to_f32(np.array([c]))[0]), eps)))
+    # eps matters for tiny y: a row of 1e-4 normalises to ~0.1, not 1
+    tiny = O.f32_to_bf16(np.full((1, DV), 1e-4, np.float32))
+    got = f64(O.norm_gate(tiny, z16[:1], np.full(DV, O.f32_to_bf16(np.float32(1.0)), np.uint16),
+                          eps)) / 16.0
+    assert got.max() == pytest.approx(1e-4 / math.sqrt(1e-8 + eps), rel=1e-2)
+
+
 # ------------------------------------------------------------ recurrence --
 
 def _brute_recurrence(q, k, v, g, beta, S):
