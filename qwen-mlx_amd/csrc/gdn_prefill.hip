@@ -455,10 +455,11 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
     if (c0 + kC < en) load_inputs(c0 + kC);
 
     // (b) waves 0-3: K K^T for token rows 16w.. -> -L (hi/lo) and its f32
-    // diagonal block; waves 4-7: Q K^T for token rows 16(w-4).. -> P. Column
-    // blocks above the row block are zero and skipped.
+    // diagonal block; waves 4-7: Q K^T for token rows 16(7-w).. -> P. Column
+    // blocks above the row block are zero and skipped, so row block I has I+1
+    // blocks; waves w and w+4 share a SIMD, which thus gets (w+1) + (4-w) = 5.
     {
-      const int I = w & 3;
+      const int I = w < 4 ? w : 7 - w;
       const bool isq = w >= 4;
       const uint16_t* A = isq ? &sm.Q[0][0] : &sm.K[0][0];
 #pragma unroll
