@@ -192,7 +192,9 @@ gdn_status gdn_decode_gated(gdn_pool* pool, int32_t layer, const int32_t* slot_i
  * recurrent state (zero after gdn_slots_zero, as the reference's fresh
  * prefill) and leaves its final states there. cu_seqlens is a DEVICE int32
  * array of nseq+1 entries with cu_seqlens[0] == 0 and
- * cu_seqlens[nseq] == total_tokens. Uses the chunked (WY form, chunk 64)
+ * cu_seqlens[nseq] == total_tokens <= 4,194,240 (65535 tiles of 64 tokens);
+ * a cu_seqlens that breaks these latches GDN_FLAG_BAD_SEQLENS (the kernels
+ * clamp every bound they read). Uses the chunked (WY form, chunk 64)
  * algorithm; results equal the token-by-token recurrence within f32/bf16
  * rounding. */
 gdn_status gdn_prefill_varlen(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,

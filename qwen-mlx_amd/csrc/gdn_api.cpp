@@ -329,6 +329,9 @@ gdn_status gdn_recurrent(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
   return GDN_OK;
 }
 
+// Token tiles of 64 run along the grid's y axis (at most 65535).
+constexpr int32_t kMaxPrefillTokens = 65535 * 64;
+
 // Grows the pool's prefill workspace to at least `need` bytes. Growing waits
 // for the stream, so work still reading the old buffer has finished.
 static gdn_status ensure_workspace(gdn_pool* pool, size_t need, void* stream, const char* what) {
@@ -431,6 +434,9 @@ gdn_status gdn_prefill_varlen(gdn_pool* pool, int32_t layer, const int32_t* slot
     return fail(GDN_ERR_INVALID, "nseq = %d, total_tokens = %d must be >= 0", nseq, total_tokens);
   if (nseq == 0) return GDN_OK;
   if (nseq > 65535) return fail(GDN_ERR_INVALID, "nseq = %d > 65535", nseq);
+  if (total_tokens > kMaxPrefillTokens)
+    return fail(GDN_ERR_INVALID, "total_tokens = %d > %d per call", total_tokens,
+                kMaxPrefillTokens);
   if (!slot_ids || !cu_seqlens || !A_log || !dt_bias || !conv_w)
     return fail(GDN_ERR_INVALID, "gdn_prefill_varlen: NULL pointer");
   if (total_tokens > 0 && (!mixed_qkv || !ab || !y))

@@ -224,12 +224,20 @@ __global__ __launch_bounds__(256) void prefill_qkv_kernel(
 }
 
 // 2. new conv state = last K-1 rows of padded (qwen3_5.rs:618-619).
-// Runs after (1) has read the old rows. grid (nseq, D/256), block 256.
+// Runs after (1) has read the old rows. grid (nseq, D/256), block 256. Also
+// checks cu_seqlens (cu[0] = 0, non-decreasing, cu[nseq] = T), latching
+// GDN_FLAG_BAD_SEQLENS; every kernel clamps the bounds it reads either way.
 __global__ __launch_bounds__(256) void prefill_conv_state_kernel(
     uint16_t* __restrict__ conv, const int32_t* __restrict__ slot_ids,
-    const int32_t* __restrict__ cu, int num_slots, int D, int T, const uint16_t* __restrict__ x) {
+    const int32_t* __restrict__ cu, int nseq, int num_slots, int D, int T,
+    const uint16_t* __restrict__ x, uint32_t* __restrict__ status) {
   const int s = blockIdx.x;
   const int ch = blockIdx.y * 256 + threadIdx.x;
+  if (blockIdx.y == 0 && threadIdx.x == 0) {
+    const int a = cu[s], b = cu[s + 1];
+    if ((s == 0 && a != 0) || b < a || b > T || (s == nseq - 1 && b != T))
+      flag_status(status, GDN_FLAG_BAD_SEQLENS);
+  }
   if (ch >= D) return;
   const int slot = slot_ids[s];
   if ((unsigned)slot >= (unsigned)num_slots) return;
@@ -622,8 +630,8 @@ static hipError_t launch_prefill_r(const PrefillArgs& a) {
     if (e != hipSuccess) return e;
   }
   hipLaunchKernelGGL(prefill_conv_state_kernel, dim3(a.nseq, (D + 255) / 256), dim3(256), 0,
-                     a.stream, a.conv, a.slot_ids, a.cu_seqlens, a.num_slots, D, a.total_tokens,
-                     a.mixed);
+                     a.stream, a.conv, a.slot_ids, a.cu_seqlens, a.nseq, a.num_slots, D,
+                     a.total_tokens, a.mixed, a.status);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(prefill_chunk_kernel<R>, dim3(Hv, a.nseq), dim3(512), 0,

@@ -68,9 +68,30 @@ hipError_t launch_slots(const SlotArgs& a) {
   return hipGetLastError();
 }
 
-// Range and uniqueness check of a slot-id list (one work-group; O(n^2/256)).
+// Range and uniqueness check of a slot-id list, one work-group. Pools of up to
+// kBitmapSlots slots mark each id in an LDS bitmap (a second mark of the same
+// bit is a duplicate), O(n); larger pools compare pairs, O(n^2).
+constexpr int kBitmapWords = 16384;  // 64 KiB of LDS
+constexpr int kBitmapSlots = kBitmapWords * 32;
+
 __global__ __launch_bounds__(256) void validate_kernel(const int32_t* __restrict__ ids, int n,
                                                        int num_slots, uint32_t* status) {
+  __shared__ uint32_t seen[kBitmapWords];
+  if (num_slots <= kBitmapSlots) {
+    const int words = (num_slots + 31) >> 5;
+    for (int i = threadIdx.x; i < words; i += blockDim.x) seen[i] = 0u;
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+      const int s = ids[i];
+      if ((unsigned)s >= (unsigned)num_slots) {
+        flag_status(status, GDN_FLAG_BAD_SLOT);
+        continue;
+      }
+      const uint32_t bit = 1u << (s & 31);
+      if (atomicOr(&seen[s >> 5], bit) & bit) flag_status(status, GDN_FLAG_DUP_SLOT);
+    }
+    return;
+  }
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
     const int s = ids[i];
     if ((unsigned)s >= (unsigned)num_slots) flag_status(status, GDN_FLAG_BAD_SLOT);

@@ -78,6 +78,16 @@ def test_slot_validation_and_bad_slot_flags(gpu):
     assert pool.check() == gdn_amd.GDN_FLAG_DUP_SLOT
     pool.validate(_ids([1, 8]))
     assert pool.check() == gdn_amd.GDN_FLAG_BAD_SLOT
+    # a long list over a larger pool (LDS bitmap path): a permutation passes,
+    # one repeated id anywhere is caught
+    big = _pool(1, 5000, 2, 4)
+    perm = np.random.default_rng(77).permutation(5000)[:3000].astype(np.int32)
+    big.validate(_ids(perm))
+    assert big.check() == 0
+    dup = perm.copy()
+    dup[2999] = dup[17]
+    big.validate(_ids(dup))
+    assert big.check() == gdn_amd.GDN_FLAG_DUP_SLOT
     # a decode launch with an out-of-range slot skips that sequence, flags it,
     # and still updates the valid one
     rng = np.random.default_rng(101)

@@ -126,3 +126,37 @@ def test_prefill_edge_lengths_from_nonzero_state(gpu, Hk, Hv):
         assert np.max(np.abs(O.bf16_to_f32(y[a:b]) - O.bf16_to_f32(yr))) <= Y_TOL
         assert rel_l2(gs[i], sr) <= STATE_TOL
     assert pool.check() == 0
+
+
+def test_prefill_bad_cu_seqlens_are_flagged_and_clamped(gpu):
+    """cu_seqlens must start at 0, not decrease and end at total_tokens; each
+    violation latches GDN_FLAG_BAD_SEQLENS while the kernels clamp the bounds,
+    so nothing outside the inputs or the named slots is touched."""
+    import torch
+    import gdn_amd
+    Hk, Hv = 2, 4
+    D = conv_dim(Hk, Hv)
+    rng = np.random.default_rng(620)
+    p = gen_layer_params(rng, Hk, Hv)
+    T = 12
+    mixed, ab = gen_tokens(rng, T, Hk, Hv)
+    pool = gdn_amd.Pool(1, 6, Hk, Hv)
+    st, cs = gen_states(rng, 6, Hk, Hv)
+    pool.write(0, _ids(list(range(6))), dev(st), dev(cs))
+    args = (dev(mixed), dev(ab), dev(p["A_log"]), dev(p["dt_bias"]), dev(p["conv_w"]))
+    y = torch.zeros((T, Hv, DV), dtype=torch.int16, device=gpu)
+    cases = {"decreasing": [0, 10, 4], "nonzero start": [2, 7, 12], "short end": [0, 4, 8],
+             "past end": [0, 6, 20]}
+    for name, cu in cases.items():
+        say("bad cu_seqlens", name, cu)
+        pool.prefill(0, _ids([1, 3]), dev(np.asarray(cu, np.int32)), T, *args, y)
+        assert pool.check() == gdn_amd.GDN_FLAG_BAD_SEQLENS, name
+    # slots never named keep their bytes
+    gs = torch.empty((4, Hv, DV, DK), dtype=torch.float32, device=gpu)
+    gc = torch.empty((4, K - 1, D), dtype=torch.int16, device=gpu)
+    pool.read(0, _ids([0, 2, 4, 5]), gs, gc)
+    assert np.array_equal(host(gs), st[[0, 2, 4, 5]])
+    assert np.array_equal(host(gc), cs[[0, 2, 4, 5]])
+    # a well-formed list raises nothing
+    pool.prefill(0, _ids([1, 3]), dev(np.asarray([0, 5, 12], np.int32)), T, *args, y)
+    assert pool.check() == 0
