@@ -68,6 +68,11 @@ def parse_args(argv=None):
     ap.add_argument("--gated", action="store_true",
                     help="decode through gdn_decode_gated (RMSNormGated epilogue, merged "
                          "qkvz rows) instead of gdn_decode")
+    ap.add_argument("--qlinear", action="store_true",
+                    help="measure the merged 4-bit input projection (gdn_qlinear_forward, "
+                         "hidden 2048 -> q|k|v|z|b|a 12352) over --layers layers instead")
+    ap.add_argument("--qlinear-rows", type=int, default=0,
+                    help="rows (tokens) per qlinear launch; default --batch (decode)")
     ap.add_argument("--seed", type=int, default=0)
     return ap.parse_args(argv)
 
@@ -189,6 +194,129 @@ def prefill_bench(args):
         return 1
     print(json.dumps(out), flush=True)
     return 0
+
+
+# Merged GDN input projection of Qwen3.5-35B-A3B (hidden 2048): in_proj_qkv
+# (2*Hk*Dk + Hv*Dv rows), in_proj_z (Hv*Dv), in_proj_b, in_proj_a (Hv each).
+QL_HIDDEN = 2048
+QL_PARTS = [D, HV * DV, HV, HV]
+
+
+def qlinear_bench(args):
+    """gdn_qlinear_forward on the merged q|k|v|z|b|a layer: `layers` distinct
+    weight sets (426 MB at 30 layers, more than the 256 MB memory-side cache,
+    so weights stream from HBM) and one launch per layer per step, inputs
+    resident in HBM. Decode-sized launches (M = batch) are HBM-bound on the
+    packed weights; prefill-sized ones (M in the thousands) are bound by the
+    bf16 MFMA rate. Prints one JSON line."""
+    import torch
+
+    import gdn_amd
+    dev = torch.device("cuda:0")
+    L, Kd = args.layers, QL_HIDDEN
+    M = args.qlinear_rows or args.batch
+    N = sum(QL_PARTS)
+    G = Kd // 64
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    layers = []
+    for _ in range(L):
+        parts = []
+        for n in QL_PARTS:
+            w = torch.randint(-2**31, 2**31 - 1, (n, Kd // 8), generator=gen, device=dev,
+                              dtype=torch.int32)
+            sc = (torch.rand((n, G), generator=gen, device=dev) * 0.01 + 0.001).to(torch.bfloat16)
+            bi = (torch.randn((n, G), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+            parts.append((w, sc, bi))
+        layers.append(gdn_amd.QLinear(Kd, parts))
+        del parts
+    nsets = 2
+    x = [torch.randn((M, Kd), generator=gen, device=dev).to(torch.bfloat16) for _ in range(nsets)]
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+
+    def step(i, events=None):
+        if events is not None:
+            events[0].record()
+        for l in range(L):
+            layers[l].forward(x[(i + l) % nsets], y)
+        if events is not None:
+            events[1].record()
+
+    steps = args.steps if M <= 256 else max(3, min(args.steps, 20))
+    for i in range(max(2, min(args.warmup, 8))):
+        step(i)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(i, ev[i])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    avg_ms = sum(a.elapsed_time(b) for a, b in ev) / (steps * L)
+    wbytes = N * Kd // 2 + 2 * N * G * 2            # packed nibbles + scales + biases
+    iobytes = M * Kd * 2 + M * N * 2
+    flops = 2.0 * M * N * Kd
+    decode = M <= 256
+    if decode:
+        achieved = (wbytes + iobytes) / (avg_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                "algorithmic_bytes_per_launch": wbytes + iobytes}
+    else:
+        tf = flops / (avg_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                "flop_per_launch": flops}
+    roof.update({"kernel": "qlinear_kernel<4,1,1,4>" if M <= 64 else "qlinear_kernel<4,4,2,2>",
+                 "kernel_avg_us": round(avg_ms * 1e3, 2),
+                 "kernel_timing": "HIP events around each step's back-to-back launches / launches"})
+    out = {
+        "metric": "GDN input projection (4-bit merged q|k|v|z|b|a) tokens/s, all layers",
+        "value": round(M * steps / elapsed, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "ms_per_step": round(elapsed / steps * 1e3, 4),
+        "higher_is_better": True,
+        "dtype": "bf16 x 4-bit affine weights, f32 accumulation",
+        "data": "synthetic",
+        "config": {"workload": f"{M} rows x hidden {Kd} -> {N} outputs per layer, {L} layers, "
+                               "MLX affine 4-bit group 64",
+                   "rows": M, "hidden": Kd, "outputs": N, "layers": L},
+        "roofline": roof,
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = qlinear_cpu_baseline(args.cpu_seconds, L)
+    for q in layers:
+        q.close()
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def qlinear_cpu_baseline(seconds: float, layers: int):
+    """The oracle's quantized matmul (float64, OpenMP over outputs) on 8-row
+    slices of the same layer shape, repeated for about `seconds`; reported per
+    token through `layers` layers like the GPU figure."""
+    import numpy as np
+    from oracle import oracle as O
+    rng = np.random.default_rng(3)
+    N = sum(QL_PARTS)
+    w = rng.integers(0, 2**32, (N, QL_HIDDEN // 8), dtype=np.uint64).astype(np.uint32)
+    sc = O.f32_to_bf16((rng.random((N, QL_HIDDEN // 64)) * 0.01).astype(np.float32))
+    bi = O.f32_to_bf16((rng.standard_normal((N, QL_HIDDEN // 64)) * 0.02).astype(np.float32))
+    x = O.f32_to_bf16(rng.standard_normal((8, QL_HIDDEN)).astype(np.float32))
+    n, t0 = 0, time.perf_counter()
+    while True:
+        O.qmatmul_w4(x, w, sc, bi)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 200:
+            break
+    return {"value": round(8 * n / el / layers, 3), "unit": "tokens/s", "cores": O.num_threads(),
+            "kind": "port",
+            "sample": f"{n} x 8-row slices through one {QL_HIDDEN}->{N} layer ({el:.1f} s), "
+                      f"scaled to {layers} layers, "
+                      f"float64 oracle, {O.num_threads()} threads, {_cpu_model()}"}
 
 
 class Workload:
@@ -332,6 +460,8 @@ def main(argv=None):
         return 0
     if args.prefill:
         return prefill_bench(args)
+    if args.qlinear:
+        return qlinear_bench(args)
     w = Workload(args)
     for _ in range(args.warmup):
         w.step()

@@ -175,15 +175,17 @@ gdn_status gdn_decode(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
  * reads the merged projection rows as the reference produces them
  * (qwen3_5.rs:572-577): qkvz [B, row_stride] bf16 holds q|k|v in columns
  * [0, D) and z in columns [D, D + Hv*Dv), row_stride >= D + Hv*Dv, so no copy
- * of either part is needed. norm_w [Dv] bf16 (the layer's norm.weight),
+ * of either part is needed; ab [B, ab_stride] holds b|a in its first 2*Hv
+ * columns (ab_stride >= 2*Hv; a view into a merged projection output works as
+ * the reference's ab slices do, qwen3_5.rs:580-584). norm_w [Dv] bf16 (the layer's norm.weight),
  * norm_eps the model's rms_norm_eps. out [B, Hv, Dv] bf16 is the out_proj
  * input; y [B, Hv, Dv] (the ungated recurrence output) may be NULL. Same state
  * updates as gdn_decode. */
 gdn_status gdn_decode_gated(gdn_pool* pool, int32_t layer, const int32_t* slot_ids, int32_t B,
                             const uint16_t* qkvz, int64_t row_stride, const uint16_t* ab,
-                            const float* A_log, const float* dt_bias, const uint16_t* conv_w,
-                            const uint16_t* norm_w, float norm_eps, uint16_t* out, uint16_t* y,
-                            void* stream);
+                            int64_t ab_stride, const float* A_log, const float* dt_bias,
+                            const uint16_t* conv_w, const uint16_t* norm_w, float norm_eps,
+                            uint16_t* out, uint16_t* y, void* stream);
 
 /* Varlen prefill of nseq sequences packed along the token axis
  * (qwen3_5.rs:611-658 with S>1; the reference runs them one at a time, B=1):
@@ -203,6 +205,46 @@ gdn_status gdn_prefill_varlen(gdn_pool* pool, int32_t layer, const int32_t* slot
                               const uint16_t* ab, const float* A_log,
                               const float* dt_bias, const uint16_t* conv_w,
                               uint16_t* y, void* stream);
+
+/* ------------------------------------------------------------------------
+ * 4-bit affine-quantized linear layer: the GDN block's input projections.
+ *
+ * Replaces mlx_rs::ops::quantized_matmul(x, w, scales, biases, transpose=true,
+ * group_size=64, bits=4) on the merged projection weights
+ * (qwen3_5.rs:572-586), including the load-time merge of the parts along the
+ * output axis (qwen3_5.rs:1023-1053: qkv|z into merged_qkvz, b|a into
+ * merged_ab). Weight format as MLX stores it: w uint32 [N_i, K/8] with element
+ * k of row n in bits 4*(k%8) of word k/8; scales, biases bf16 [N_i, K/64];
+ * dequantized weight = scales * q + biases.
+ *
+ * y[m, n] = sum_k x[m, k] * w[n, k], computed exactly up to f32 accumulation
+ * and rounded once to bf16.
+ * ------------------------------------------------------------------------ */
+typedef struct gdn_qlinear gdn_qlinear;
+
+/* Merge nparts MLX-format parts (device pointers, part i has part_rows[i]
+ * output rows) into one layer with N = sum(part_rows) outputs and repack it
+ * for the kernel on `device`. The layer owns its memory (about N*K/2 +
+ * 3*N*K/32 bytes); the sources are only read, and may be freed once this
+ * returns (it synchronises `stream`). Supported: bits 4, group_size 64,
+ * K a multiple of 512 up to 4096, part_rows multiples of 16. */
+gdn_status gdn_qlinear_create(int32_t K, int32_t nparts, const int32_t* part_rows,
+                              const uint32_t* const* w, const uint16_t* const* scales,
+                              const uint16_t* const* biases, int32_t group_size, int32_t bits,
+                              int32_t device, void* stream, gdn_qlinear** out);
+gdn_status gdn_qlinear_destroy(gdn_qlinear* layer);
+
+/* Input width K and output width N of a layer. */
+gdn_status gdn_qlinear_dims(const gdn_qlinear* layer, int32_t* K, int32_t* N);
+
+/* y [M, y_stride] bf16 = x [M, x_stride] bf16 . W^T over the first N columns
+ * (columns past N untouched). x: 16-byte aligned, x_stride >= K and a
+ * multiple of 8; y: 8-byte aligned, y_stride >= N and a multiple of 4;
+ * M <= 8,388,480. Allocates nothing. For the merged qkv|z|b|a layer the
+ * output row is [q|k|v|z|b|a], which gdn_decode_gated reads in place
+ * (qkvz = y, row_stride = y_stride; ab = y + D + Hv*Dv, ab_stride = y_stride). */
+gdn_status gdn_qlinear_forward(const gdn_qlinear* layer, const uint16_t* x, int64_t x_stride,
+                               int32_t M, uint16_t* y, int64_t y_stride, void* stream);
 
 #ifdef __cplusplus
 }

@@ -398,6 +398,91 @@ void orc_prefill(uint16_t* conv_state, float* state, const uint16_t* mixed_qkv,
   free(xc); free(q); free(k); free(v); free(beta); free(g);
 }
 
+/* ------------------------------------------------ quantized matmul ----- */
+
+/*
+ * mlx::core::quantized_matmul(x, w, scales, biases, transpose=true,
+ * group_size=64, bits=4) as the reference calls it on the merged GDN input
+ * projections (src/models/qwen3_5.rs:572-586, weights merged along the output
+ * axis at :1037-1053) and the lm_head (:869-874). The operation lives in the
+ * MLX dependency (mlx-rs 0.25.3 over mlx-sys 0.2.0, not vendored); its
+ * published affine 4-bit format is restated here:
+ *   w uint32 [N, K/8]: element k of row n is the nibble at bits 4*(k%8) of
+ *   word k/8; scales, biases [N, K/64] (bf16 here); dequantized weight
+ *   W[n,k] = scales[n,k/64] * q[n,k] + biases[n,k/64]   (mlx dequantize,
+ *   used by the reference at qwen3_5.rs:852).
+ * orc_dequant_w4 writes W in f64 (exact). orc_qmatmul_w4 forms
+ *   y_exact[m,n] = sum_k x[m,k] W[n,k] in f64 (the dequantized weight is
+ *   never rounded), y = y_exact correctly rounded to bf16 (round to odd to
+ *   f32, then to nearest even: no double-rounding error), and
+ *   mag[m,n] = sum_k |x[m,k]| (|s| (128 + q) + |b|), a scale for checkers'
+ *   f32-accumulation bounds. MLX's own kernels accumulate in f32 (and its
+ *   large-M path rounds the dequantized weight to bf16 first), so a result
+ *   within f32 accumulation error of y_exact, rounded once, is as close as any
+ *   implementation of this contract gets. Any pointer among y_exact, mag, y
+ *   may be NULL.
+ */
+static inline uint16_t f64_to_bf16(double d) {
+  float f = (float)d;
+  if ((double)f != d && isfinite(f)) {  /* round to odd: truncate, set the sticky bit */
+    if (fabs((double)f) > fabs(d)) f = nextafterf(f, 0.0f);
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    u |= 1u;
+    memcpy(&f, &u, 4);
+  }
+  return f2bf(f);
+}
+
+uint16_t orc_f64_to_bf16(double d) { return f64_to_bf16(d); }
+
+void orc_dequant_w4(const uint32_t* w, const uint16_t* s, const uint16_t* b, int N, int K,
+                    double* out) {
+  const int words = K / 8, G = K / 64;
+#pragma omp parallel for schedule(static)
+  for (int n = 0; n < N; ++n)
+    for (int k = 0; k < K; ++k) {
+      const uint32_t q = (w[(int64_t)n * words + k / 8] >> (4 * (k % 8))) & 0xFu;
+      out[(int64_t)n * K + k] =
+          (double)bf2f(s[(int64_t)n * G + k / 64]) * (double)q + (double)bf2f(b[(int64_t)n * G + k / 64]);
+    }
+}
+
+void orc_qmatmul_w4(const uint16_t* x, int64_t xs, int M, int K, const uint32_t* w,
+                    const uint16_t* s, const uint16_t* b, int N, double* y_exact, double* mag,
+                    uint16_t* y) {
+  const int words = K / 8, G = K / 64;
+#pragma omp parallel
+  {
+    double* wr = (double*)malloc(sizeof(double) * K);
+    double* wa = (double*)malloc(sizeof(double) * K);
+#pragma omp for schedule(static)
+    for (int n = 0; n < N; ++n) {
+      for (int k = 0; k < K; ++k) {
+        const uint32_t q = (w[(int64_t)n * words + k / 8] >> (4 * (k % 8))) & 0xFu;
+        const double sc = bf2f(s[(int64_t)n * G + k / 64]), bi = bf2f(b[(int64_t)n * G + k / 64]);
+        wr[k] = sc * (double)q + bi;
+        wa[k] = fabs(sc) * (128.0 + (double)q) + fabs(bi);
+      }
+      for (int m = 0; m < M; ++m) {
+        const uint16_t* xr = x + (int64_t)m * xs;
+        double acc = 0.0, am = 0.0;
+        for (int k = 0; k < K; ++k) {
+          const double xv = bf2f(xr[k]);
+          acc += xv * wr[k];
+          am += fabs(xv) * wa[k];
+        }
+        const int64_t o = (int64_t)m * N + n;
+        if (y_exact) y_exact[o] = acc;
+        if (mag) mag[o] = am;
+        if (y) y[o] = f64_to_bf16(acc);
+      }
+    }
+    free(wr);
+    free(wa);
+  }
+}
+
 /* ---------------------------------------------------- stack/unstack ----- */
 
 /*

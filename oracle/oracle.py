@@ -24,6 +24,7 @@ _u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
 _i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_u32p = np.ctypeslib.ndpointer(dtype=np.uint32, flags="C_CONTIGUOUS")
 _c_int, _c_i64, _c_float = ctypes.c_int, ctypes.c_int64, ctypes.c_float
 
 
@@ -58,6 +59,11 @@ def lib():
     L.orc_prefill.argtypes = [_u16p, _f32p, _u16p, _u16p, _f32p, _f32p, _u16p, _u16p,
                               _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]
     L.orc_num_threads.restype = _c_int
+    L.orc_f64_to_bf16.argtypes = [ctypes.c_double]
+    L.orc_f64_to_bf16.restype = ctypes.c_uint16
+    L.orc_dequant_w4.argtypes = [_u32p, _u16p, _u16p, _c_int, _c_int, _f64p]
+    L.orc_qmatmul_w4.argtypes = [_u16p, _c_i64, _c_int, _c_int, _u32p, _u16p, _u16p, _c_int,
+                                 _f64p, _f64p, _u16p]
     L.orc_baseline_step.restype = None
     _lib = L
     return L
@@ -225,6 +231,37 @@ def split_qkv(x, Hk: int, Hv: int, Dk: int, Dv: int):
     k = x[..., qk:2 * qk].reshape(x.shape[:-1] + (Hk, Dk))
     v = x[..., 2 * qk:].reshape(x.shape[:-1] + (Hv, Dv))
     return q, k, v
+
+
+def f64_to_bf16(v: float) -> int:
+    """Correctly rounded (nearest even) bf16 bits of a float64."""
+    return int(lib().orc_f64_to_bf16(float(v)))
+
+
+def dequant_w4(w, scales, biases):
+    """MLX affine 4-bit dequantize, group 64 (qwen3_5.rs:852): w uint32 [N, K/8],
+    scales/biases bf16 [N, K/64] -> float64 [N, K] (exact)."""
+    w = np.ascontiguousarray(w, np.uint32)
+    N, K = w.shape[0], w.shape[1] * 8
+    out = np.empty((N, K), np.float64)
+    lib().orc_dequant_w4(w, _c(scales, np.uint16), _c(biases, np.uint16), N, K, out)
+    return out
+
+
+def qmatmul_w4(x, w, scales, biases):
+    """quantized_matmul(x, w, scales, biases, transpose=True, group_size=64,
+    bits=4) (qwen3_5.rs:572-586): x bf16 [M, K] -> (y bf16 [M, N] correctly
+    rounded, y_exact float64 [M, N], mag float64 [M, N] = sum |x|(|s|(128+q)+|b|))."""
+    x = _c(x, np.uint16)
+    w = np.ascontiguousarray(w, np.uint32)
+    M, K = x.shape
+    N = w.shape[0]
+    assert w.shape[1] * 8 == K and K % 64 == 0
+    ye = np.empty((M, N), np.float64)
+    mag = np.empty((M, N), np.float64)
+    y = np.empty((M, N), np.uint16)
+    lib().orc_qmatmul_w4(x, K, M, K, w, _c(scales, np.uint16), _c(biases, np.uint16), N, ye, mag, y)
+    return y, ye, mag
 
 
 def stack(pool, slot_ids):

@@ -331,6 +331,8 @@ gdn_status gdn_recurrent(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
 
 // Token tiles of 64 run along the grid's y axis (at most 65535).
 constexpr int32_t kMaxPrefillTokens = 65535 * 64;
+// qlinear rows per call: 65535 tiles of 128 rows
+constexpr int32_t kMaxQLinearRows = 65535 * 128;
 
 // Grows the pool's prefill workspace to at least `need` bytes. Growing waits
 // for the stream, so work still reading the old buffer has finished.
@@ -355,9 +357,9 @@ static gdn_status ensure_workspace(gdn_pool* pool, size_t need, void* stream, co
 // Shared checks and launch of the fused decode (gdn_decode, gdn_decode_gated).
 static gdn_status decode_common(gdn_pool* pool, int32_t layer, const int32_t* slot_ids, int32_t B,
                                 const uint16_t* qkv, int64_t xstride, const uint16_t* ab,
-                                const float* A_log, const float* dt_bias, const uint16_t* conv_w,
-                                uint16_t* y, const uint16_t* norm_w, float norm_eps, uint16_t* out,
-                                void* stream, const char* who) {
+                                int64_t ab_stride, const float* A_log, const float* dt_bias,
+                                const uint16_t* conv_w, uint16_t* y, const uint16_t* norm_w,
+                                float norm_eps, uint16_t* out, void* stream, const char* who) {
   gdn_status st = check_layer(pool, layer, false);
   if (st) return st;
   if (B < 0) return fail(GDN_ERR_INVALID, "%s: B = %d < 0", who, B);
@@ -382,6 +384,7 @@ static gdn_status decode_common(gdn_pool* pool, int32_t layer, const int32_t* sl
   a.mixed = qkv;
   a.xstride = xstride;
   a.ab = ab;
+  a.ab_stride = ab_stride;
   a.A_log = A_log;
   a.dt_bias = dt_bias;
   a.conv_w = conv_w;
@@ -400,27 +403,31 @@ gdn_status gdn_decode(gdn_pool* pool, int32_t layer, const int32_t* slot_ids, in
                       const uint16_t* mixed_qkv, const uint16_t* ab, const float* A_log,
                       const float* dt_bias, const uint16_t* conv_w, uint16_t* y, void* stream) {
   if (!y && B > 0) return fail(GDN_ERR_INVALID, "gdn_decode: NULL tensor pointer");
-  return decode_common(pool, layer, slot_ids, B, mixed_qkv, pool ? pool->D : 0, ab, A_log,
-                       dt_bias, conv_w, y, nullptr, 0.0f, nullptr, stream, "gdn_decode");
+  return decode_common(pool, layer, slot_ids, B, mixed_qkv, pool ? pool->D : 0, ab,
+                       pool ? 2 * pool->d.num_v_heads : 0, A_log, dt_bias, conv_w, y, nullptr,
+                       0.0f, nullptr, stream, "gdn_decode");
 }
 
 gdn_status gdn_decode_gated(gdn_pool* pool, int32_t layer, const int32_t* slot_ids, int32_t B,
                             const uint16_t* qkvz, int64_t row_stride, const uint16_t* ab,
-                            const float* A_log, const float* dt_bias, const uint16_t* conv_w,
-                            const uint16_t* norm_w, float norm_eps, uint16_t* out, uint16_t* y,
-                            void* stream) {
+                            int64_t ab_stride, const float* A_log, const float* dt_bias,
+                            const uint16_t* conv_w, const uint16_t* norm_w, float norm_eps,
+                            uint16_t* out, uint16_t* y, void* stream) {
   if (pool) {
     const int64_t need = (int64_t)pool->D + (int64_t)pool->d.num_v_heads * pool->d.head_v_dim;
     if (row_stride < need)
       return fail(GDN_ERR_INVALID, "gdn_decode_gated: row_stride %lld < D + Hv*Dv = %lld",
                   (long long)row_stride, (long long)need);
+    if (ab_stride < 2 * pool->d.num_v_heads)
+      return fail(GDN_ERR_INVALID, "gdn_decode_gated: ab_stride %lld < 2*Hv = %d",
+                  (long long)ab_stride, 2 * pool->d.num_v_heads);
   }
   if (B > 0 && (!norm_w || !out))
     return fail(GDN_ERR_INVALID, "gdn_decode_gated: NULL norm_w / out");
   if (!(norm_eps >= 0.0f))
     return fail(GDN_ERR_INVALID, "gdn_decode_gated: norm_eps must be >= 0");
-  return decode_common(pool, layer, slot_ids, B, qkvz, row_stride, ab, A_log, dt_bias, conv_w, y,
-                       norm_w, norm_eps, out, stream, "gdn_decode_gated");
+  return decode_common(pool, layer, slot_ids, B, qkvz, row_stride, ab, ab_stride, A_log, dt_bias,
+                       conv_w, y, norm_w, norm_eps, out, stream, "gdn_decode_gated");
 }
 
 gdn_status gdn_prefill_varlen(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
@@ -469,6 +476,154 @@ gdn_status gdn_prefill_varlen(gdn_pool* pool, int32_t layer, const int32_t* slot
   a.stream = as_stream(stream);
   hipError_t e = gdn::launch_prefill(a);
   if (e != hipSuccess) return hip_fail(e, "gdn_prefill_varlen launch");
+  return GDN_OK;
+}
+
+
+// ------------------------------------------------------------ qlinear --
+
+struct gdn_qlinear {
+  int K = 0, N = 0, Npad = 0, G = 0, device = 0;
+  void* wp = nullptr;        // packed weights [Npad/16][K/128][64][4] u32
+  uint16_t* sp = nullptr;    // packed scales  [Npad/16][K/128][16][2] bf16
+  uint16_t* bias = nullptr;  // [Npad, G] bf16
+  uint16_t* nsc = nullptr;   // [Npad, G] bf16, -128 * scales
+};
+
+static void qlinear_release(gdn_qlinear* q) {
+  if (!q) return;
+  if (q->wp) (void)hipFree(q->wp);
+  if (q->sp) (void)hipFree(q->sp);
+  if (q->bias) (void)hipFree(q->bias);
+  if (q->nsc) (void)hipFree(q->nsc);
+  delete q;
+}
+
+gdn_status gdn_qlinear_create(int32_t K, int32_t nparts, const int32_t* part_rows,
+                              const uint32_t* const* w, const uint16_t* const* scales,
+                              const uint16_t* const* biases, int32_t group_size, int32_t bits,
+                              int32_t device, void* stream, gdn_qlinear** out) {
+  if (!out) return fail(GDN_ERR_INVALID, "gdn_qlinear_create: out is NULL");
+  *out = nullptr;
+  if (bits != 4 || group_size != 64)
+    return fail(GDN_ERR_UNSUPPORTED, "gdn_qlinear_create: bits = %d, group_size = %d (need 4, 64)",
+                bits, group_size);
+  if (K <= 0 || K % 512 != 0 || K > 4096)
+    return fail(GDN_ERR_UNSUPPORTED, "gdn_qlinear_create: K = %d must be a multiple of 512 in "
+                "[512, 4096]", K);
+  if (nparts < 1 || nparts > 64 || !part_rows || !w || !scales || !biases)
+    return fail(GDN_ERR_INVALID, "gdn_qlinear_create: nparts = %d / NULL part arrays", nparts);
+  int64_t N = 0;
+  for (int i = 0; i < nparts; ++i) {
+    if (part_rows[i] <= 0 || part_rows[i] % 16 != 0)
+      return fail(GDN_ERR_UNSUPPORTED, "gdn_qlinear_create: part %d has %d rows (need a positive "
+                  "multiple of 16)", i, part_rows[i]);
+    if (!w[i] || !scales[i] || !biases[i])
+      return fail(GDN_ERR_INVALID, "gdn_qlinear_create: part %d has a NULL tensor", i);
+    N += part_rows[i];
+  }
+  if (N > (1 << 24)) return fail(GDN_ERR_INVALID, "gdn_qlinear_create: %lld rows", (long long)N);
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev)
+    return fail(GDN_ERR_INVALID, "gdn_qlinear_create: device %d not present", device);
+  DeviceGuard guard(device);
+  if (!guard.ok()) return fail(GDN_ERR_HIP, "gdn_qlinear_create: hipSetDevice(%d) failed", device);
+
+  gdn_qlinear* q = new gdn_qlinear();
+  q->K = K;
+  q->N = (int)N;
+  q->Npad = (int)((N + 127) / 128 * 128);
+  q->G = K / 64;
+  q->device = device;
+  const size_t wbytes = (size_t)q->Npad * K / 2, gbytes = (size_t)q->Npad * q->G * 2;
+  if (hipMalloc(&q->wp, wbytes) != hipSuccess || hipMalloc(&q->sp, gbytes) != hipSuccess ||
+      hipMalloc(&q->bias, gbytes) != hipSuccess || hipMalloc(&q->nsc, gbytes) != hipSuccess) {
+    qlinear_release(q);
+    return fail(GDN_ERR_OOM, "gdn_qlinear_create: hipMalloc of %zu bytes failed",
+                wbytes + 3 * gbytes);
+  }
+  hipStream_t s = as_stream(stream);
+  hipError_t e;
+  if ((e = hipMemsetAsync(q->wp, 0, wbytes, s)) != hipSuccess ||
+      (e = hipMemsetAsync(q->sp, 0, gbytes, s)) != hipSuccess ||
+      (e = hipMemsetAsync(q->bias, 0, gbytes, s)) != hipSuccess ||
+      (e = hipMemsetAsync(q->nsc, 0, gbytes, s)) != hipSuccess) {
+    qlinear_release(q);
+    return hip_fail(e, "gdn_qlinear_create: clear");
+  }
+  int frag = 0;
+  for (int i = 0; i < nparts; ++i) {
+    gdn::QLinearPackArgs a{};
+    a.w = w[i];
+    a.s = scales[i];
+    a.b = biases[i];
+    a.N = part_rows[i];
+    a.K = K;
+    a.frag0 = frag;
+    a.wp = q->wp;
+    a.sp = q->sp;
+    a.bias = q->bias;
+    a.nsc = q->nsc;
+    a.stream = s;
+    if ((e = gdn::launch_qlinear_pack(a)) != hipSuccess) {
+      qlinear_release(q);
+      return hip_fail(e, "gdn_qlinear_create: pack");
+    }
+    frag += part_rows[i] / 16;
+  }
+  if ((e = hipStreamSynchronize(s)) != hipSuccess) {
+    qlinear_release(q);
+    return hip_fail(e, "gdn_qlinear_create: synchronize");
+  }
+  *out = q;
+  return GDN_OK;
+}
+
+gdn_status gdn_qlinear_destroy(gdn_qlinear* q) {
+  if (!q) return GDN_OK;
+  DeviceGuard guard(q->device);
+  qlinear_release(q);
+  return GDN_OK;
+}
+
+gdn_status gdn_qlinear_dims(const gdn_qlinear* q, int32_t* K, int32_t* N) {
+  if (!q) return fail(GDN_ERR_INVALID, "gdn_qlinear_dims: NULL layer");
+  if (K) *K = q->K;
+  if (N) *N = q->N;
+  return GDN_OK;
+}
+
+gdn_status gdn_qlinear_forward(const gdn_qlinear* q, const uint16_t* x, int64_t x_stride,
+                               int32_t M, uint16_t* y, int64_t y_stride, void* stream) {
+  if (!q) return fail(GDN_ERR_INVALID, "gdn_qlinear_forward: NULL layer");
+  if (M < 0) return fail(GDN_ERR_INVALID, "gdn_qlinear_forward: M = %d < 0", M);
+  if (M == 0) return GDN_OK;
+  if (M > kMaxQLinearRows)
+    return fail(GDN_ERR_INVALID, "gdn_qlinear_forward: M = %d > %d", M, kMaxQLinearRows);
+  if (!x || !y) return fail(GDN_ERR_INVALID, "gdn_qlinear_forward: NULL tensor pointer");
+  if (x_stride < q->K || x_stride % 8 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0)
+    return fail(GDN_ERR_INVALID, "gdn_qlinear_forward: x needs 16-byte alignment and a row "
+                "stride >= K that is a multiple of 8 (got %lld)", (long long)x_stride);
+  if (y_stride < q->N || y_stride % 4 != 0 || reinterpret_cast<uintptr_t>(y) % 8 != 0)
+    return fail(GDN_ERR_INVALID, "gdn_qlinear_forward: y needs 8-byte alignment and a row "
+                "stride >= N that is a multiple of 4 (got %lld)", (long long)y_stride);
+  DeviceGuard guard(q->device);
+  gdn::QLinearArgs a{};
+  a.x = x;
+  a.xs = x_stride;
+  a.M = M;
+  a.K = q->K;
+  a.N = q->N;
+  a.Npad = q->Npad;
+  a.wp = q->wp;
+  a.sp = q->sp;
+  a.bias = q->bias;
+  a.nsc = q->nsc;
+  a.y = y;
+  a.ys = y_stride;
+  a.stream = as_stream(stream);
+  hipError_t e = gdn::launch_qlinear(a);
+  if (e != hipSuccess) return hip_fail(e, "gdn_qlinear_forward launch");
   return GDN_OK;
 }
 

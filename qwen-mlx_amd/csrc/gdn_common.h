@@ -124,6 +124,7 @@ struct DecodeArgs {
   const uint16_t* mixed;   // [B, xstride] rows: q|k|v in the first D columns (then z if gated)
   int64_t xstride;         // row stride of mixed in elements (D, or the merged qkvz width)
   const uint16_t* ab;
+  int64_t ab_stride;       // row stride of ab in elements (>= 2*Hv)
   const float* A_log;
   const float* dt_bias;
   const uint16_t* conv_w;
@@ -178,6 +179,35 @@ struct PrefillArgs {
   size_t workspace_bytes;
   hipStream_t stream;
 };
+
+// 4-bit affine-quantized linear layer (gdn_qlinear.hip).
+struct QLinearPackArgs {
+  const uint32_t* w;  // MLX part: [N, K/8]
+  const uint16_t* s;  // [N, K/64]
+  const uint16_t* b;  // [N, K/64]
+  int N, K, frag0;    // part rows, input width, first 16-row fragment in the merged matrix
+  void* wp;           // packed weights of the merged matrix
+  uint16_t* sp;       // packed scales
+  uint16_t* bias;     // [Npad, K/64]
+  uint16_t* nsc;      // [Npad, K/64] = -128 * scales
+  hipStream_t stream;
+};
+
+struct QLinearArgs {
+  const uint16_t* x;  // [M, xs] bf16
+  int64_t xs;
+  int M, K, N, Npad;
+  const void* wp;
+  const uint16_t* sp;
+  const uint16_t* bias;
+  const uint16_t* nsc;
+  uint16_t* y;        // [M, ys] bf16
+  int64_t ys;
+  hipStream_t stream;
+};
+
+hipError_t launch_qlinear_pack(const QLinearPackArgs& a);
+hipError_t launch_qlinear(const QLinearArgs& a);
 
 hipError_t launch_decode(const DecodeArgs& a);
 hipError_t launch_recurrent(const RecurrentArgs& a);

@@ -198,7 +198,7 @@ template <int R, bool GATED>
 __global__ __launch_bounds__(256 * R) void decode_kernel(
     float* __restrict__ state, uint16_t* __restrict__ conv, const int32_t* __restrict__ slot_ids,
     int num_slots, int Hk, const uint16_t* __restrict__ mixed, int64_t xstride,
-    const uint16_t* __restrict__ ab, const float* __restrict__ A_log,
+    const uint16_t* __restrict__ ab, int64_t ab_stride, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, const uint16_t* __restrict__ conv_w,
     uint16_t* __restrict__ y, const uint16_t* __restrict__ norm_w, float norm_eps,
     uint16_t* __restrict__ out, uint32_t* __restrict__ status) {
@@ -250,7 +250,7 @@ __global__ __launch_bounds__(256 * R) void decode_kernel(
   }
   const int gr = tid & (R - 1), gh = hk * R + gr;
   const float alog = A_log[gh], dtb = dt_bias[gh];
-  const uint16_t braw = ab[(size_t)b * 2 * Hv + gh], araw = ab[(size_t)b * 2 * Hv + Hv + gh];
+  const uint16_t braw = ab[(size_t)b * ab_stride + gh], araw = ab[(size_t)b * ab_stride + Hv + gh];
   // gate inputs of (head hk*R + e/Dv, row e%Dv), e = t mod R*Dv: z follows
   // q|k|v in the merged row, so the R heads' z are contiguous
   uint16_t zr = 0, wr = 0;
@@ -364,11 +364,11 @@ template <int R>
 static hipError_t launch_decode_r(const DecodeArgs& a) {
   if (a.out)
     hipLaunchKernelGGL((decode_kernel<R, true>), dim3(a.Hk, a.B), dim3(256 * R), 0, a.stream,
-                       a.state, a.conv, a.slot_ids, a.num_slots, a.Hk, a.mixed, a.xstride, a.ab,
+                       a.state, a.conv, a.slot_ids, a.num_slots, a.Hk, a.mixed, a.xstride, a.ab, a.ab_stride,
                        a.A_log, a.dt_bias, a.conv_w, a.y, a.norm_w, a.norm_eps, a.out, a.status);
   else
     hipLaunchKernelGGL((decode_kernel<R, false>), dim3(a.Hk, a.B), dim3(256 * R), 0, a.stream,
-                       a.state, a.conv, a.slot_ids, a.num_slots, a.Hk, a.mixed, a.xstride, a.ab,
+                       a.state, a.conv, a.slot_ids, a.num_slots, a.Hk, a.mixed, a.xstride, a.ab, a.ab_stride,
                        a.A_log, a.dt_bias, a.conv_w, a.y, a.norm_w, a.norm_eps, a.out, a.status);
   return hipGetLastError();
 }

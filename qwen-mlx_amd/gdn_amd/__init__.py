@@ -47,10 +47,16 @@ SIGNATURES = {
     "gdn_recurrent": ([_VP, _I32, _VP, _I32, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _VP],
                       ctypes.c_int),
     "gdn_decode": ([_VP, _I32, _VP, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _VP], ctypes.c_int),
-    "gdn_decode_gated": ([_VP, _I32, _VP, _I32, _VP, ctypes.c_int64, _VP, _VP, _VP, _VP, _VP,
-                          ctypes.c_float, _VP, _VP, _VP], ctypes.c_int),
+    "gdn_decode_gated": ([_VP, _I32, _VP, _I32, _VP, ctypes.c_int64, _VP, ctypes.c_int64, _VP,
+                          _VP, _VP, _VP, ctypes.c_float, _VP, _VP, _VP], ctypes.c_int),
     "gdn_prefill_varlen": ([_VP, _I32, _VP, _VP, _I32, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _VP],
                            ctypes.c_int),
+    "gdn_qlinear_create": ([_I32, _I32, _VP, _VP, _VP, _VP, _I32, _I32, _I32, _VP,
+                            ctypes.POINTER(_VP)], ctypes.c_int),
+    "gdn_qlinear_destroy": ([_VP], ctypes.c_int),
+    "gdn_qlinear_dims": ([_VP, ctypes.POINTER(_I32), ctypes.POINTER(_I32)], ctypes.c_int),
+    "gdn_qlinear_forward": ([_VP, _VP, ctypes.c_int64, _I32, _VP, ctypes.c_int64, _VP],
+                            ctypes.c_int),
 }
 
 
@@ -111,6 +117,16 @@ def _ptr(t) -> int | None:
     if not t.is_contiguous():
         raise ValueError("libgdn takes contiguous tensors")
     return t.data_ptr()
+
+
+def _rows(t) -> tuple[int, int]:
+    """(pointer, row stride in elements) of a 2-D device tensor whose rows are
+    contiguous (a column slice of a wider matrix is fine)."""
+    if not t.is_cuda:
+        raise ValueError("libgdn takes device tensors")
+    if t.dim() != 2 or (t.shape[1] > 1 and t.stride(1) != 1):
+        raise ValueError("expected a 2-D tensor with contiguous rows")
+    return t.data_ptr(), t.stride(0)
 
 
 def _stream(stream) -> int | None:
@@ -211,14 +227,15 @@ class Pool:
 
     def decode_gated(self, layer, slot_ids, qkvz, ab, A_log, dt_bias, conv_w, norm_w, norm_eps,
                      out, y=None, stream=None):
-        """Decode with the RMSNormGated epilogue. qkvz: [B, row_stride] rows holding
-        q|k|v then z (the merged projection output); out (and optional y) [B,Hv,Dv]."""
-        if qkvz.dim() != 2:
-            raise ValueError("qkvz must be [B, row_stride]")
+        """Decode with the RMSNormGated epilogue. qkvz: [B, >= D + Hv*Dv] rows holding
+        q|k|v then z, ab: [B, >= 2*Hv] rows holding b|a; either may be a column
+        slice of the merged projection output. out (and optional y) [B,Hv,Dv]."""
+        xp, xs = _rows(qkvz)
+        ap, as_ = _rows(ab)
         _check(self.lib.gdn_decode_gated(self.handle, layer, _ptr(slot_ids), slot_ids.numel(),
-                                         _ptr(qkvz), qkvz.shape[1], _ptr(ab), _ptr(A_log),
-                                         _ptr(dt_bias), _ptr(conv_w), _ptr(norm_w),
-                                         float(norm_eps), _ptr(out), _ptr(y), _stream(stream)))
+                                         xp, xs, ap, as_, _ptr(A_log), _ptr(dt_bias),
+                                         _ptr(conv_w), _ptr(norm_w), float(norm_eps), _ptr(out),
+                                         _ptr(y), _stream(stream)))
 
     def prefill(self, layer, slot_ids, cu_seqlens, total_tokens, mixed_qkv, ab, A_log, dt_bias,
                 conv_w, y, stream=None):
@@ -226,6 +243,53 @@ class Pool:
                                            slot_ids.numel(), total_tokens, _ptr(mixed_qkv),
                                            _ptr(ab), _ptr(A_log), _ptr(dt_bias), _ptr(conv_w),
                                            _ptr(y), _stream(stream)))
+
+
+class QLinear:
+    """4-bit affine-quantized linear layer (MLX format, group 64) built from one
+    or more weight parts merged along the output axis, e.g. the GDN block's
+    [in_proj_qkv, in_proj_z, in_proj_b, in_proj_a]. parts: list of (w uint32
+    [N_i, K/8], scales [N_i, K/64], biases [N_i, K/64]) device tensors (bf16 as
+    torch.bfloat16 or int16 bit patterns; uint32 as int32 bit patterns)."""
+
+    def __init__(self, K: int, parts, device: int = 0, stream=None, group_size: int = 64,
+                 bits: int = 4):
+        self.lib = load()
+        n = len(parts)
+        rows = (_I32 * n)(*[int(p[0].shape[0]) for p in parts])
+        ws = (_VP * n)(*[_ptr(p[0]) for p in parts])
+        ss = (_VP * n)(*[_ptr(p[1]) for p in parts])
+        bs = (_VP * n)(*[_ptr(p[2]) for p in parts])
+        h = _VP()
+        _check(self.lib.gdn_qlinear_create(K, n, rows, ws, ss, bs, group_size, bits, device,
+                                           _stream(stream), ctypes.byref(h)))
+        self.handle = h
+        k, nn = _I32(), _I32()
+        _check(self.lib.gdn_qlinear_dims(h, ctypes.byref(k), ctypes.byref(nn)))
+        self.K, self.N = k.value, nn.value
+        self.device = device
+
+    def forward(self, x, y, stream=None):
+        """y[:, :N] = x . W^T; x [M, >= K], y [M, >= N], rows contiguous."""
+        xp, xs = _rows(x)
+        yp, ys = _rows(y)
+        if y.shape[0] != x.shape[0]:
+            raise ValueError("x and y row counts differ")
+        if x.shape[1] < self.K or y.shape[1] < self.N:
+            raise ValueError(f"need x [M, >= {self.K}] and y [M, >= {self.N}]")
+        _check(self.lib.gdn_qlinear_forward(self.handle, xp, xs, x.shape[0], yp, ys,
+                                            _stream(stream)))
+
+    def close(self):
+        if getattr(self, "handle", None):
+            _check(self.lib.gdn_qlinear_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def _wrap_device(ptr: int, numel: int, dtype, device: int):

@@ -148,6 +148,36 @@ def np_conv_depthwise(padded, w):
     return out
 
 
+def quantize_w4(wf):
+    """Test-data generator: affine 4-bit quantization of float weights [N, K] in
+    groups of 64 into MLX's storage format. Per group scale = (max - min) / 15
+    and bias = min, both rounded to bf16; q = clip(rint((w - bias) / scale), 0,
+    15); eight nibbles per uint32 with element k at bits 4*(k % 8). Returns
+    (w uint32 [N, K/8], scales uint16 [N, K/64], biases uint16 [N, K/64])."""
+    wf = np.asarray(wf, np.float64)
+    N, Kd = wf.shape
+    g = wf.reshape(N, Kd // 64, 64)
+    lo, hi = g.min(-1), g.max(-1)
+    s = O.f32_to_bf16(((hi - lo) / 15.0).astype(np.float32))
+    b = O.f32_to_bf16(lo.astype(np.float32))
+    sf = O.bf16_to_f32(s).astype(np.float64)
+    bf = O.bf16_to_f32(b).astype(np.float64)
+    q = np.clip(np.rint((g - bf[..., None]) / np.where(sf == 0, 1.0, sf)[..., None]), 0, 15)
+    q = q.astype(np.uint32).reshape(N, Kd // 8, 8)
+    w = np.bitwise_or.reduce(q << (4 * np.arange(8, dtype=np.uint32)), axis=-1).astype(np.uint32)
+    return w, s, b
+
+
+def unpack_w4_bytes(w):
+    """Nibbles of MLX 4-bit words read byte by byte (little-endian words: byte j
+    holds elements 2j (low nibble) and 2j+1 (high nibble)): uint8 [N, K]."""
+    by = np.ascontiguousarray(w, "<u4").view(np.uint8).reshape(w.shape[0], -1)
+    out = np.empty((w.shape[0], by.shape[1] * 2), np.uint8)
+    out[:, 0::2] = by & 0xF
+    out[:, 1::2] = by >> 4
+    return out
+
+
 def rel_l2(a, b):
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)

@@ -56,3 +56,28 @@ def test_product_has_no_cpu_fallback():
     import torch
     with pytest.raises(ValueError):
         gdn_amd._ptr(torch.zeros(4))
+
+
+def test_qlinear_rejects_unsupported_formats_on_host():
+    """gdn_qlinear_create checks format and shapes before touching a device."""
+    lib = gdn_amd.load()
+    h = ctypes.c_void_p()
+    fake = ctypes.c_void_p(0x1000)
+    rows = (ctypes.c_int32 * 1)(16)
+    ptrs = (ctypes.c_void_p * 1)(fake)
+
+    def create(K, rows_, gs=64, bits=4, n=1):
+        return lib.gdn_qlinear_create(K, n, rows_, ptrs, ptrs, ptrs, gs, bits, 0, None,
+                                      ctypes.byref(h))
+
+    assert create(2048, rows, bits=8) == gdn_amd.GDN_ERR_UNSUPPORTED
+    assert create(2048, rows, gs=32) == gdn_amd.GDN_ERR_UNSUPPORTED
+    assert create(1000, rows) == gdn_amd.GDN_ERR_UNSUPPORTED       # K % 512
+    assert create(8192, rows) == gdn_amd.GDN_ERR_UNSUPPORTED       # K > 4096
+    assert create(2048, (ctypes.c_int32 * 1)(24)) == gdn_amd.GDN_ERR_UNSUPPORTED  # rows % 16
+    assert create(2048, rows, n=0) == gdn_amd.GDN_ERR_INVALID
+    assert h.value is None
+    assert lib.gdn_qlinear_create(2048, 1, rows, ptrs, ptrs, ptrs, 64, 4, 0, None, None) \
+        == gdn_amd.GDN_ERR_INVALID
+    assert lib.gdn_qlinear_forward(None, None, 0, 1, None, 0, None) == gdn_amd.GDN_ERR_INVALID
+    assert lib.gdn_qlinear_destroy(None) == gdn_amd.GDN_OK

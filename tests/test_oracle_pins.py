@@ -14,7 +14,7 @@ import pytest
 
 from gdn_testlib import (O, DK, DV, K, conv_dim, f64, gen_recurrent_inputs, gen_layer_params,
                          gen_states, gen_tokens, np_chunked_one_head, np_conv_depthwise,
-                         np_recurrent_dkdv, rel_l2)
+                         np_recurrent_dkdv, quantize_w4, rel_l2, unpack_w4_bytes)
 
 
 # ------------------------------------------------------------------ bf16 --
@@ -381,3 +381,94 @@ def test_stack_unstack_are_gather_scatter():
     assert np.array_equal(new[[7, 2, 9]], pool[[7, 2, 9]] * 2)
     untouched = [i for i in range(10) if i not in (7, 2, 9)]
     assert np.array_equal(new[untouched], pool[untouched])
+
+
+# ------------------------------------------------ 4-bit quantized matmul --
+# quantized_matmul(x, w, scales, biases, transpose, group 64, bits 4)
+# (qwen3_5.rs:572-586). MLX is not importable here; the oracle's reading of
+# the MLX storage format and of the operation is pinned below by hand-built
+# words, a byte-wise re-reading of the nibbles, a quantize round trip and
+# brute force, and its bf16 rounding by ties built to expose double rounding.
+
+def _bf(v):
+    return int(np.ravel(O.f32_to_bf16(np.array([v], np.float32)))[0])
+
+
+def test_w4_dequant_known_words_and_affine_direction():
+    w = np.array([[0x76543210, 0xFEDCBA98] * 4], np.uint32)  # K = 64: one group
+    s = np.array([[_bf(2.0)]], np.uint16)
+    b = np.array([[_bf(-3.0)]], np.uint16)
+    d = O.dequant_w4(w, s, b)
+    q = np.tile(np.arange(16), 4)
+    assert np.array_equal(d[0], 2.0 * q - 3.0)  # scale * q + bias, element k at bits 4*(k%8)
+
+
+def test_w4_dequant_matches_bytewise_unpack_and_group_indexing():
+    rng = np.random.default_rng(40)
+    N, Kd = 48, 512
+    w = rng.integers(0, 2**32, (N, Kd // 8), dtype=np.uint64).astype(np.uint32)
+    s = O.f32_to_bf16(rng.standard_normal((N, Kd // 64)).astype(np.float32))
+    b = O.f32_to_bf16(rng.standard_normal((N, Kd // 64)).astype(np.float32))
+    q = unpack_w4_bytes(w).astype(np.float64)
+    sf = np.repeat(O.bf16_to_f32(s).astype(np.float64), 64, axis=1)
+    bf = np.repeat(O.bf16_to_f32(b).astype(np.float64), 64, axis=1)
+    assert np.array_equal(O.dequant_w4(w, s, b), sf * q + bf)
+
+
+def test_w4_quantize_round_trip_within_half_step():
+    rng = np.random.default_rng(41)
+    wf = rng.standard_normal((32, 1024)) * 0.02
+    w, s, b = quantize_w4(wf)
+    d = O.dequant_w4(w, s, b)
+    step = np.repeat(O.bf16_to_f32(s).astype(np.float64), 64, axis=1)
+    # half a step from rounding q, plus the bf16 rounding of the group minimum
+    # and of the step (at most 15 steps' worth of it)
+    slack = np.repeat(np.abs(O.bf16_to_f32(b)).astype(np.float64), 64, axis=1) * 2.0**-8
+    assert np.all(np.abs(d - wf) <= 0.5 * step + 15 * step * 2.0**-8 + slack)
+
+
+def _rne_bf16_exact(v):
+    """Independent nearest-even bf16 of a float64 (frexp arithmetic is exact)."""
+    import math
+    if v == 0.0:
+        return 0x8000 if math.copysign(1.0, v) < 0 else 0
+    m, e = math.frexp(abs(v))          # v = m 2^e, m in [0.5, 1)
+    t = m * 256.0                      # 8 significant bits above the point
+    f = math.floor(t)
+    r = t - f
+    if r > 0.5 or (r == 0.5 and f % 2 == 1):
+        f += 1
+    mag = f * 2.0 ** (e - 8)
+    return _bf(math.copysign(mag, v))
+
+
+def test_qmatmul_w4_brute_force_and_rounding():
+    rng = np.random.default_rng(42)
+    M, N, Kd = 5, 32, 512
+    x = O.f32_to_bf16(rng.standard_normal((M, Kd)).astype(np.float32))
+    w, s, b = quantize_w4(rng.standard_normal((N, Kd)) * 0.05)
+    y, ye, mag = O.qmatmul_w4(x, w, s, b)
+    W = (np.repeat(O.bf16_to_f32(s).astype(np.float64), 64, axis=1) * unpack_w4_bytes(w)
+         + np.repeat(O.bf16_to_f32(b).astype(np.float64), 64, axis=1))
+    ref = O.bf16_to_f32(x).astype(np.float64) @ W.T
+    assert np.allclose(ye, ref, rtol=1e-12, atol=1e-12)
+    assert all(int(y.flat[i]) == _rne_bf16_exact(float(ye.flat[i])) for i in range(y.size))
+    assert np.all(mag >= np.abs(ye))
+
+
+def test_qmatmul_w4_ties_round_once():
+    """y = 1 + 2^-8 is a bf16 tie (to even: 1.0); 1 + 2^-8 + 2^-40 lies just
+    above it (1 + 2^-7). Rounding to f32 first with round-to-nearest would give
+    1.0 for both."""
+    Kd = 128
+    words = np.zeros((1, Kd // 8), np.uint32)
+    words[0, 0] = 1                                   # q[0] = 1, every other q = 0
+    s = np.array([[_bf(2.0**-8), 0]], np.uint16)      # group 0: w[0] = 2^-8, rest 0
+    b = np.array([[0, _bf(1.0)]], np.uint16)          # group 1: w = 0 * q + 1 = 1
+    x = np.zeros((2, Kd), np.uint16)
+    x[:, 0] = _bf(1.0)
+    x[:, 64] = _bf(1.0)
+    x[1, 65] = _bf(2.0**-40)
+    y, ye, _ = O.qmatmul_w4(x, words, s, b)
+    assert ye[0, 0] == 1.0 + 2.0**-8 and int(y[0, 0]) == 0x3F80
+    assert ye[1, 0] == 1.0 + 2.0**-8 + 2.0**-40 and int(y[1, 0]) == 0x3F81
