@@ -38,23 +38,17 @@ __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-// (v & m) | e in one v_and_or_b32. gfx950 VOP3 takes no literal and at most
-// one scalar operand, so the mask comes in a VGPR and the exponent bits in an
-// SGPR; written out because the compiler otherwise splits it into v_and +
-// v_or with two literals.
-__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t m, uint32_t e) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "v"(m), "s"(e));
-  return r;
-}
-
 // One packed dword (nibble order k0 k2 k4 k6 k1 k3 k5 k7 of eight consecutive
 // k) -> the MFMA operand dwords (128+q_k0, 128+q_k1), ..., (128+q_k6, 128+q_k7).
-// m = 0x000F000F (in a VGPR), e = 0x43004300.
+// m = 0x000F000F held in a VGPR: with one literal left, (v & m) | e selects a
+// single v_and_or_b32 (gfx950 VOP3 takes no literal, the exponent bits go in
+// an SGPR); with both constants literal the compiler emits v_and + v_or.
+// (Written in C, not inline asm: the hazard recognizer cannot see into inline
+// asm, and a VALU write into a VGPR an in-flight MFMA still reads as its
+// accumulator input needs wait states it then does not insert.)
 __device__ __forceinline__ u32x4 unpack_w(uint32_t w, uint32_t m) {
   const uint32_t e = 0x43004300u;
-  return (u32x4){and_or(w, m, e), and_or(w >> 4, m, e), and_or(w >> 8, m, e),
-                 and_or(w >> 12, m, e)};
+  return (u32x4){(w & m) | e, ((w >> 4) & m) | e, ((w >> 8) & m) | e, ((w >> 12) & m) | e};
 }
 
 // Packed layout written by qlinear_pack_kernel, per 16-row fragment f and
