@@ -206,6 +206,21 @@ gdn_status gdn_prefill_varlen(gdn_pool* pool, int32_t layer, const int32_t* slot
                               const float* dt_bias, const uint16_t* conv_w,
                               uint16_t* y, void* stream);
 
+/* gdn_prefill_varlen on merged projection rows with the RMSNormGated epilogue
+ * fused into the chunk kernel's readout (qwen3_5.rs:660-665 after the S>1
+ * path): out [total_tokens, Hv, Dv] = silu(z) * rms_norm(y, norm_w, norm_eps)
+ * per (token, value head). qkvz [total_tokens, row_stride] holds q|k|v in
+ * columns [0, D) and z in [D, D + Hv*Dv) (row_stride >= D + Hv*Dv, a multiple
+ * of 8, qkvz 16-byte aligned); ab [total_tokens, ab_stride] holds b|a in its
+ * first 2*Hv columns. y [total_tokens, Hv, Dv] (the ungated output) may be
+ * NULL. Same state updates as gdn_prefill_varlen. */
+gdn_status gdn_prefill_varlen_gated(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
+                                    const int32_t* cu_seqlens, int32_t nseq, int32_t total_tokens,
+                                    const uint16_t* qkvz, int64_t row_stride, const uint16_t* ab,
+                                    int64_t ab_stride, const float* A_log, const float* dt_bias,
+                                    const uint16_t* conv_w, const uint16_t* norm_w,
+                                    float norm_eps, uint16_t* out, uint16_t* y, void* stream);
+
 /* ------------------------------------------------------------------------
  * 4-bit affine-quantized linear layer: the GDN block's input projections.
  *
@@ -245,6 +260,58 @@ gdn_status gdn_qlinear_dims(const gdn_qlinear* layer, int32_t* K, int32_t* N);
  * (qkvz = y, row_stride = y_stride; ab = y + D + Hv*Dv, ab_stride = y_stride). */
 gdn_status gdn_qlinear_forward(const gdn_qlinear* layer, const uint16_t* x, int64_t x_stride,
                                int32_t M, uint16_t* y, int64_t y_stride, void* stream);
+
+/* ------------------------------------------------------------------------
+ * One GatedDeltaNet layer end to end: GatedDeltaNet::forward_with_cache
+ * (qwen3_5.rs:558-668) with the (conv_state, recurrent_state) cache pair
+ * replaced by pool slots:
+ *   proj = in_proj(x)                          [q|k|v|z|b|a], one gdn_qlinear_forward
+ *   gated = gdn_decode_gated / gdn_prefill_varlen_gated on column views of proj
+ *   out = out_proj(gated)                      one gdn_qlinear_forward
+ * x and out are hidden-size bf16 rows (the decoder layer's input_layernorm
+ * output and the mixer output the residual adds, qwen3_5.rs DecoderLayer).
+ * The layer keeps pointers only: the pool, the two projections and the
+ * weight tensors must outlive it. Activations go to a buffer held by the
+ * pool (shared by every layer of the pool, so the pool's calls are ordered
+ * on one stream): a call needing more of it than any earlier call
+ * synchronises its stream and grows it; gdn_pool_reserve sizes it (and the
+ * prefill workspace) up front so later calls allocate nothing.
+ * ------------------------------------------------------------------------ */
+typedef struct gdn_layer gdn_layer;
+
+typedef struct gdn_layer_desc {
+  gdn_pool* pool;
+  int32_t layer;                /* this layer's state arrays in the pool      */
+  const gdn_qlinear* in_proj;   /* merged q|k|v|z|b|a: N = D + Hv*Dv + 2*Hv,
+                                   K = hidden size (qwen3_5.rs:1037-1053)     */
+  const gdn_qlinear* out_proj;  /* Hv*Dv -> hidden size (qwen3_5.rs:668)     */
+  const float* A_log;           /* [Hv] f32                                   */
+  const float* dt_bias;         /* [Hv] f32                                   */
+  const uint16_t* conv_w;       /* [D, K] bf16, 8-byte aligned                */
+  const uint16_t* norm_w;       /* [Dv] bf16 (linear_attn.norm.weight)        */
+  float norm_eps;               /* rms_norm_eps                               */
+} gdn_layer_desc;
+
+gdn_status gdn_layer_create(const gdn_layer_desc* desc, gdn_layer** out);
+gdn_status gdn_layer_destroy(gdn_layer* layer);
+
+/* Size the pool's activation buffer and prefill workspace for calls of up
+ * to max_tokens tokens (decode batch size or packed prefill tokens). */
+gdn_status gdn_pool_reserve(gdn_pool* pool, int32_t max_tokens, void* stream);
+
+/* S = 1 step of B sequences: x [B, x_stride] -> out [B, out_stride], state of
+ * slot_ids[B] updated in place. x: 16-byte aligned, x_stride a multiple of 8;
+ * out: 8-byte aligned, out_stride a multiple of 4; both strides >= hidden. */
+gdn_status gdn_layer_decode(gdn_layer* layer, const int32_t* slot_ids, int32_t B,
+                            const uint16_t* x, int64_t x_stride, uint16_t* out,
+                            int64_t out_stride, void* stream);
+
+/* Varlen prefill of nseq packed sequences (cu_seqlens as gdn_prefill_varlen):
+ * x [total_tokens, x_stride] -> out [total_tokens, out_stride]. */
+gdn_status gdn_layer_prefill(gdn_layer* layer, const int32_t* slot_ids,
+                             const int32_t* cu_seqlens, int32_t nseq, int32_t total_tokens,
+                             const uint16_t* x, int64_t x_stride, uint16_t* out,
+                             int64_t out_stride, void* stream);
 
 #ifdef __cplusplus
 }

@@ -63,6 +63,8 @@ struct gdn_pool {
   uint32_t* d_status = nullptr;
   void* workspace = nullptr;
   size_t workspace_bytes = 0;
+  void* act = nullptr;  // gdn_layer_* activations: projection rows, gated rows
+  size_t act_bytes = 0;
   std::set<int32_t> free_slots;
   std::vector<uint8_t> in_use;
 };
@@ -78,6 +80,7 @@ void release(gdn_pool* p) {
   if (p->d_conv_ptrs) (void)hipFree(p->d_conv_ptrs);
   if (p->d_status) (void)hipFree(p->d_status);
   if (p->workspace) (void)hipFree(p->workspace);
+  if (p->act) (void)hipFree(p->act);
   delete p;
 }
 
@@ -334,24 +337,29 @@ constexpr int32_t kMaxPrefillTokens = 65535 * 64;
 // qlinear rows per call: 65535 tiles of 128 rows
 constexpr int32_t kMaxQLinearRows = 65535 * 128;
 
-// Grows the pool's prefill workspace to at least `need` bytes. Growing waits
+// Grows a pool-held device buffer to at least `need` bytes. Growing waits
 // for the stream, so work still reading the old buffer has finished.
-static gdn_status ensure_workspace(gdn_pool* pool, size_t need, void* stream, const char* what) {
-  if (need <= pool->workspace_bytes) return GDN_OK;
-  if (pool->workspace) {
+static gdn_status ensure_buffer(void*& buf, size_t& bytes, size_t need, void* stream,
+                                const char* what) {
+  if (need <= bytes) return GDN_OK;
+  if (buf) {
     hipError_t e = hipStreamSynchronize(as_stream(stream));
     if (e != hipSuccess) return hip_fail(e, "workspace grow sync");
-    (void)hipFree(pool->workspace);
-    pool->workspace = nullptr;
-    pool->workspace_bytes = 0;
+    (void)hipFree(buf);
+    buf = nullptr;
+    bytes = 0;
   }
-  if (hipMalloc(&pool->workspace, need) != hipSuccess) {
+  if (hipMalloc(&buf, need) != hipSuccess) {
     (void)hipGetLastError();
-    pool->workspace = nullptr;
+    buf = nullptr;
     return fail(GDN_ERR_OOM, "%s workspace of %zu bytes", what, need);
   }
-  pool->workspace_bytes = need;
+  bytes = need;
   return GDN_OK;
+}
+
+static gdn_status ensure_workspace(gdn_pool* pool, size_t need, void* stream, const char* what) {
+  return ensure_buffer(pool->workspace, pool->workspace_bytes, need, stream, what);
 }
 
 // Shared checks and launch of the fused decode (gdn_decode, gdn_decode_gated).
@@ -430,26 +438,33 @@ gdn_status gdn_decode_gated(gdn_pool* pool, int32_t layer, const int32_t* slot_i
                        conv_w, y, norm_w, norm_eps, out, stream, "gdn_decode_gated");
 }
 
-gdn_status gdn_prefill_varlen(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
-                              const int32_t* cu_seqlens, int32_t nseq, int32_t total_tokens,
-                              const uint16_t* mixed_qkv, const uint16_t* ab, const float* A_log,
-                              const float* dt_bias, const uint16_t* conv_w, uint16_t* y,
-                              void* stream) {
+// Shared checks and launches of the varlen prefill (gdn_prefill_varlen,
+// gdn_prefill_varlen_gated).
+static gdn_status prefill_common(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
+                                 const int32_t* cu_seqlens, int32_t nseq, int32_t total_tokens,
+                                 const uint16_t* qkv, int64_t xstride, const uint16_t* ab,
+                                 int64_t ab_stride, const float* A_log, const float* dt_bias,
+                                 const uint16_t* conv_w, uint16_t* y, const uint16_t* norm_w,
+                                 float norm_eps, uint16_t* out, void* stream, const char* who) {
   gdn_status st = check_layer(pool, layer, false);
   if (st) return st;
   if (nseq < 0 || total_tokens < 0)
-    return fail(GDN_ERR_INVALID, "nseq = %d, total_tokens = %d must be >= 0", nseq, total_tokens);
+    return fail(GDN_ERR_INVALID, "%s: nseq = %d, total_tokens = %d must be >= 0", who, nseq,
+                total_tokens);
   if (nseq == 0) return GDN_OK;
-  if (nseq > 65535) return fail(GDN_ERR_INVALID, "nseq = %d > 65535", nseq);
+  if (nseq > 65535) return fail(GDN_ERR_INVALID, "%s: nseq = %d > 65535", who, nseq);
   if (total_tokens > kMaxPrefillTokens)
-    return fail(GDN_ERR_INVALID, "total_tokens = %d > %d per call", total_tokens,
+    return fail(GDN_ERR_INVALID, "%s: total_tokens = %d > %d per call", who, total_tokens,
                 kMaxPrefillTokens);
   if (!slot_ids || !cu_seqlens || !A_log || !dt_bias || !conv_w)
-    return fail(GDN_ERR_INVALID, "gdn_prefill_varlen: NULL pointer");
-  if (total_tokens > 0 && (!mixed_qkv || !ab || !y))
-    return fail(GDN_ERR_INVALID, "gdn_prefill_varlen: NULL token tensor");
+    return fail(GDN_ERR_INVALID, "%s: NULL pointer", who);
+  if (total_tokens > 0 && (!qkv || !ab || (!y && !out)))
+    return fail(GDN_ERR_INVALID, "%s: NULL token tensor", who);
   if (reinterpret_cast<uintptr_t>(conv_w) % 8 != 0)
-    return fail(GDN_ERR_INVALID, "gdn_prefill_varlen: conv_w must be 8-byte aligned");
+    return fail(GDN_ERR_INVALID, "%s: conv_w must be 8-byte aligned", who);
+  if (reinterpret_cast<uintptr_t>(qkv) % 16 != 0 || xstride % 8 != 0)
+    return fail(GDN_ERR_INVALID, "%s: token rows must be 16-byte aligned (pointer %% 16 == 0, "
+                "row stride %% 8 == 0)", who);
   DeviceGuard guard(pool->d.device);
   st = ensure_workspace(pool, gdn::prefill_workspace_bytes(pool->R, pool->d.num_k_heads, total_tokens),
                         stream, "prefill");
@@ -464,19 +479,60 @@ gdn_status gdn_prefill_varlen(gdn_pool* pool, int32_t layer, const int32_t* slot
   a.conv = pool->conv[layer];
   a.slot_ids = slot_ids;
   a.cu_seqlens = cu_seqlens;
-  a.mixed = mixed_qkv;
+  a.mixed = qkv;
+  a.xstride = xstride;
   a.ab = ab;
+  a.ab_stride = ab_stride;
   a.A_log = A_log;
   a.dt_bias = dt_bias;
   a.conv_w = conv_w;
   a.y = y;
+  a.norm_w = norm_w;
+  a.norm_eps = norm_eps;
+  a.out = out;
   a.status = pool->d_status;
   a.workspace = pool->workspace;
   a.workspace_bytes = pool->workspace_bytes;
   a.stream = as_stream(stream);
   hipError_t e = gdn::launch_prefill(a);
-  if (e != hipSuccess) return hip_fail(e, "gdn_prefill_varlen launch");
+  if (e != hipSuccess) return hip_fail(e, who);
   return GDN_OK;
+}
+
+gdn_status gdn_prefill_varlen(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
+                              const int32_t* cu_seqlens, int32_t nseq, int32_t total_tokens,
+                              const uint16_t* mixed_qkv, const uint16_t* ab, const float* A_log,
+                              const float* dt_bias, const uint16_t* conv_w, uint16_t* y,
+                              void* stream) {
+  if (!y && total_tokens > 0 && nseq > 0)
+    return fail(GDN_ERR_INVALID, "gdn_prefill_varlen: NULL token tensor");
+  return prefill_common(pool, layer, slot_ids, cu_seqlens, nseq, total_tokens, mixed_qkv,
+                        pool ? pool->D : 0, ab, pool ? 2 * pool->d.num_v_heads : 0, A_log, dt_bias,
+                        conv_w, y, nullptr, 0.0f, nullptr, stream, "gdn_prefill_varlen");
+}
+
+gdn_status gdn_prefill_varlen_gated(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
+                                    const int32_t* cu_seqlens, int32_t nseq, int32_t total_tokens,
+                                    const uint16_t* qkvz, int64_t row_stride, const uint16_t* ab,
+                                    int64_t ab_stride, const float* A_log, const float* dt_bias,
+                                    const uint16_t* conv_w, const uint16_t* norm_w,
+                                    float norm_eps, uint16_t* out, uint16_t* y, void* stream) {
+  if (pool) {
+    const int64_t need = (int64_t)pool->D + (int64_t)pool->d.num_v_heads * pool->d.head_v_dim;
+    if (row_stride < need)
+      return fail(GDN_ERR_INVALID, "gdn_prefill_varlen_gated: row_stride %lld < D + Hv*Dv = %lld",
+                  (long long)row_stride, (long long)need);
+    if (ab_stride < 2 * pool->d.num_v_heads)
+      return fail(GDN_ERR_INVALID, "gdn_prefill_varlen_gated: ab_stride %lld < 2*Hv = %d",
+                  (long long)ab_stride, 2 * pool->d.num_v_heads);
+  }
+  if (nseq > 0 && total_tokens > 0 && (!norm_w || !out))
+    return fail(GDN_ERR_INVALID, "gdn_prefill_varlen_gated: NULL norm_w / out");
+  if (!(norm_eps >= 0.0f))
+    return fail(GDN_ERR_INVALID, "gdn_prefill_varlen_gated: norm_eps must be >= 0");
+  return prefill_common(pool, layer, slot_ids, cu_seqlens, nseq, total_tokens, qkvz, row_stride,
+                        ab, ab_stride, A_log, dt_bias, conv_w, y, norm_w, norm_eps,
+                        out, stream, "gdn_prefill_varlen_gated");
 }
 
 
@@ -625,6 +681,173 @@ gdn_status gdn_qlinear_forward(const gdn_qlinear* q, const uint16_t* x, int64_t 
   hipError_t e = gdn::launch_qlinear(a);
   if (e != hipSuccess) return hip_fail(e, "gdn_qlinear_forward launch");
   return GDN_OK;
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------ gdn_layer --
+// One GatedDeltaNet layer end to end (GatedDeltaNet::forward_with_cache,
+// qwen3_5.rs:558-668): merged input projection -> conv / norm / gates /
+// recurrence / RMSNormGated -> out_proj. Three launches per call (four with
+// prefill's conv-state and chunk kernels); activations live in the pool's
+// activation buffer.
+struct gdn_layer {
+  gdn_pool* pool = nullptr;
+  int32_t layer = 0;
+  const gdn_qlinear* in_proj = nullptr;
+  const gdn_qlinear* out_proj = nullptr;
+  const float* A_log = nullptr;
+  const float* dt_bias = nullptr;
+  const uint16_t* conv_w = nullptr;
+  const uint16_t* norm_w = nullptr;
+  float norm_eps = 0.0f;
+  int64_t proj_stride = 0;  // row stride of the projection rows (N rounded up to 8)
+};
+
+namespace {
+
+// Bytes of activations for ntok tokens: projection rows [ntok, proj_stride]
+// then gated rows [ntok, Hv*Dv], both bf16 (the second starts 16-byte aligned
+// because proj_stride is a multiple of 8).
+size_t layer_act_bytes(const gdn_pool* p, int64_t ntok) {
+  const int64_t n = (int64_t)p->D + 2LL * p->d.num_v_heads * p->d.head_v_dim + 2 * p->d.num_v_heads;
+  const int64_t stride = (n + 7) & ~7LL;
+  return (size_t)ntok * (size_t)(stride + (int64_t)p->d.num_v_heads * p->d.head_v_dim) * 2;
+}
+
+gdn_status layer_args(const gdn_layer* L, const uint16_t* x, int64_t x_stride, uint16_t* out,
+                      int64_t out_stride, const char* who) {
+  if (!L) return fail(GDN_ERR_INVALID, "%s: NULL layer", who);
+  if (!x || !out) return fail(GDN_ERR_INVALID, "%s: NULL x / out", who);
+  const int hidden = L->in_proj->K;
+  if (x_stride < hidden || out_stride < hidden)
+    return fail(GDN_ERR_INVALID, "%s: row strides (%lld, %lld) below the hidden size %d", who,
+                (long long)x_stride, (long long)out_stride, hidden);
+  return GDN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+gdn_status gdn_layer_create(const gdn_layer_desc* desc, gdn_layer** out) {
+  if (!desc || !out) return fail(GDN_ERR_INVALID, "gdn_layer_create: desc/out is NULL");
+  *out = nullptr;
+  const gdn_layer_desc& d = *desc;
+  gdn_status st = check_layer(d.pool, d.layer, false);
+  if (st) return st;
+  if (!d.in_proj || !d.out_proj || !d.A_log || !d.dt_bias || !d.conv_w || !d.norm_w)
+    return fail(GDN_ERR_INVALID, "gdn_layer_create: NULL weight");
+  if (reinterpret_cast<uintptr_t>(d.conv_w) % 8 != 0)
+    return fail(GDN_ERR_INVALID, "gdn_layer_create: conv_w must be 8-byte aligned");
+  if (!(d.norm_eps >= 0.0f)) return fail(GDN_ERR_INVALID, "gdn_layer_create: norm_eps < 0");
+  const gdn_pool* p = d.pool;
+  const int Hv = p->d.num_v_heads, value = Hv * p->d.head_v_dim;
+  const int n_in = p->D + value + 2 * Hv;
+  if (d.in_proj->N != n_in)
+    return fail(GDN_ERR_INVALID, "gdn_layer_create: in_proj has %d outputs, the layer needs "
+                "D + Hv*Dv + 2*Hv = %d (q|k|v|z|b|a)", d.in_proj->N, n_in);
+  if (d.out_proj->K != value)
+    return fail(GDN_ERR_INVALID, "gdn_layer_create: out_proj input width %d != Hv*Dv = %d",
+                d.out_proj->K, value);
+  if (d.out_proj->N != d.in_proj->K)
+    return fail(GDN_ERR_INVALID, "gdn_layer_create: out_proj width %d != in_proj input width %d",
+                d.out_proj->N, d.in_proj->K);
+  if (d.in_proj->device != p->d.device || d.out_proj->device != p->d.device)
+    return fail(GDN_ERR_INVALID, "gdn_layer_create: projections and pool on different devices");
+  gdn_layer* L = new gdn_layer;
+  L->pool = d.pool;
+  L->layer = d.layer;
+  L->in_proj = d.in_proj;
+  L->out_proj = d.out_proj;
+  L->A_log = d.A_log;
+  L->dt_bias = d.dt_bias;
+  L->conv_w = d.conv_w;
+  L->norm_w = d.norm_w;
+  L->norm_eps = d.norm_eps;
+  L->proj_stride = ((int64_t)n_in + 7) & ~7LL;
+  *out = L;
+  return GDN_OK;
+}
+
+gdn_status gdn_layer_destroy(gdn_layer* layer) {
+  delete layer;
+  return GDN_OK;
+}
+
+gdn_status gdn_pool_reserve(gdn_pool* pool, int32_t max_tokens, void* stream) {
+  gdn_status st = check_layer(pool, 0, false);
+  if (st) return st;
+  if (max_tokens < 0 || max_tokens > kMaxPrefillTokens)
+    return fail(GDN_ERR_INVALID, "gdn_pool_reserve: max_tokens = %d outside [0, %d]", max_tokens,
+                kMaxPrefillTokens);
+  DeviceGuard guard(pool->d.device);
+  st = ensure_buffer(pool->act, pool->act_bytes, layer_act_bytes(pool, max_tokens), stream,
+                     "layer activation");
+  if (st) return st;
+  return ensure_workspace(pool, gdn::prefill_workspace_bytes(pool->R, pool->d.num_k_heads,
+                                                             max_tokens), stream, "prefill");
+}
+
+gdn_status gdn_layer_decode(gdn_layer* L, const int32_t* slot_ids, int32_t B, const uint16_t* x,
+                            int64_t x_stride, uint16_t* out, int64_t out_stride, void* stream) {
+  if (B == 0 && L) return GDN_OK;
+  gdn_status st = layer_args(L, x, x_stride, out, out_stride, "gdn_layer_decode");
+  if (st) return st;
+  gdn_pool* p = L->pool;
+  if (B < 0 || B > p->d.num_slots)
+    return fail(GDN_ERR_INVALID, "gdn_layer_decode: B = %d outside [0, num_slots = %d]", B,
+                p->d.num_slots);
+  {
+    DeviceGuard guard(p->d.device);
+    st = ensure_buffer(p->act, p->act_bytes, layer_act_bytes(p, B), stream, "layer activation");
+    if (st) return st;
+  }
+  const int64_t value = (int64_t)p->d.num_v_heads * p->d.head_v_dim;
+  uint16_t* proj = static_cast<uint16_t*>(p->act);
+  uint16_t* gated = proj + (size_t)B * L->proj_stride;
+  st = gdn_qlinear_forward(L->in_proj, x, x_stride, B, proj, L->proj_stride, stream);
+  if (st) return st;
+  st = gdn_decode_gated(p, L->layer, slot_ids, B, proj, L->proj_stride, proj + p->D + value,
+                        L->proj_stride, L->A_log, L->dt_bias, L->conv_w, L->norm_w, L->norm_eps,
+                        gated, nullptr, stream);
+  if (st) return st;
+  return gdn_qlinear_forward(L->out_proj, gated, value, B, out, out_stride, stream);
+}
+
+gdn_status gdn_layer_prefill(gdn_layer* L, const int32_t* slot_ids, const int32_t* cu_seqlens,
+                             int32_t nseq, int32_t total_tokens, const uint16_t* x,
+                             int64_t x_stride, uint16_t* out, int64_t out_stride, void* stream) {
+  if ((nseq == 0 || total_tokens == 0) && L && nseq >= 0 && total_tokens >= 0) {
+    if (nseq == 0) return GDN_OK;
+    // empty sequences only: no tokens to project, the slots keep their state
+    return gdn_prefill_varlen_gated(L->pool, L->layer, slot_ids, cu_seqlens, nseq, 0, nullptr,
+                                    L->proj_stride, nullptr, L->proj_stride, L->A_log, L->dt_bias,
+                                    L->conv_w, L->norm_w, L->norm_eps, nullptr, nullptr, stream);
+  }
+  gdn_status st = layer_args(L, x, x_stride, out, out_stride, "gdn_layer_prefill");
+  if (st) return st;
+  gdn_pool* p = L->pool;
+  if (total_tokens < 0 || total_tokens > kMaxPrefillTokens)
+    return fail(GDN_ERR_INVALID, "gdn_layer_prefill: total_tokens = %d outside [0, %d]",
+                total_tokens, kMaxPrefillTokens);
+  {
+    DeviceGuard guard(p->d.device);
+    st = ensure_buffer(p->act, p->act_bytes, layer_act_bytes(p, total_tokens), stream,
+                       "layer activation");
+    if (st) return st;
+  }
+  const int64_t value = (int64_t)p->d.num_v_heads * p->d.head_v_dim;
+  uint16_t* proj = static_cast<uint16_t*>(p->act);
+  uint16_t* gated = proj + (size_t)total_tokens * L->proj_stride;
+  st = gdn_qlinear_forward(L->in_proj, x, x_stride, total_tokens, proj, L->proj_stride, stream);
+  if (st) return st;
+  st = gdn_prefill_varlen_gated(p, L->layer, slot_ids, cu_seqlens, nseq, total_tokens, proj,
+                                L->proj_stride, proj + p->D + value, L->proj_stride, L->A_log,
+                                L->dt_bias, L->conv_w, L->norm_w, L->norm_eps, gated, nullptr,
+                                stream);
+  if (st) return st;
+  return gdn_qlinear_forward(L->out_proj, gated, value, total_tokens, out, out_stride, stream);
 }
 
 }  // extern "C"

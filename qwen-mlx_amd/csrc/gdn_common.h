@@ -81,6 +81,12 @@ __device__ __forceinline__ float sum8(float v) {
   return v;
 }
 
+// Sum over the 16 lanes of a DPP row (every lane receives the sum).
+__device__ __forceinline__ float sum16(float v) {
+  v = sum8(v);
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+}
+
 // Sum over a full 64-lane wave (result in every lane).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -168,12 +174,17 @@ struct PrefillArgs {
   uint16_t* conv;
   const int32_t* slot_ids;
   const int32_t* cu_seqlens;
-  const uint16_t* mixed;
-  const uint16_t* ab;
+  const uint16_t* mixed;  // [T, xstride]: q|k|v in columns [0, D), z (gated) in [D, D + Hv*Dv)
+  int64_t xstride;
+  const uint16_t* ab;     // [T, ab_stride]: b|a in the first 2*Hv columns
+  int64_t ab_stride;
   const float* A_log;
   const float* dt_bias;
   const uint16_t* conv_w;
-  uint16_t* y;
+  uint16_t* y;            // [T, Hv, Dv]; may be null when out is set
+  const uint16_t* norm_w; // RMSNormGated epilogue (out != null): weight [Dv], eps
+  float norm_eps;
+  uint16_t* out;          // [T, Hv, Dv] = silu(z) * rms_norm(y), or null
   uint32_t* status;
   void* workspace;       // device scratch sized by prefill_workspace_bytes
   size_t workspace_bytes;

@@ -53,12 +53,6 @@ __device__ __forceinline__ float dot4(const v4f& a, const v4f& b) {
   return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
 }
 
-// Sum over the 16 lanes of a DPP row (every lane receives the sum).
-__device__ __forceinline__ float sum16(float v) {
-  v = sum8(v);
-  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
-}
-
 // One token on the register tile. kl/ql: k and q of the token in LDS (Dk
 // floats each); vrow[i]: v at row grp+32i; kq = k.q over all of Dk. yrow[i]
 // gets the output of row grp+32i (identical in the 8 lanes of a row group).

@@ -91,8 +91,8 @@ template <int R>
 __global__ __launch_bounds__(256) void prefill_qkv_kernel(
     const uint16_t* __restrict__ conv, const int32_t* __restrict__ slot_ids,
     const int32_t* __restrict__ cu, int nseq, int num_slots, int Hk, int T,
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ conv_w,
-    const uint16_t* __restrict__ ab, const float* __restrict__ A_log,
+    const uint16_t* __restrict__ x, int64_t xs, const uint16_t* __restrict__ conv_w,
+    const uint16_t* __restrict__ ab, int64_t abs_, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, uint16_t* __restrict__ qn, uint16_t* __restrict__ kn,
     uint16_t* __restrict__ vc, uint16_t* __restrict__ beta, float* __restrict__ lg) {
   constexpr int KH = kConvK - 1;
@@ -108,7 +108,7 @@ __global__ __launch_bounds__(256) void prefill_qkv_kernel(
     const int r = e >> 4, c = e & 15, u = t0 - KH + r;
     u32x4 v = {0u, 0u, 0u, 0u};
     if (u >= 0 && u < T)
-      v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + (size_t)u * D + hcol) + c);
+      v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + (size_t)u * xs + hcol) + c);
     tile[r][c] = make_uint4(v.x, v.y, v.z, v.w);
   }
   if (tid < kTT) {
@@ -212,8 +212,8 @@ __global__ __launch_bounds__(256) void prefill_qkv_kernel(
   }
   if (!isq && !isk && tid < kTT && t0 + tid < T) {
     const int t = t0 + tid, h = head - 2 * Hk;
-    const float braw = bf2f(ab[(size_t)t * 2 * Hv + h]);
-    const float araw = bf2f(ab[(size_t)t * 2 * Hv + Hv + h]);
+    const float braw = bf2f(ab[(size_t)t * abs_ + h]);
+    const float araw = bf2f(ab[(size_t)t * abs_ + Hv + h]);
     beta[(size_t)t * Hv + h] = f2bf(sigmoid_f32(braw));
     // log of the decay multiplier g = exp(lg) (compiled_ops.rs:36-43); the
     // naive softplus overflows to inf for a+dt_bias >~ 88 (g = 0), clamped so
@@ -230,7 +230,7 @@ __global__ __launch_bounds__(256) void prefill_qkv_kernel(
 __global__ __launch_bounds__(256) void prefill_conv_state_kernel(
     uint16_t* __restrict__ conv, const int32_t* __restrict__ slot_ids,
     const int32_t* __restrict__ cu, int nseq, int num_slots, int D, int T,
-    const uint16_t* __restrict__ x, uint32_t* __restrict__ status) {
+    const uint16_t* __restrict__ x, int64_t xs, uint32_t* __restrict__ status) {
   const int s = blockIdx.x;
   const int ch = blockIdx.y * 256 + threadIdx.x;
   if (blockIdx.y == 0 && threadIdx.x == 0) {
@@ -252,7 +252,7 @@ __global__ __launch_bounds__(256) void prefill_conv_state_kernel(
   for (int j = 0; j < kConvK - 1; ++j) {
     const int p = len + j;
     const uint16_t v = p < kConvK - 1 ? cs[(size_t)p * D + ch]
-                                      : x[(size_t)(st + p - (kConvK - 1)) * D + ch];
+                                      : x[(size_t)(st + p - (kConvK - 1)) * xs + ch];
     cs[(size_t)j * D + ch] = v;
   }
 }
@@ -309,6 +309,7 @@ struct ChunkSmem {
   uint16_t Dh[4][16][kLdD];  // D_I = (I + L_II)^-1, hi
   uint16_t Dl[4][16][kLdD];  // lo
   float beta[kC], G[kC], eG[kC], dec_end[kC];  // G: cumulative log2 decay
+  float ysq[kC][8];          // RMSNormGated: per token, each wave's sum of y^2
 };
 
 __device__ __forceinline__ f32x4 mfma32(bf16x8 a, bf16x8 b, f32x4 c) {
@@ -361,13 +362,19 @@ __device__ __forceinline__ void split4(const f32x4& x, s16x4& hi, s16x4& lo) {
 }
 }  // namespace
 
-template <int R>
+// With GATED the RMSNormGated epilogue (qwen3_5.rs:660-665) runs on the
+// chunk's outputs: out[t, hv, :] = silu(z) * rms_norm(y, norm_w, norm_eps)
+// over the Dv rows of the head, z read from the merged projection row
+// (z = zrow + t * xs, columns hv*Dv ..); y is also stored when non-null.
+template <int R, bool GATED>
 __global__ __launch_bounds__(512) void prefill_chunk_kernel(
     float* __restrict__ state, const int32_t* __restrict__ slot_ids,
     const int32_t* __restrict__ cu, int num_slots, int Hk, int T,
     const uint16_t* __restrict__ qn, const uint16_t* __restrict__ kn,
     const uint16_t* __restrict__ vc, const float* __restrict__ lgv,
-    const uint16_t* __restrict__ betav, uint16_t* __restrict__ y, uint32_t* __restrict__ status) {
+    const uint16_t* __restrict__ betav, uint16_t* __restrict__ y,
+    const uint16_t* __restrict__ zrow, int64_t xs, const uint16_t* __restrict__ norm_w,
+    float norm_eps, uint16_t* __restrict__ out, uint32_t* __restrict__ status) {
   constexpr int NT = 512;
   __shared__ ChunkSmem sm;
   const int hv = blockIdx.x, s = blockIdx.y;
@@ -384,6 +391,13 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
   // this lane's state row (accumulator column) and 4-row group
   float* gstate = state + ((size_t)slot * Hv + hv) * kTileElems + (size_t)(16 * w + (lane0 & 15)) * kDk +
                   4 * (lane0 >> 4);
+  // RMSNormGated: the norm weight of this lane's output row, and its z column
+  float nw = 0.f;
+  const uint16_t* zcol = nullptr;
+  if constexpr (GATED) {
+    nw = bf2f(norm_w[16 * w + (lane0 & 15)]);
+    zcol = zrow + (size_t)hv * kDv + 16 * w + (lane0 & 15);
+  }
 
   // state accumulators: S^T tiles (dk block a, this wave's 16 state rows)
   f32x4 acc[8];
@@ -566,6 +580,15 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
       split4(v, vph[I], vpl[I]);
     }
     // (g) O_I = exp(G) * Z_I + sum_{j<=I} P_Ij V'_j
+    float yo[4][4];      // GATED: y of tokens 16I + 4lq + r, row drow (bf16 values)
+    uint16_t zv[4][4];   // GATED: z of the same outputs
+    if constexpr (GATED) {  // issued first, consumed after the y^2 sums
+#pragma unroll
+      for (int I = 0; I < 4; ++I)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          zv[I][r] = zcol[(size_t)min(c0 + 16 * I + 4 * lq + r, en - 1) * xs];
+    }
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       f32x4 o;
@@ -580,8 +603,30 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = 16 * I + 4 * lq + r;
-        if (i < n) y[((size_t)(c0 + i) * Hv + hv) * kDv + drow] = f2bf(o[r]);
+        if constexpr (GATED) {
+          yo[I][r] = rbf(o[r]);
+          // sum of y^2 over this wave's 16 rows (the 16 lanes of the DPP row)
+          const float ss = sum16(yo[I][r] * yo[I][r]);
+          if (lc == 0) sm.ysq[i][w] = ss;
+        }
+        if (y != nullptr && i < n) y[((size_t)(c0 + i) * Hv + hv) * kDv + drow] = f2bf(o[r]);
       }
+    }
+    if constexpr (GATED) {  // RMSNormGated over the Dv = 128 rows of each token
+      __syncthreads();
+#pragma unroll
+      for (int I = 0; I < 4; ++I)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = 16 * I + 4 * lq + r;
+          const f32x4 p0 = *reinterpret_cast<const f32x4*>(&sm.ysq[i][0]);
+          const f32x4 p1 = *reinterpret_cast<const f32x4*>(&sm.ysq[i][4]);
+          const float tot = ((p0[0] + p0[1]) + (p0[2] + p0[3])) + ((p1[0] + p1[1]) + (p1[2] + p1[3]));
+          const float rn = 1.0f / sqrtf(tot / (float)kDv + norm_eps);
+          const float normed = rbf(nw * rbf(yo[I][r] * rn));
+          if (i < n)
+            out[((size_t)(c0 + i) * Hv + hv) * kDv + drow] = f2bf(silu_bf16(bf2f(zv[I][r])) * normed);
+        }
     }
     // (h) S^T <- exp(G_C) S^T + K^T (exp(G_C - G) * V')
     const float eC = sm.eG[kC - 1];
@@ -624,19 +669,27 @@ static hipError_t launch_prefill_r(const PrefillArgs& a) {
   if (a.total_tokens > 0) {
     hipLaunchKernelGGL(prefill_qkv_kernel<R>, dim3(2 * a.Hk + Hv, (a.total_tokens + kTT - 1) / kTT),
                        dim3(256), 0, a.stream, a.conv, a.slot_ids, a.cu_seqlens, a.nseq,
-                       a.num_slots, a.Hk, a.total_tokens, a.mixed, a.conv_w, a.ab, a.A_log,
+                       a.num_slots, a.Hk, a.total_tokens, a.mixed, a.xstride, a.conv_w, a.ab,
+                       a.ab_stride, a.A_log,
                        a.dt_bias, ws.qn, ws.kn, ws.vc, ws.beta, ws.lg);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   hipLaunchKernelGGL(prefill_conv_state_kernel, dim3(a.nseq, (D + 255) / 256), dim3(256), 0,
                      a.stream, a.conv, a.slot_ids, a.cu_seqlens, a.nseq, a.num_slots, D,
-                     a.total_tokens, a.mixed, a.status);
+                     a.total_tokens, a.mixed, a.xstride, a.status);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(prefill_chunk_kernel<R>, dim3(Hv, a.nseq), dim3(512), 0,
-                     a.stream, a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk,
-                     a.total_tokens, ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, a.y, a.status);
+  if (a.out)
+    hipLaunchKernelGGL((prefill_chunk_kernel<R, true>), dim3(Hv, a.nseq), dim3(512), 0,
+                       a.stream, a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk,
+                       a.total_tokens, ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, a.y, a.mixed + D,
+                       a.xstride, a.norm_w, a.norm_eps, a.out, a.status);
+  else
+    hipLaunchKernelGGL((prefill_chunk_kernel<R, false>), dim3(Hv, a.nseq), dim3(512), 0,
+                       a.stream, a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk,
+                       a.total_tokens, ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, a.y, nullptr,
+                       a.xstride, nullptr, 0.0f, nullptr, a.status);
   return hipGetLastError();
 }
 

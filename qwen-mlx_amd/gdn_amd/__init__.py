@@ -51,12 +51,22 @@ SIGNATURES = {
                           _VP, _VP, _VP, ctypes.c_float, _VP, _VP, _VP], ctypes.c_int),
     "gdn_prefill_varlen": ([_VP, _I32, _VP, _VP, _I32, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _VP],
                            ctypes.c_int),
+    "gdn_prefill_varlen_gated": ([_VP, _I32, _VP, _VP, _I32, _I32, _VP, ctypes.c_int64, _VP,
+                                  ctypes.c_int64, _VP, _VP, _VP, _VP, ctypes.c_float, _VP, _VP,
+                                  _VP], ctypes.c_int),
     "gdn_qlinear_create": ([_I32, _I32, _VP, _VP, _VP, _VP, _I32, _I32, _I32, _VP,
                             ctypes.POINTER(_VP)], ctypes.c_int),
     "gdn_qlinear_destroy": ([_VP], ctypes.c_int),
     "gdn_qlinear_dims": ([_VP, ctypes.POINTER(_I32), ctypes.POINTER(_I32)], ctypes.c_int),
     "gdn_qlinear_forward": ([_VP, _VP, ctypes.c_int64, _I32, _VP, ctypes.c_int64, _VP],
                             ctypes.c_int),
+    "gdn_layer_create": ([_VP, ctypes.POINTER(_VP)], ctypes.c_int),
+    "gdn_layer_destroy": ([_VP], ctypes.c_int),
+    "gdn_pool_reserve": ([_VP, _I32, _VP], ctypes.c_int),
+    "gdn_layer_decode": ([_VP, _VP, _I32, _VP, ctypes.c_int64, _VP, ctypes.c_int64, _VP],
+                         ctypes.c_int),
+    "gdn_layer_prefill": ([_VP, _VP, _VP, _I32, _I32, _VP, ctypes.c_int64, _VP, ctypes.c_int64,
+                           _VP], ctypes.c_int),
 }
 
 
@@ -64,6 +74,12 @@ class GdnError(RuntimeError):
     def __init__(self, status: int, msg: str):
         super().__init__(f"libgdn status {status}: {msg}")
         self.status = status
+
+
+class LayerDesc(ctypes.Structure):
+    _fields_ = [("pool", _VP), ("layer", _I32), ("in_proj", _VP), ("out_proj", _VP),
+                ("A_log", _VP), ("dt_bias", _VP), ("conv_w", _VP), ("norm_w", _VP),
+                ("norm_eps", ctypes.c_float)]
 
 
 class PoolDesc(ctypes.Structure):
@@ -186,6 +202,11 @@ class Pool:
         _check(self.lib.gdn_pool_check(self.handle, _stream(stream), ctypes.byref(f)))
         return f.value
 
+    def reserve(self, max_tokens: int, stream=None):
+        """Size the activation buffer and prefill workspace for Layer calls of up
+        to max_tokens tokens."""
+        _check(self.lib.gdn_pool_reserve(self.handle, max_tokens, _stream(stream)))
+
     def alloc_slot(self) -> int:
         s = _I32()
         _check(self.lib.gdn_slot_alloc(self.handle, ctypes.byref(s)))
@@ -244,6 +265,18 @@ class Pool:
                                            _ptr(ab), _ptr(A_log), _ptr(dt_bias), _ptr(conv_w),
                                            _ptr(y), _stream(stream)))
 
+    def prefill_gated(self, layer, slot_ids, cu_seqlens, total_tokens, qkvz, ab, A_log, dt_bias,
+                      conv_w, norm_w, norm_eps, out, y=None, stream=None):
+        """Prefill with the RMSNormGated epilogue; qkvz / ab as in decode_gated, one
+        row per packed token. out (and optional y) [total_tokens, Hv, Dv]."""
+        xp, xs = _rows(qkvz)
+        ap, as_ = _rows(ab)
+        _check(self.lib.gdn_prefill_varlen_gated(self.handle, layer, _ptr(slot_ids),
+                                                 _ptr(cu_seqlens), slot_ids.numel(), total_tokens,
+                                                 xp, xs, ap, as_, _ptr(A_log), _ptr(dt_bias),
+                                                 _ptr(conv_w), _ptr(norm_w), float(norm_eps),
+                                                 _ptr(out), _ptr(y), _stream(stream)))
+
 
 class QLinear:
     """4-bit affine-quantized linear layer (MLX format, group 64) built from one
@@ -283,6 +316,51 @@ class QLinear:
     def close(self):
         if getattr(self, "handle", None):
             _check(self.lib.gdn_qlinear_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Layer:
+    """One GatedDeltaNet layer (in_proj -> conv/norm/gates/recurrence/RMSNormGated
+    -> out_proj) on pool layer `layer`. in_proj, out_proj: QLinear; the weight
+    tensors are device tensors kept alive by this object."""
+
+    def __init__(self, pool, layer: int, in_proj, out_proj, A_log, dt_bias, conv_w, norm_w,
+                 norm_eps: float):
+        self.lib = load()
+        self._keep = (pool, in_proj, out_proj, A_log, dt_bias, conv_w, norm_w)
+        d = LayerDesc(pool.handle, layer, in_proj.handle, out_proj.handle, _ptr(A_log),
+                      _ptr(dt_bias), _ptr(conv_w), _ptr(norm_w), float(norm_eps))
+        h = _VP()
+        _check(self.lib.gdn_layer_create(ctypes.byref(d), ctypes.byref(h)))
+        self.handle = h
+        self.hidden = in_proj.K
+
+    def decode(self, slot_ids, x, out, stream=None):
+        xp, xs = _rows(x)
+        op, os_ = _rows(out)
+        if x.shape[0] != slot_ids.numel() or out.shape[0] != x.shape[0]:
+            raise ValueError("x / out rows must match the slot count")
+        _check(self.lib.gdn_layer_decode(self.handle, _ptr(slot_ids), slot_ids.numel(), xp, xs,
+                                         op, os_, _stream(stream)))
+
+    def prefill(self, slot_ids, cu_seqlens, total_tokens, x, out, stream=None):
+        xp, xs = _rows(x)
+        op, os_ = _rows(out)
+        if total_tokens and (x.shape[0] < total_tokens or out.shape[0] < total_tokens):
+            raise ValueError("x / out hold fewer rows than total_tokens")
+        _check(self.lib.gdn_layer_prefill(self.handle, _ptr(slot_ids), _ptr(cu_seqlens),
+                                          slot_ids.numel(), total_tokens, xp, xs, op, os_,
+                                          _stream(stream)))
+
+    def close(self):
+        if getattr(self, "handle", None):
+            _check(self.lib.gdn_layer_destroy(self.handle))
             self.handle = None
 
     def __del__(self):
