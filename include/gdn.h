@@ -269,7 +269,7 @@ gdn_status gdn_qlinear_forward(const gdn_qlinear* layer, const uint16_t* x, int6
  *   gated = gdn_decode_gated / gdn_prefill_varlen_gated on column views of proj
  *   out = out_proj(gated)                      one gdn_qlinear_forward
  * x and out are hidden-size bf16 rows (the decoder layer's input_layernorm
- * output and the mixer output the residual adds, qwen3_5.rs DecoderLayer).
+ * output and the mixer output the residual adds, qwen3_5.rs:729-739).
  * The layer keeps pointers only: the pool, the two projections and the
  * weight tensors must outlive it. Activations go to a buffer held by the
  * pool (shared by every layer of the pool, so the pool's calls are ordered
@@ -312,6 +312,87 @@ gdn_status gdn_layer_prefill(gdn_layer* layer, const int32_t* slot_ids,
                              const int32_t* cu_seqlens, int32_t nseq, int32_t total_tokens,
                              const uint16_t* x, int64_t x_stride, uint16_t* out,
                              int64_t out_stride, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Executor: the ModelExecutor contract (src/scheduler/executor.rs:21-49) on
+ * pool slots, in place of Qwen35Executor (src/scheduler/mlx_executor.rs:23-257).
+ * A sequence's per-layer caches (Qwen35State, mlx_executor.rs:19-21) are one
+ * slot id, the same in every layer, so stack_caches / unstack_caches
+ * (:92-130) disappear: a decode step hands the layers B slot ids. Prefill
+ * admits the sequence (slot alloc + zero in every layer: the fresh caches of
+ * qwen3_5.rs:598-648), gdn_exec_release retires it (the Sequence's state
+ * dropped), submit / collect pipeline one batch against the host
+ * (mlx_executor.rs:195-254 as driven by qwen_mlx_serve.rs:110-177).
+ *
+ * The model the executor runs is the GDN half of the Qwen3.5 decoder stack:
+ *   h = embed[token]; per layer l: h = h + layer_l(rms_norm(h, input_norm_w[l]));
+ *   token = argmax(lm_head(rms_norm(h, final_norm_w)))
+ * (Qwen35Model::forward, qwen3_5.rs:826-880, over its GatedDeltaNet decoder
+ * layers, DecoderLayer::forward_with_cache :723-743 without the MLP half).
+ * Attention layers, MoE MLPs and temperature sampling are outside this
+ * library; the greedy pick keeps runs reproducible.
+ *
+ * One thread owns an executor (qwen_mlx_serve.rs:96-99). All its device work
+ * runs on the stream given at creation, in call order. Sequence ids are the
+ * caller's (SequenceId, sequence.rs:7); token ids are checked against the
+ * vocabulary on the host.
+ * ------------------------------------------------------------------------ */
+typedef struct gdn_exec gdn_exec;
+
+typedef struct gdn_exec_desc {
+  gdn_pool* pool;                       /* every sequence's GDN state, one slot each     */
+  int32_t num_layers;
+  gdn_layer* const* layers;             /* the GDN layers in model order (on `pool`)     */
+  const uint16_t* const* input_norm_w;  /* per layer [hidden] bf16 input_layernorm       */
+  const uint16_t* final_norm_w;         /* [hidden] bf16                                 */
+  float rms_eps;
+  const uint16_t* embed;                /* [vocab, hidden] bf16, 16-byte aligned         */
+  const gdn_qlinear* head;              /* lm_head: hidden -> vocab (sets both sizes)    */
+  int32_t max_batch;                    /* decode batch bound (max_batch_size)           */
+  int32_t max_prompt;                   /* longest prompt one prefill takes              */
+  int32_t device;                       /* HIP device of the pool and weights            */
+} gdn_exec_desc;
+
+/* Allocates the executor's buffers (activations for max(max_batch,
+ * max_prompt) rows, logits for max_batch rows, pinned staging) and sizes the
+ * pool's layer buffers with gdn_pool_reserve: later calls allocate nothing. */
+gdn_status gdn_exec_create(const gdn_exec_desc* desc, void* stream, gdn_exec** out);
+/* Waits for the stream, frees the buffers and the slots still held. */
+gdn_status gdn_exec_destroy(gdn_exec* exec);
+
+/* ModelExecutor::prefill (executor.rs:23): admit seq_id (a free slot, or its
+ * own slot again if it is known) with zeroed state, run the prompt through
+ * every layer and return the first picked token. Synchronous. */
+gdn_status gdn_exec_prefill(gdn_exec* exec, uint64_t seq_id, const int32_t* prompt, int32_t len,
+                            uint32_t* first_token);
+
+/* ModelExecutor::decode_batch (executor.rs:26): one token for each of B
+ * prefilled, distinct sequences, fed their current tokens; the results in
+ * input order. = submit_batch + collect_batch. */
+gdn_status gdn_exec_decode_batch(gdn_exec* exec, const uint64_t* seq_ids, const uint32_t* tokens,
+                                 int32_t B, uint32_t* next_tokens);
+
+/* ModelExecutor::submit_batch / collect_batch (executor.rs:31-42): queue the
+ * step and return at once; collect waits for it. One batch in flight at a
+ * time (a second submit before collect fails). A prefill between the two is
+ * allowed (it waits for the batch). */
+gdn_status gdn_exec_submit_batch(gdn_exec* exec, const uint64_t* seq_ids, const uint32_t* tokens,
+                                 int32_t B);
+gdn_status gdn_exec_collect_batch(gdn_exec* exec, uint32_t* next_tokens, int32_t B);
+
+/* The sequence is finished (its Sequence and state dropped): its slot goes
+ * back to the pool. Work already queued on the slot still completes first. */
+gdn_status gdn_exec_release(gdn_exec* exec, uint64_t seq_id);
+
+/* ModelExecutor::max_batch_size / supports_pipeline (executor.rs:45-48). */
+int32_t gdn_exec_max_batch_size(const gdn_exec* exec);
+int32_t gdn_exec_supports_pipeline(const gdn_exec* exec);
+
+/* Introspection: the slot of a sequence; the device logits of the last
+ * forward (rows x vocab bf16, valid until the next call). */
+gdn_status gdn_exec_seq_slot(const gdn_exec* exec, uint64_t seq_id, int32_t* slot);
+gdn_status gdn_exec_logits(const gdn_exec* exec, const uint16_t** logits, int32_t* rows,
+                           int32_t* vocab);
 
 #ifdef __cplusplus
 }

@@ -25,6 +25,15 @@ gdn_status fail(gdn_status code, const char* fmt, ...) {
   return code;
 }
 
+}  // namespace
+
+gdn_status gdn::set_error(gdn_status code, const char* msg) {
+  g_err = msg;
+  return code;
+}
+
+namespace {
+
 gdn_status hip_fail(hipError_t e, const char* what) {
   return fail(GDN_ERR_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
 }

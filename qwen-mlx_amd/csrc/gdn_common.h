@@ -228,4 +228,15 @@ hipError_t launch_validate(const int32_t* slot_ids, int n, int num_slots, uint32
 size_t prefill_workspace_bytes(int R, int Hk, int total_tokens);
 hipError_t launch_prefill(const PrefillArgs& a);
 
+// Sets the calling thread's gdn_last_error() message and returns code.
+gdn_status set_error(gdn_status code, const char* msg);
+
+// Executor model-body kernels (gdn_exec.hip).
+hipError_t launch_embed(const uint16_t* table, const int32_t* tok, int n, int vocab, int hidden,
+                        uint16_t* h, hipStream_t s);
+hipError_t launch_add_norm(uint16_t* h, const uint16_t* d, int n, int hidden, const uint16_t* w,
+                           float eps, uint16_t* hn, hipStream_t s);
+hipError_t launch_argmax(const uint16_t* logits, int64_t ld, int n, int vocab, int32_t* out,
+                         hipStream_t s);
+
 }  // namespace gdn

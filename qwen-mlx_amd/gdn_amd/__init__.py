@@ -60,6 +60,19 @@ SIGNATURES = {
     "gdn_qlinear_dims": ([_VP, ctypes.POINTER(_I32), ctypes.POINTER(_I32)], ctypes.c_int),
     "gdn_qlinear_forward": ([_VP, _VP, ctypes.c_int64, _I32, _VP, ctypes.c_int64, _VP],
                             ctypes.c_int),
+    "gdn_exec_create": ([_VP, _VP, ctypes.POINTER(_VP)], ctypes.c_int),
+    "gdn_exec_destroy": ([_VP], ctypes.c_int),
+    "gdn_exec_prefill": ([_VP, ctypes.c_uint64, _VP, _I32, ctypes.POINTER(ctypes.c_uint32)],
+                         ctypes.c_int),
+    "gdn_exec_decode_batch": ([_VP, _VP, _VP, _I32, _VP], ctypes.c_int),
+    "gdn_exec_submit_batch": ([_VP, _VP, _VP, _I32], ctypes.c_int),
+    "gdn_exec_collect_batch": ([_VP, _VP, _I32], ctypes.c_int),
+    "gdn_exec_release": ([_VP, ctypes.c_uint64], ctypes.c_int),
+    "gdn_exec_max_batch_size": ([_VP], _I32),
+    "gdn_exec_supports_pipeline": ([_VP], _I32),
+    "gdn_exec_seq_slot": ([_VP, ctypes.c_uint64, ctypes.POINTER(_I32)], ctypes.c_int),
+    "gdn_exec_logits": ([_VP, ctypes.POINTER(_VP), ctypes.POINTER(_I32), ctypes.POINTER(_I32)],
+                        ctypes.c_int),
     "gdn_layer_create": ([_VP, ctypes.POINTER(_VP)], ctypes.c_int),
     "gdn_layer_destroy": ([_VP], ctypes.c_int),
     "gdn_pool_reserve": ([_VP, _I32, _VP], ctypes.c_int),
@@ -80,6 +93,13 @@ class LayerDesc(ctypes.Structure):
     _fields_ = [("pool", _VP), ("layer", _I32), ("in_proj", _VP), ("out_proj", _VP),
                 ("A_log", _VP), ("dt_bias", _VP), ("conv_w", _VP), ("norm_w", _VP),
                 ("norm_eps", ctypes.c_float)]
+
+
+class ExecDesc(ctypes.Structure):
+    _fields_ = [("pool", _VP), ("num_layers", _I32), ("layers", ctypes.POINTER(_VP)),
+                ("input_norm_w", ctypes.POINTER(_VP)), ("final_norm_w", _VP),
+                ("rms_eps", ctypes.c_float), ("embed", _VP), ("head", _VP),
+                ("max_batch", _I32), ("max_prompt", _I32), ("device", _I32)]
 
 
 class PoolDesc(ctypes.Structure):
@@ -361,6 +381,92 @@ class Layer:
     def close(self):
         if getattr(self, "handle", None):
             _check(self.lib.gdn_layer_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Executor:
+    """ModelExecutor (src/scheduler/executor.rs:21-49) over pool slots: the GDN
+    decoder stack h = embed[tok]; h += layer_l(rms_norm(h, w_l)) per layer;
+    greedy token of lm_head(rms_norm(h, w_final)). layers: Layer objects on
+    `pool`; embed [vocab, hidden] bf16 device tensor; head: QLinear hidden ->
+    vocab. Sequence ids are caller-chosen integers."""
+
+    def __init__(self, pool, layers, input_norm_w, final_norm_w, embed, head, rms_eps=1e-6,
+                 max_batch=64, max_prompt=4096, device=0, stream=None):
+        self.lib = load()
+        self._keep = (pool, list(layers), list(input_norm_w), final_norm_w, embed, head)
+        n = len(layers)
+        self._layers = (_VP * max(n, 1))(*[l.handle.value for l in layers])
+        self._norms = (_VP * max(n, 1))(*[_ptr(w) for w in input_norm_w])
+        d = ExecDesc(pool.handle, n, self._layers, self._norms, _ptr(final_norm_w),
+                     float(rms_eps), _ptr(embed), head.handle, max_batch, max_prompt, device)
+        h = _VP()
+        self._stream = stream
+        _check(self.lib.gdn_exec_create(ctypes.byref(d), _stream(stream), ctypes.byref(h)))
+        self.handle = h
+
+    def prefill(self, seq_id: int, prompt) -> int:
+        p = (_I32 * len(prompt))(*[int(t) for t in prompt])
+        t = ctypes.c_uint32()
+        _check(self.lib.gdn_exec_prefill(self.handle, seq_id, p, len(prompt), ctypes.byref(t)))
+        return t.value
+
+    @staticmethod
+    def _batch(seq_ids, tokens):
+        B = len(seq_ids)
+        if len(tokens) != B:
+            raise ValueError("one current token per sequence")
+        return (B, (ctypes.c_uint64 * B)(*[int(s) for s in seq_ids]),
+                (ctypes.c_uint32 * B)(*[int(t) for t in tokens]))
+
+    def decode_batch(self, seq_ids, tokens) -> list:
+        B, s, t = self._batch(seq_ids, tokens)
+        out = (ctypes.c_uint32 * max(B, 1))()
+        _check(self.lib.gdn_exec_decode_batch(self.handle, s, t, B, out))
+        return list(out[:B])
+
+    def submit_batch(self, seq_ids, tokens) -> int:
+        B, s, t = self._batch(seq_ids, tokens)
+        _check(self.lib.gdn_exec_submit_batch(self.handle, s, t, B))
+        return B
+
+    def collect_batch(self, B: int) -> list:
+        out = (ctypes.c_uint32 * max(B, 1))()
+        _check(self.lib.gdn_exec_collect_batch(self.handle, out, B))
+        return list(out[:B])
+
+    def release(self, seq_id: int):
+        _check(self.lib.gdn_exec_release(self.handle, seq_id))
+
+    def max_batch_size(self) -> int:
+        return self.lib.gdn_exec_max_batch_size(self.handle)
+
+    def supports_pipeline(self) -> bool:
+        return bool(self.lib.gdn_exec_supports_pipeline(self.handle))
+
+    def slot(self, seq_id: int) -> int:
+        s = _I32()
+        _check(self.lib.gdn_exec_seq_slot(self.handle, seq_id, ctypes.byref(s)))
+        return s.value
+
+    def logits(self):
+        """Device logits of the last forward as a [rows, vocab] int16 (bf16 bits) view."""
+        p, r, v = _VP(), _I32(), _I32()
+        _check(self.lib.gdn_exec_logits(self.handle, ctypes.byref(p), ctypes.byref(r),
+                                        ctypes.byref(v)))
+        dev_idx = self._keep[0].device
+        return _wrap_device(p.value, r.value * v.value, __import__("torch").int16,
+                            dev_idx).view(r.value, v.value)
+
+    def close(self):
+        if getattr(self, "handle", None):
+            _check(self.lib.gdn_exec_destroy(self.handle))
             self.handle = None
 
     def __del__(self):
