@@ -73,6 +73,11 @@ def parse_args(argv=None):
                          "hidden 2048 -> q|k|v|z|b|a 12352) over --layers layers instead")
     ap.add_argument("--qlinear-rows", type=int, default=0,
                     help="rows (tokens) per qlinear launch; default --batch (decode)")
+    ap.add_argument("--exec", action="store_true",
+                    help="the executor (gdn_exec) decode step over the GDN decoder stack: "
+                         "embedding, per layer norm + in_proj + fused decode + out_proj, "
+                         "final norm, lm_head, greedy pick")
+    ap.add_argument("--vocab", type=int, default=248320)
     ap.add_argument("--seed", type=int, default=0)
     return ap.parse_args(argv)
 
@@ -200,6 +205,7 @@ def prefill_bench(args):
 # (2*Hk*Dk + Hv*Dv rows), in_proj_z (Hv*Dv), in_proj_b, in_proj_a (Hv each).
 QL_HIDDEN = 2048
 QL_PARTS = [D, HV * DV, HV, HV]
+QL_N = sum(QL_PARTS)
 
 
 def qlinear_bench(args):
@@ -289,6 +295,108 @@ def qlinear_bench(args):
         out["cpu_baseline"] = qlinear_cpu_baseline(args.cpu_seconds, L)
     for q in layers:
         q.close()
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def _rand_qlinear(K_, parts_rows, gen, dev):
+    """A QLinear of random MLX-format 4-bit parts (scales ~U(0.001, 0.011),
+    biases ~N(0, 0.02))."""
+    import torch
+
+    import gdn_amd
+    G = K_ // 64
+    parts = []
+    for n in parts_rows:
+        w = torch.randint(-2**31, 2**31 - 1, (n, K_ // 8), generator=gen, device=dev,
+                          dtype=torch.int32)
+        sc = (torch.rand((n, G), generator=gen, device=dev) * 0.01 + 0.001).to(torch.bfloat16)
+        bi = (torch.randn((n, G), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+        parts.append((w, sc, bi))
+    q = gdn_amd.QLinear(K_, parts)
+    del parts
+    return q
+
+
+def exec_bench(args):
+    """The executor's decode step (gdn_exec_submit_batch + collect) over the GDN
+    decoder stack of Qwen3.5-35B-A3B's shapes: hidden 2048, `layers` GDN layers
+    (merged 4-bit in_proj 2048 -> 12352, fused conv/norm/gates/recurrence/
+    norm-gate, 4-bit out_proj 4096 -> 2048), 4-bit lm_head 2048 -> vocab,
+    greedy pick; `slots`-slot pools, B sequences prefilled with 16-token
+    prompts. Random weights; tokens are the executor's own picks. Prints one
+    JSON line; the step time includes the host side (staging, launches, the
+    wait for the picked tokens)."""
+    import torch
+
+    import gdn_amd
+    dev = torch.device("cuda:0")
+    L, B, V = args.layers, args.batch, args.vocab
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    bf = torch.bfloat16
+    pool = gdn_amd.Pool(L, args.slots, HK, HV)
+    gl, keep = [], []
+    for l in range(L):
+        inp = _rand_qlinear(QL_HIDDEN, QL_PARTS, gen, dev)
+        outp = _rand_qlinear(HV * DV, [QL_HIDDEN], gen, dev)
+        A_log = torch.rand(HV, generator=gen, device=dev) * math.log(16.0)
+        dt_bias = torch.randn(HV, generator=gen, device=dev) * 0.1
+        conv_w = (torch.randn((D, KW), generator=gen, device=dev) * 0.25).to(bf)
+        norm_w = (1 + 0.1 * torch.randn(DV, generator=gen, device=dev)).to(bf)
+        gl.append(gdn_amd.Layer(pool, l, inp, outp, A_log, dt_bias, conv_w, norm_w, 1e-6))
+        keep += [inp, outp]
+    in_norm = [(1 + 0.1 * torch.randn(QL_HIDDEN, generator=gen, device=dev)).to(bf)
+               for _ in range(L)]
+    fin = (1 + 0.1 * torch.randn(QL_HIDDEN, generator=gen, device=dev)).to(bf)
+    embed = torch.randn((V, QL_HIDDEN), generator=gen, device=dev).to(bf)
+    head = _rand_qlinear(QL_HIDDEN, [V], gen, dev)
+    ex = gdn_amd.Executor(pool, gl, in_norm, fin, embed, head, 1e-6, max_batch=B, max_prompt=64)
+    rng = torch.Generator().manual_seed(args.seed)
+    ids = list(range(1, B + 1))
+    cur = [ex.prefill(i, torch.randint(0, V, (16,), generator=rng).tolist()) for i in ids]
+    for _ in range(args.warmup):
+        cur = ex.decode_batch(ids, cur)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ex.submit_batch(ids, cur)
+        cur = ex.collect_batch(B)
+    elapsed = time.perf_counter() - t0
+    flags = pool.check()
+    if flags:
+        print(f"pool status flags 0x{flags:x}", file=sys.stderr)
+        return 1
+    ms = elapsed / args.steps * 1e3
+    wbytes = L * (QL_N * QL_HIDDEN // 2 + 2 * QL_N * (QL_HIDDEN // 64) * 2
+                  + QL_HIDDEN * HV * DV // 2 + 2 * QL_HIDDEN * (HV * DV // 64) * 2) \
+        + V * QL_HIDDEN // 2 + 2 * V * (QL_HIDDEN // 64) * 2
+    step_bytes = B * L * STATE_BYTES + wbytes
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    out = {
+        "metric": "GDN decoder-stack decode tokens/s through the executor (B sequences, all layers)",
+        "value": round(B * args.steps / elapsed, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "dtype": "bf16 activations, 4-bit affine weights, f32 state",
+        "data": "synthetic",
+        "config": {"workload": f"executor decode step: {L} GDN layers (in_proj, fused decode + "
+                               f"norm-gate, out_proj) + lm_head {QL_HIDDEN}->{V}, B={B}, "
+                               f"{args.slots}-slot pools",
+                   "layers": L, "batch": B, "slots": args.slots, "hidden": QL_HIDDEN,
+                   "vocab": V},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_step": step_bytes,
+                     "note": "whole step (state read+write of B sequences in every layer plus "
+                             "every weight byte once) over the host-measured step time"},
+    }
+    ex.close()
+    for g in gl:
+        g.close()
     print(json.dumps(out), flush=True)
     return 0
 
@@ -462,6 +570,8 @@ def main(argv=None):
         return prefill_bench(args)
     if args.qlinear:
         return qlinear_bench(args)
+    if args.exec:
+        return exec_bench(args)
     w = Workload(args)
     for _ in range(args.warmup):
         w.step()

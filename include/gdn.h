@@ -240,9 +240,11 @@ typedef struct gdn_qlinear gdn_qlinear;
 /* Merge nparts MLX-format parts (device pointers, part i has part_rows[i]
  * output rows) into one layer with N = sum(part_rows) outputs and repack it
  * for the kernel on `device`. The layer owns its memory (about N*K/2 +
- * 3*N*K/32 bytes); the sources are only read, and may be freed once this
- * returns (it synchronises `stream`). Supported: bits 4, group_size 64,
- * K a multiple of 512 up to 4096, part_rows multiples of 16. */
+ * 3*N*K/32 bytes, plus K/512 * 64 * N f32 partial sums for layers whose
+ * decode-sized calls split K: K > 2048, or N < 8192 with K >= 1024); the
+ * sources are only read, and may be freed once this returns (it synchronises
+ * `stream`). Supported: bits 4, group_size 64, K a multiple of 512 up to
+ * 4096, part_rows multiples of 16. */
 gdn_status gdn_qlinear_create(int32_t K, int32_t nparts, const int32_t* part_rows,
                               const uint32_t* const* w, const uint16_t* const* scales,
                               const uint16_t* const* biases, int32_t group_size, int32_t bits,
@@ -255,7 +257,9 @@ gdn_status gdn_qlinear_dims(const gdn_qlinear* layer, int32_t* K, int32_t* N);
 /* y [M, y_stride] bf16 = x [M, x_stride] bf16 . W^T over the first N columns
  * (columns past N untouched). x: 16-byte aligned, x_stride >= K and a
  * multiple of 8; y: 8-byte aligned, y_stride >= N and a multiple of 4;
- * M <= 8,388,480. Allocates nothing. For the merged qkv|z|b|a layer the
+ * M <= 8,388,480. Allocates nothing. Calls on one layer must be ordered on
+ * one stream (a K-split call uses the layer's partial-sum buffer). For the
+ * merged qkv|z|b|a layer the
  * output row is [q|k|v|z|b|a], which gdn_decode_gated reads in place
  * (qkvz = y, row_stride = y_stride; ab = y + D + Hv*Dv, ab_stride = y_stride). */
 gdn_status gdn_qlinear_forward(const gdn_qlinear* layer, const uint16_t* x, int64_t x_stride,

@@ -553,6 +553,7 @@ struct gdn_qlinear {
   uint16_t* sp = nullptr;    // packed scales  [Npad/16][K/128][16][2] bf16
   uint16_t* bias = nullptr;  // [Npad, G] bf16
   uint16_t* nsc = nullptr;   // [Npad, G] bf16, -128 * scales
+  float* part = nullptr;     // K-slice partials of decode-sized calls [slices][64][Npad] f32
 };
 
 static void qlinear_release(gdn_qlinear* q) {
@@ -561,6 +562,7 @@ static void qlinear_release(gdn_qlinear* q) {
   if (q->sp) (void)hipFree(q->sp);
   if (q->bias) (void)hipFree(q->bias);
   if (q->nsc) (void)hipFree(q->nsc);
+  if (q->part) (void)hipFree(q->part);
   delete q;
 }
 
@@ -601,8 +603,11 @@ gdn_status gdn_qlinear_create(int32_t K, int32_t nparts, const int32_t* part_row
   q->G = K / 64;
   q->device = device;
   const size_t wbytes = (size_t)q->Npad * K / 2, gbytes = (size_t)q->Npad * q->G * 2;
+  const int slices = gdn::qlinear_decode_slices(K, q->Npad);
+  const size_t pbytes = slices > 1 ? (size_t)slices * 64 * q->Npad * sizeof(float) : 0;
   if (hipMalloc(&q->wp, wbytes) != hipSuccess || hipMalloc(&q->sp, gbytes) != hipSuccess ||
-      hipMalloc(&q->bias, gbytes) != hipSuccess || hipMalloc(&q->nsc, gbytes) != hipSuccess) {
+      hipMalloc(&q->bias, gbytes) != hipSuccess || hipMalloc(&q->nsc, gbytes) != hipSuccess ||
+      (pbytes && hipMalloc(&q->part, pbytes) != hipSuccess)) {
     qlinear_release(q);
     return fail(GDN_ERR_OOM, "gdn_qlinear_create: hipMalloc of %zu bytes failed",
                 wbytes + 3 * gbytes);
@@ -686,6 +691,7 @@ gdn_status gdn_qlinear_forward(const gdn_qlinear* q, const uint16_t* x, int64_t 
   a.nsc = q->nsc;
   a.y = y;
   a.ys = y_stride;
+  a.part = q->part;
   a.stream = as_stream(stream);
   hipError_t e = gdn::launch_qlinear(a);
   if (e != hipSuccess) return hip_fail(e, "gdn_qlinear_forward launch");

@@ -214,11 +214,14 @@ struct QLinearArgs {
   const uint16_t* nsc;
   uint16_t* y;        // [M, ys] bf16
   int64_t ys;
+  float* part;        // K-slice partials [slices][64][Npad] f32 (decode shapes), or null
   hipStream_t stream;
 };
 
 hipError_t launch_qlinear_pack(const QLinearPackArgs& a);
 hipError_t launch_qlinear(const QLinearArgs& a);
+// K slices the decode path uses for a layer (1 = no partials workspace needed).
+int qlinear_decode_slices(int K, int Npad);
 
 hipError_t launch_decode(const DecodeArgs& a);
 hipError_t launch_recurrent(const RecurrentArgs& a);
@@ -236,7 +239,9 @@ hipError_t launch_embed(const uint16_t* table, const int32_t* tok, int n, int vo
                         uint16_t* h, hipStream_t s);
 hipError_t launch_add_norm(uint16_t* h, const uint16_t* d, int n, int hidden, const uint16_t* w,
                            float eps, uint16_t* hn, hipStream_t s);
-hipError_t launch_argmax(const uint16_t* logits, int64_t ld, int n, int vocab, int32_t* out,
-                         hipStream_t s);
+// Greedy pick in two passes; pv / pi hold n * argmax_chunks(vocab) partials.
+int argmax_chunks(int vocab);
+hipError_t launch_argmax(const uint16_t* logits, int64_t ld, int n, int vocab, float* pv, int* pi,
+                         int32_t* out, hipStream_t s);
 
 }  // namespace gdn

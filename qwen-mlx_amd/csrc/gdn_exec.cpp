@@ -72,6 +72,8 @@ struct gdn_exec {
   uint16_t* hn = nullptr;     // normed rows fed to a layer
   uint16_t* mix = nullptr;    // layer output rows
   uint16_t* logits = nullptr; // [max_batch, vocab]
+  float* d_pv = nullptr;      // greedy-pick partials [max_batch, argmax_chunks(vocab)]
+  int* d_pi = nullptr;
   // pinned host staging (one region per direction and kind, so a prefill
   // staged while a batch is in flight does not overwrite it)
   int32_t* p_dec = nullptr;
@@ -90,7 +92,7 @@ void exec_release(gdn_exec* x) {
   if (!x) return;
   if (x->stream) (void)hipStreamSynchronize(x->stream);
   for (void* p : {(void*)x->d_dec, (void*)x->d_pre, (void*)x->d_next, (void*)x->h, (void*)x->hn,
-                  (void*)x->mix, (void*)x->logits})
+                  (void*)x->mix, (void*)x->logits, (void*)x->d_pv, (void*)x->d_pi})
     if (p) (void)hipFree(p);
   for (void* p : {(void*)x->p_dec, (void*)x->p_pre, (void*)x->p_next, (void*)x->p_first})
     if (p) (void)hipHostFree(p);
@@ -138,7 +140,9 @@ gdn_status pick(gdn_exec* x, int r0, int n, int32_t* dst) {
   HIP_TRY(gdn::launch_add_norm(hr, mr, n, x->hidden, x->final_norm_w, x->eps, nr, x->stream),
           "final norm");
   GDN_TRY(gdn_qlinear_forward(x->head, nr, x->hidden, n, x->logits, x->vocab, x->stream));
-  HIP_TRY(gdn::launch_argmax(x->logits, x->vocab, n, x->vocab, x->d_next, x->stream), "argmax");
+  HIP_TRY(gdn::launch_argmax(x->logits, x->vocab, n, x->vocab, x->d_pv, x->d_pi, x->d_next,
+                             x->stream),
+          "argmax");
   HIP_TRY(hipMemcpyAsync(dst, x->d_next, sizeof(int32_t) * n, hipMemcpyDeviceToHost, x->stream),
           "token copy");
   x->logits_rows = n;
@@ -190,6 +194,8 @@ gdn_status gdn_exec_create(const gdn_exec_desc* desc, void* stream, gdn_exec** o
             hipMalloc(&x->h, act) == hipSuccess && hipMalloc(&x->hn, act) == hipSuccess &&
             hipMalloc(&x->mix, act) == hipSuccess &&
             hipMalloc(&x->logits, (size_t)d.max_batch * vocab * sizeof(uint16_t)) == hipSuccess &&
+            hipMalloc(&x->d_pv, sizeof(float) * d.max_batch * gdn::argmax_chunks(vocab)) == hipSuccess &&
+            hipMalloc(&x->d_pi, sizeof(int) * d.max_batch * gdn::argmax_chunks(vocab)) == hipSuccess &&
             hipHostMalloc(&x->p_dec, sizeof(int32_t) * 2 * d.max_batch, 0) == hipSuccess &&
             hipHostMalloc(&x->p_pre, sizeof(int32_t) * (3 + (size_t)d.max_prompt), 0) == hipSuccess &&
             hipHostMalloc(&x->p_next, sizeof(int32_t) * d.max_batch, 0) == hipSuccess &&

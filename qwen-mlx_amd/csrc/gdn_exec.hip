@@ -1,6 +1,8 @@
 // gdn_exec.hip -- the small kernels of the executor's model body around the
 // GDN layers: token embedding rows, residual add + rms-norm, greedy pick.
 // All three are row-parallel and HBM/latency bound (a few KB per row).
+#include <climits>
+
 #include "gdn_common.h"
 
 namespace gdn {
@@ -40,7 +42,8 @@ __global__ __launch_bounds__(kRowThreads) void embed_kernel(const uint16_t* __re
 // `x + mixer(input_layernorm(x))` seam, qwen3_5.rs:729-739):
 //   h = bf16(h + d)   (skipped when d is null)
 //   hn = bf16(w * bf16(h * rsqrt(mean(h^2) + eps)))
-// grid n, block 256; thread t owns elements t + 256 j.
+// grid n, block 256; thread t owns the 8 elements from 8t + 2048j (16-byte
+// accesses; hidden a multiple of 8, at most 4096).
 __global__ __launch_bounds__(kRowThreads) void add_norm_kernel(uint16_t* __restrict__ h,
                                                                const uint16_t* __restrict__ d,
                                                                int hidden,
@@ -48,59 +51,92 @@ __global__ __launch_bounds__(kRowThreads) void add_norm_kernel(uint16_t* __restr
                                                                float eps,
                                                                uint16_t* __restrict__ hn) {
   __shared__ float red[4];
+  constexpr int J = kMaxHiddenPerThread / 8;
   const size_t row = (size_t)blockIdx.x * hidden;
-  float v[kMaxHiddenPerThread];
+  float v[J][8];
   float ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < kMaxHiddenPerThread; ++j) {
-    const int c = threadIdx.x + kRowThreads * j;
-    v[j] = 0.f;
+  for (int j = 0; j < J; ++j) {
+    const int c = 8 * (threadIdx.x + kRowThreads * j);
     if (c < hidden) {
-      float x = bf2f(h[row + c]);
+      uint4 hv = *reinterpret_cast<const uint4*>(h + row + c);
+      const uint32_t* hw = reinterpret_cast<const uint32_t*>(&hv);
       if (d != nullptr) {
-        x = rbf(x + bf2f(d[row + c]));
-        h[row + c] = f2bf(x);
+        const uint4 dv = *reinterpret_cast<const uint4*>(d + row + c);
+        const uint32_t* dw = reinterpret_cast<const uint32_t*>(&dv);
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          o[e] = f2bf2(bf_lo(hw[e]) + bf_lo(dw[e]), bf_hi(hw[e]) + bf_hi(dw[e]));
+        hv = make_uint4(o[0], o[1], o[2], o[3]);
+        *reinterpret_cast<uint4*>(h + row + c) = hv;
       }
-      v[j] = x;
-      ss += x * x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[j][2 * e] = bf_lo(hw[e]);
+        v[j][2 * e + 1] = bf_hi(hw[e]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += v[j][e] * v[j][e];
     }
   }
   const float tot = block_sum(ss, red);
   const float rn = 1.0f / sqrtf(tot / (float)hidden + eps);
 #pragma unroll
-  for (int j = 0; j < kMaxHiddenPerThread; ++j) {
-    const int c = threadIdx.x + kRowThreads * j;
-    if (c < hidden) hn[row + c] = f2bf(bf2f(w[c]) * rbf(v[j] * rn));
+  for (int j = 0; j < J; ++j) {
+    const int c = 8 * (threadIdx.x + kRowThreads * j);
+    if (c < hidden) {
+      const uint4 wv = *reinterpret_cast<const uint4*>(w + c);
+      const uint32_t* ww = reinterpret_cast<const uint32_t*>(&wv);
+      uint32_t o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o[e] = f2bf2(bf_lo(ww[e]) * rbf(v[j][2 * e] * rn), bf_hi(ww[e]) * rbf(v[j][2 * e + 1] * rn));
+      *reinterpret_cast<uint4*>(hn + row + c) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
   }
 }
 
-// out[i] = the index of the largest logit of row i (bf16 [n, ld]); ties go
-// to the lowest index and NaN never wins (an all-NaN row gives 0). grid n,
-// block 256.
-__global__ __launch_bounds__(kRowThreads) void argmax_kernel(const uint16_t* __restrict__ logits,
-                                                             int64_t ld, int vocab,
-                                                             int32_t* __restrict__ out) {
+// Greedy pick: out[i] = the index of the largest logit of row i (bf16
+// [n, ld]); ties go to the lowest index and NaN never wins (an all-NaN row
+// gives 0). Two passes: chunks of kArgChunk logits per work-group (16-byte
+// loads), then one wave per row over the chunk winners.
+constexpr int kArgChunk = 8192;
+
+__device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
+__global__ __launch_bounds__(kRowThreads) void argmax_part_kernel(const uint16_t* __restrict__ logits,
+                                                                  int64_t ld, int vocab, int nchunk,
+                                                                  float* __restrict__ pv,
+                                                                  int* __restrict__ pi) {
   __shared__ float bvs[4];
   __shared__ int bis[4];
-  const uint16_t* row = logits + (size_t)blockIdx.x * ld;
+  const int chunk = blockIdx.x, r = blockIdx.y;
+  const uint16_t* row = logits + (size_t)r * ld;
   float bv = -INFINITY;
-  int bi = vocab;  // no candidate yet
-  for (int c = threadIdx.x; c < vocab; c += kRowThreads) {
-    const float x = bf2f(row[c]);
-    if (x > bv || (bi == vocab && x == bv)) {  // first -inf still counts
-      bv = x;
-      bi = c;
+  int bi = INT_MAX;  // no candidate yet
+#pragma unroll
+  for (int k = 0; k < kArgChunk / (8 * kRowThreads); ++k) {
+    const int e = chunk * kArgChunk + 8 * (k * kRowThreads + threadIdx.x);
+    if (e < vocab) {  // vocab is a multiple of 8
+      const uint4 q = *reinterpret_cast<const uint4*>(row + e);
+      const uint32_t* qw = reinterpret_cast<const uint32_t*>(&q);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float a = bf_lo(qw[u]), b = bf_hi(qw[u]);
+        if (a > bv || (bi == INT_MAX && a == bv)) { bv = a; bi = e + 2 * u; }
+        if (b > bv || (bi == INT_MAX && b == bv)) { bv = b; bi = e + 2 * u + 1; }
+      }
     }
   }
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const float ov = __shfl_xor(bv, off, 64);
-    const int oi = __shfl_xor(bi, off, 64);
-    if (ov > bv || (ov == bv && oi < bi)) {
-      bv = ov;
-      bi = oi;
-    }
-  }
+  for (int off = 32; off > 0; off >>= 1)
+    better(bv, bi, __shfl_xor(bv, off, 64), __shfl_xor(bi, off, 64));
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
     bvs[wave] = bv;
@@ -108,13 +144,27 @@ __global__ __launch_bounds__(kRowThreads) void argmax_kernel(const uint16_t* __r
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int k = 1; k < 4; ++k)
-      if (bvs[k] > bv || (bvs[k] == bv && bis[k] < bi)) {
-        bv = bvs[k];
-        bi = bis[k];
-      }
-    out[blockIdx.x] = bi == vocab ? 0 : bi;
+    for (int k = 1; k < 4; ++k) better(bv, bi, bvs[k], bis[k]);
+    pv[(size_t)r * nchunk + chunk] = bv;
+    pi[(size_t)r * nchunk + chunk] = bi;
   }
+}
+
+__global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restrict__ pv,
+                                                          const int* __restrict__ pi, int nchunk,
+                                                          int32_t* __restrict__ out) {
+  const int r = blockIdx.x;
+  float bv = -INFINITY;
+  int bi = INT_MAX;
+  for (int c = threadIdx.x; c < nchunk; c += 64) {
+    const float v = pv[(size_t)r * nchunk + c];
+    const int i = pi[(size_t)r * nchunk + c];
+    if (i != INT_MAX) better(bv, bi, v, i);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1)
+    better(bv, bi, __shfl_xor(bv, off, 64), __shfl_xor(bi, off, 64));
+  if (threadIdx.x == 0) out[r] = bi == INT_MAX ? 0 : bi;
 }
 
 hipError_t launch_embed(const uint16_t* table, const int32_t* tok, int n, int vocab, int hidden,
@@ -127,15 +177,22 @@ hipError_t launch_embed(const uint16_t* table, const int32_t* tok, int n, int vo
 hipError_t launch_add_norm(uint16_t* h, const uint16_t* d, int n, int hidden, const uint16_t* w,
                            float eps, uint16_t* hn, hipStream_t s) {
   if (n <= 0) return hipSuccess;
-  if (hidden > kRowThreads * kMaxHiddenPerThread) return hipErrorInvalidValue;
+  if (hidden > kRowThreads * kMaxHiddenPerThread || hidden % 8) return hipErrorInvalidValue;
   hipLaunchKernelGGL(add_norm_kernel, dim3(n), dim3(kRowThreads), 0, s, h, d, hidden, w, eps, hn);
   return hipGetLastError();
 }
 
-hipError_t launch_argmax(const uint16_t* logits, int64_t ld, int n, int vocab, int32_t* out,
-                         hipStream_t s) {
+int argmax_chunks(int vocab) { return (vocab + kArgChunk - 1) / kArgChunk; }
+
+hipError_t launch_argmax(const uint16_t* logits, int64_t ld, int n, int vocab, float* pv, int* pi,
+                         int32_t* out, hipStream_t s) {
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(argmax_kernel, dim3(n), dim3(kRowThreads), 0, s, logits, ld, vocab, out);
+  const int nc = argmax_chunks(vocab);
+  hipLaunchKernelGGL(argmax_part_kernel, dim3(nc, n), dim3(kRowThreads), 0, s, logits, ld, vocab,
+                     nc, pv, pi);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(n), dim3(64), 0, s, pv, pi, nc, out);
   return hipGetLastError();
 }
 

@@ -294,20 +294,31 @@ __global__ __launch_bounds__(256) void qlinear_kernel(
 // scale slice and its correction operands, then x three stages ahead of use.
 // Vector-memory counters drain in issue order, so each stage waits only for
 // its own weights and x, never for the loads queued behind them.
+//
+// A work-group covers the K slice [kof, kof + 128 KS S) of a K-wide layer,
+// kof = 128 KS S * blockIdx.y. With one slice (gridDim.y == 1) it writes bf16
+// y; with several (layers too narrow in N to fill the chip) it writes its f32
+// partial sums, correction of its own groups included, to
+// part[blockIdx.y][m][n] (row stride Npad), and qlinear_sum_kernel adds the
+// slices in order and rounds once.
 template <int KS, int S>
 __global__ __launch_bounds__(256 * KS) void qlinear_decode_kernel(
     const uint16_t* __restrict__ x, int64_t xs, int M, int K, const u32x4* __restrict__ wp,
     const uint16_t* __restrict__ sp, const uint16_t* __restrict__ bias,
-    const uint16_t* __restrict__ nsc, int N, uint16_t* __restrict__ y, int64_t ys) {
+    const uint16_t* __restrict__ nsc, int N, uint16_t* __restrict__ y, int64_t ys,
+    float* __restrict__ part, int Npad) {
   static_assert(S >= 2 && S % 2 == 0, "S stages per K part, alternating x buffers");
   constexpr int MT = 64, XROW = kStageK * 2, SJ = MT / 16;
+  constexpr int G = 2 * KS * S;  // groups of the work-group's K slice
   __shared__ __align__(16) uint8_t xl[KS][2][MT * XROW];
-  __shared__ float sx[kMaxGroups * MT];  // X_g[m] at sx[g*MT + m]
+  __shared__ float sx[G * MT];  // X_g[m] at sx[g*MT + m], g local to the slice
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ks = wave >> 2, wn = wave & 3;
-  const int G = K >> 6, P = K >> 7, p0 = ks * S;  // P == KS * S (host)
+  const int Ptot = K >> 7, Gtot = K >> 6;
+  const int pbase = blockIdx.y * (KS * S);  // first stage of the slice in the layer
+  const int p0 = ks * S;                    // first stage of the wave's K part in the slice
   const int f = blockIdx.x * 4 + wn;  // the wave's column fragment
   const int r16 = lane & 15, c4 = lane >> 4;
 
@@ -317,7 +328,7 @@ __global__ __launch_bounds__(256 * KS) void qlinear_decode_kernel(
   const uint16_t* xsrc[SJ];
 #pragma unroll
   for (int j = 0; j < SJ; ++j)
-    xsrc[j] = x + (int64_t)min(srow + 16 * j, M - 1) * xs + sch * 8 + p0 * kStageK;
+    xsrc[j] = x + (int64_t)min(srow + 16 * j, M - 1) * xs + sch * 8 + (pbase + p0) * kStageK;
   constexpr int XD = S < 3 ? S : 3;  // x stages in flight
   u32x4 R[XD][SJ];
 #pragma unroll
@@ -329,8 +340,8 @@ __global__ __launch_bounds__(256 * KS) void qlinear_decode_kernel(
 
   // Weights, scales and the correction operands are read once: nontemporal,
   // so the stream does not evict x, which every work-group re-reads, from L2.
-  const u32x4* wsrc = wp + ((int64_t)f * P + p0) * 64 + lane;
-  const u32x4* ssrc = reinterpret_cast<const u32x4*>(sp) + ((int64_t)f * P + p0) * 4 + c4;
+  const u32x4* wsrc = wp + ((int64_t)f * Ptot + pbase + p0) * 64 + lane;
+  const u32x4* ssrc = reinterpret_cast<const u32x4*>(sp) + ((int64_t)f * Ptot + pbase + p0) * 4 + c4;
   u32x4 wr[S], sr[S];
 #pragma unroll
   for (int p = 0; p < S; ++p) {
@@ -338,13 +349,13 @@ __global__ __launch_bounds__(256 * KS) void qlinear_decode_kernel(
     sr[p] = __builtin_nontemporal_load(ssrc + p * 4);
     __builtin_amdgcn_sched_barrier(0);
   }
-  constexpr int GJ = (2 * KS * S + 31) / 32;  // 32-group blocks of the correction
+  constexpr int GJ = (G + 31) / 32;  // 32-group blocks of the correction
   u32x4 Ab[GJ], As[GJ];
 #pragma unroll
   for (int j = 0; j < GJ; ++j) {
     Ab[j] = As[j] = (u32x4){0u, 0u, 0u, 0u};
-    if (32 * j + 8 * c4 < G) {
-      const int64_t o = ((int64_t)f * 16 + r16) * G + 32 * j + 8 * c4;
+    if (32 * j + 8 * c4 < G) {  // G is a multiple of 8: whole 8-group words
+      const int64_t o = ((int64_t)f * 16 + r16) * Gtot + 2 * pbase + 32 * j + 8 * c4;
       Ab[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bias + o));
       As[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(nsc + o));
     }
@@ -459,7 +470,14 @@ __global__ __launch_bounds__(256 * KS) void qlinear_decode_kernel(
   }
 
   const int n = f * 16 + 4 * c4;
-  if (n < N) {
+  if (part != nullptr) {  // f32 partial of this K slice (all Npad columns)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int m = u * 16 + r16;
+      if (m < M)
+        *reinterpret_cast<f32x4*>(part + ((int64_t)blockIdx.y * MT + m) * Npad + n) = T[u];
+    }
+  } else if (n < N) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int m = u * 16 + r16;
@@ -468,6 +486,22 @@ __global__ __launch_bounds__(256 * KS) void qlinear_decode_kernel(
             (u32x2){f2bf2(T[u][0], T[u][1]), f2bf2(T[u][2], T[u][3])};
     }
   }
+}
+
+// y[m, n..n+3] = bf16(sum over the K slices, in slice order, of the f32
+// partials of qlinear_decode_kernel). grid ceil(M * Npad / 4 / 256), block 256.
+__global__ __launch_bounds__(256) void qlinear_sum_kernel(const float* __restrict__ part,
+                                                          int nslice, int M, int N, int Npad,
+                                                          uint16_t* __restrict__ y, int64_t ys) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // float4 index in [M, Npad]
+  const int q = Npad / 4;
+  if (i >= (int64_t)M * q) return;
+  const int m = (int)(i / q), n = (int)(i % q) * 4;
+  if (n >= N) return;
+  f32x4 t = *reinterpret_cast<const f32x4*>(part + (int64_t)m * Npad + n);
+  for (int sl = 1; sl < nslice; ++sl)
+    t += *reinterpret_cast<const f32x4*>(part + ((int64_t)sl * 64 + m) * Npad + n);
+  *reinterpret_cast<u32x2*>(y + (int64_t)m * ys + n) = (u32x2){f2bf2(t[0], t[1]), f2bf2(t[2], t[3])};
 }
 
 template <int MW, int NW, int WM, int WN>
@@ -491,17 +525,41 @@ hipError_t launch_qlinear_pack(const QLinearPackArgs& a) {
   return hipGetLastError();
 }
 
-// Tile choice: up to 64 rows (batched decode) with K up to 2048
-// qlinear_decode_kernel; otherwise 128 x 128 tiles (prefill).
+int qlinear_decode_slices(int K, int Npad) {
+  // one work-group per 64 columns; layers with fewer than 128 such groups
+  // (out_proj: 2048 columns), and every K above 2048, split K into 512-wide
+  // slices (K <= 4096: at most 8)
+  if (K <= 512 || (K <= 2048 && Npad / 64 >= 128)) return 1;
+  return K / 512;
+}
+
+// Tile choice: up to 64 rows (batched decode) qlinear_decode_kernel, whole K
+// (K <= 2048) or K slices of 512 (narrow layers, and every K above 2048 --
+// those always get a workspace); otherwise 128 x 128 tiles (prefill).
 hipError_t launch_qlinear(const QLinearArgs& a) {
-  if (a.M <= 64 && (a.K == 512 || a.K == 1024 || a.K == 2048)) {
-    // two K parts of S = K/256 stages each
-    auto kern = a.K == 2048   ? qlinear_decode_kernel<2, 8>
-                : a.K == 1024 ? qlinear_decode_kernel<2, 4>
-                              : qlinear_decode_kernel<2, 2>;
-    hipLaunchKernelGGL(kern, dim3(a.Npad / 64), dim3(512), 0, a.stream, a.x, a.xs, a.M, a.K,
-                       reinterpret_cast<const u32x4*>(a.wp), a.sp, a.bias, a.nsc, a.N, a.y, a.ys);
-    return hipGetLastError();
+  if (a.M <= 64) {
+    const int ns = a.part ? qlinear_decode_slices(a.K, a.Npad) : 1;
+    if (ns > 1 || a.K == 512 || a.K == 1024 || a.K == 2048) {
+      const u32x4* wp = reinterpret_cast<const u32x4*>(a.wp);
+      if (ns > 1) {  // 512-wide slices: two K parts of two stages
+        hipLaunchKernelGGL((qlinear_decode_kernel<2, 2>), dim3(a.Npad / 64, ns), dim3(512), 0,
+                           a.stream, a.x, a.xs, a.M, a.K, wp, a.sp, a.bias, a.nsc, a.N, a.y, a.ys,
+                           a.part, a.Npad);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const int64_t n4 = (int64_t)a.M * (a.Npad / 4);
+        hipLaunchKernelGGL(qlinear_sum_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0,
+                           a.stream, a.part, ns, a.M, a.N, a.Npad, a.y, a.ys);
+        return hipGetLastError();
+      }
+      // two K parts of S = K/256 stages each
+      auto kern = a.K == 2048   ? qlinear_decode_kernel<2, 8>
+                  : a.K == 1024 ? qlinear_decode_kernel<2, 4>
+                                : qlinear_decode_kernel<2, 2>;
+      hipLaunchKernelGGL(kern, dim3(a.Npad / 64), dim3(512), 0, a.stream, a.x, a.xs, a.M, a.K, wp,
+                         a.sp, a.bias, a.nsc, a.N, a.y, a.ys, nullptr, a.Npad);
+      return hipGetLastError();
+    }
   }
   return launch_cfg<4, 4, 2, 2>(a);
 }

@@ -21,7 +21,7 @@ from gdn_testlib import O, DV, dev, quantize_w4, rel_l2, say
 
 pytestmark = pytest.mark.gpu
 
-HK, HV, HIDDEN, VOCAB, LAYERS = 4, 16, 1024, 2048, 3
+HK, HV, HIDDEN, VOCAB, LAYERS = 4, 16, 1024, 10240, 3  # vocab: two greedy-pick chunks
 EPS = 1e-6
 
 
