@@ -170,17 +170,20 @@ __global__ __launch_bounds__(256) void qlinear_kernel(
   uint32_t nib = 0x000F000Fu;
   asm volatile("" : "+v"(nib));  // keep the nibble mask in a VGPR
 
+  // Straight-line stage body: the last stage reloads itself and writes the
+  // idle LDS buffer instead of branching (a branch around the prefetch made
+  // the compiler keep more registers live and cost 5%).
   for (int p = 0; p < P; ++p) {
     const int buf = p & 1;
-    const bool more = p + 1 < P;
-    if (more) {
+    const int pn = min(p + 1, P - 1);
+    {
 #pragma unroll
       for (int j = 0; j < SJ; ++j)
-        stg[j] = *reinterpret_cast<const u32x4*>(xsrc[j] + (p + 1) * kStageK);
+        stg[j] = *reinterpret_cast<const u32x4*>(xsrc[j] + pn * kStageK);
 #pragma unroll
       for (int i = 0; i < NW; ++i) {
-        wnx[i] = wsrc[i][(p + 1) * 64];
-        snx[i] = ssrc[i][(p + 1) * 4];
+        wnx[i] = wsrc[i][pn * 64];
+        snx[i] = ssrc[i][pn * 4];
       }
     }
 #pragma unroll
@@ -200,7 +203,7 @@ __global__ __launch_bounds__(256) void qlinear_kernel(
         if (u % WN == wn) {
           f32x4 a = mfma(ones, X[u][0], zero);
           a = mfma(ones, X[u][1], a);
-          if (c4 == 0) sx[(2 * p + gl) * MT + (wm * MW + u) * 16 + r16] = a[0];
+          sx[(2 * p + gl) * MT + (wm * MW + u) * 16 + r16] = a[0];  // the 4 lane groups agree
         }
 #pragma unroll
       for (int i = 0; i < NW; ++i) {
@@ -217,7 +220,7 @@ __global__ __launch_bounds__(256) void qlinear_kernel(
         }
       }
     }
-    if (more) {
+    {
 #pragma unroll
       for (int j = 0; j < SJ; ++j)
         *reinterpret_cast<u32x4*>(&xl[buf ^ 1][sdst + 16 * j * XROW]) = stg[j];
@@ -535,7 +538,14 @@ int qlinear_decode_slices(int K, int Npad) {
 
 // Tile choice: up to 64 rows (batched decode) qlinear_decode_kernel, whole K
 // (K <= 2048) or K slices of 512 (narrow layers, and every K above 2048 --
-// those always get a workspace); otherwise 128 x 128 tiles (prefill).
+// those always get a workspace); otherwise 64 x 128 tiles (prefill). Of the
+// tilings swept at 16384 x 2048 -> 12352 (four waves each, 16-wide fragments
+// per wave m x n: 4x4, 2x4, 4x2, 2x2, 2x4 in one row of waves, 1x4, 2x2 in
+// one column), 2 x 4 fragments per wave in a 2 x 2 wave grid was fastest:
+// about 200 VGPRs and 48 KB of LDS give two waves per SIMD (1.42 ms; 4 x 4
+// with one wave per SIMD took 1.98 ms). Deeper x prefetch (two stages in
+// registers) pushed it to one wave per SIMD and 2.06 ms; an XCD-aware tile
+// order (each XCD's L2 holding its own weight columns) changed nothing.
 hipError_t launch_qlinear(const QLinearArgs& a) {
   if (a.M <= 64) {
     const int ns = a.part ? qlinear_decode_slices(a.K, a.Npad) : 1;
@@ -561,7 +571,7 @@ hipError_t launch_qlinear(const QLinearArgs& a) {
       return hipGetLastError();
     }
   }
-  return launch_cfg<4, 4, 2, 2>(a);
+  return launch_cfg<2, 4, 2, 2>(a);
 }
 
 }  // namespace gdn
