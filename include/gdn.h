@@ -36,6 +36,11 @@
  *     one stream; a call with a new maximum total_tokens synchronizes its
  *     stream and reallocates it, later calls at or below that size allocate
  *     nothing. gdn_decode allocates nothing.
+ *   - The decode entries launch kernels only (no memset nodes, no host
+ *     synchronisation), so a decode step over every layer can be captured in
+ *     one HIP graph and replayed: gdn_decode, gdn_decode_gated, gdn_recurrent,
+ *     gdn_slots_zero, gdn_qlinear_forward, and gdn_layer_decode once
+ *     gdn_pool_reserve has sized the pool's buffers for the batch.
  *   - Model shape limits: head_k_dim == head_v_dim == 128, conv_kernel == 4,
  *     num_v_heads / num_k_heads in {1, 2, 4}.
  *
