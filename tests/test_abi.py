@@ -81,3 +81,39 @@ def test_qlinear_rejects_unsupported_formats_on_host():
         == gdn_amd.GDN_ERR_INVALID
     assert lib.gdn_qlinear_forward(None, None, 0, 1, None, 0, None) == gdn_amd.GDN_ERR_INVALID
     assert lib.gdn_qlinear_destroy(None) == gdn_amd.GDN_OK
+
+
+def test_layer_and_executor_entries_reject_null_on_host():
+    """The whole-layer, reserve, gated-prefill and executor entries check their
+    handles and descriptors before touching a device."""
+    lib = gdn_amd.load()
+    h = ctypes.c_void_p()
+    E = gdn_amd.GDN_ERR_INVALID
+    assert lib.gdn_layer_create(None, ctypes.byref(h)) == E
+    desc = gdn_amd.LayerDesc()  # NULL pool
+    assert lib.gdn_layer_create(ctypes.byref(desc), ctypes.byref(h)) == E
+    assert h.value is None
+    assert lib.gdn_layer_destroy(None) == gdn_amd.GDN_OK
+    assert lib.gdn_layer_decode(None, None, 1, None, 0, None, 0, None) == E
+    assert lib.gdn_layer_prefill(None, None, None, 1, 4, None, 0, None, 0, None) == E
+    assert lib.gdn_pool_reserve(None, 16, None) == E
+    assert lib.gdn_prefill_varlen_gated(None, 0, None, None, 1, 1, None, 0, None, 0, None, None,
+                                        None, None, ctypes.c_float(1e-6), None, None,
+                                        None) == E
+    assert lib.gdn_exec_create(None, None, ctypes.byref(h)) == E
+    ed = gdn_amd.ExecDesc()  # NULL pool / weights
+    assert lib.gdn_exec_create(ctypes.byref(ed), None, ctypes.byref(h)) == E
+    assert h.value is None
+    assert b"NULL" in lib.gdn_last_error()
+    assert lib.gdn_exec_destroy(None) == gdn_amd.GDN_OK
+    tok = ctypes.c_uint32()
+    prompt = (ctypes.c_int32 * 1)(0)
+    ids = (ctypes.c_uint64 * 1)(1)
+    toks = (ctypes.c_uint32 * 1)(0)
+    assert lib.gdn_exec_prefill(None, 1, prompt, 1, ctypes.byref(tok)) == E
+    assert lib.gdn_exec_decode_batch(None, ids, toks, 1, toks) == E
+    assert lib.gdn_exec_submit_batch(None, ids, toks, 1) == E
+    assert lib.gdn_exec_collect_batch(None, toks, 1) == E
+    assert lib.gdn_exec_release(None, 1) == E
+    assert lib.gdn_exec_max_batch_size(None) == 0
+    assert lib.gdn_exec_supports_pipeline(None) == 0
