@@ -353,7 +353,20 @@ def exec_bench(args):
     ex = gdn_amd.Executor(pool, gl, in_norm, fin, embed, head, 1e-6, max_batch=B, max_prompt=64)
     rng = torch.Generator().manual_seed(args.seed)
     ids = list(range(1, B + 1))
-    cur = [ex.prefill(i, torch.randint(0, V, (16,), generator=rng).tolist()) for i in ids]
+    prompts = [torch.randint(0, V, (16,), generator=rng).tolist() for _ in ids]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    cur = [ex.prefill(i, p) for i, p in zip(ids, prompts)]
+    pre_one = (time.perf_counter() - t0) / B
+    # the same prompts again (known sequences start over), four per call
+    g = min(4, B)
+    t0 = time.perf_counter()
+    again = []
+    for k in range(0, B, g):
+        again += ex.prefill_batch(ids[k:k + g], prompts[k:k + g])
+    pre_batched = (time.perf_counter() - t0) / B
+    if again != cur:
+        print("batched prefill picked other first tokens than single prefills", file=sys.stderr)
     for _ in range(args.warmup):
         cur = ex.decode_batch(ids, cur)
     torch.cuda.synchronize()
@@ -388,6 +401,8 @@ def exec_bench(args):
                                f"{args.slots}-slot pools",
                    "layers": L, "batch": B, "slots": args.slots, "hidden": QL_HIDDEN,
                    "vocab": V},
+        "prefill_ms_per_sequence": {"prompt_tokens": 16, "one_per_call": round(pre_one * 1e3, 3),
+                                    f"{g}_per_call": round(pre_batched * 1e3, 3)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
                      "algorithmic_bytes_per_step": step_bytes,

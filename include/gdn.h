@@ -375,6 +375,18 @@ gdn_status gdn_exec_destroy(gdn_exec* exec);
 gdn_status gdn_exec_prefill(gdn_exec* exec, uint64_t seq_id, const int32_t* prompt, int32_t len,
                             uint32_t* first_token);
 
+/* Prefill of nseq <= max_batch distinct sequences in one pass: the prompts are
+ * packed back to back in `prompts` (lens[i] >= 1 tokens each, at most
+ * max_prompt in total) and share every layer's varlen prefill launches
+ * (the reference prefills one sequence per call, scheduler.rs:196-216).
+ * first_tokens[i] is sequence i's first picked token. The projections' row
+ * count changes with the packing, and with it their f32 summation order, so
+ * results equal separate prefills up to that rounding. A call that finds no
+ * free slot for some sequence admits none of its new sequences. */
+gdn_status gdn_exec_prefill_batch(gdn_exec* exec, int32_t nseq, const uint64_t* seq_ids,
+                                  const int32_t* prompts, const int32_t* lens,
+                                  uint32_t* first_tokens);
+
 /* ModelExecutor::decode_batch (executor.rs:26): one token for each of B
  * prefilled, distinct sequences, fed their current tokens; the results in
  * input order. = submit_batch + collect_batch. */

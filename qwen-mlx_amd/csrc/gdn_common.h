@@ -239,6 +239,8 @@ hipError_t launch_embed(const uint16_t* table, const int32_t* tok, int n, int vo
                         uint16_t* h, hipStream_t s);
 hipError_t launch_add_norm(uint16_t* h, const uint16_t* d, int n, int hidden, const uint16_t* w,
                            float eps, uint16_t* hn, hipStream_t s);
+hipError_t launch_gather_rows(const uint16_t* src, const int32_t* idx, int n, int hidden,
+                              uint16_t* dst, hipStream_t s);
 // Greedy pick in two passes; pv / pi hold n * argmax_chunks(vocab) partials.
 int argmax_chunks(int vocab);
 hipError_t launch_argmax(const uint16_t* logits, int64_t ld, int n, int vocab, float* pv, int* pi,

@@ -63,10 +63,11 @@ struct gdn_exec {
   int hidden = 0, vocab = 0, max_batch = 0, max_prompt = 0, rows = 0;
   int device = 0;
   hipStream_t stream = nullptr;
-  hipEvent_t done = nullptr;
+  hipEvent_t done = nullptr;         // a submitted batch's tokens are in p_next
+  hipEvent_t pre_copied = nullptr;   // the prefill block has left p_pre
   // device buffers
   int32_t* d_dec = nullptr;   // [2 * max_batch]: slots, then tokens
-  int32_t* d_pre = nullptr;   // [3 + max_prompt]: slot, cu[0..1], prompt
+  int32_t* d_pre = nullptr;   // prefill block, pre_words(): slots, cu, last rows, tokens
   int32_t* d_next = nullptr;  // [max_batch] picked tokens
   uint16_t* h = nullptr;      // residual stream [rows, hidden]
   uint16_t* hn = nullptr;     // normed rows fed to a layer
@@ -79,7 +80,7 @@ struct gdn_exec {
   int32_t* p_dec = nullptr;
   int32_t* p_pre = nullptr;
   int32_t* p_next = nullptr;   // a batch's picked tokens
-  int32_t* p_first = nullptr;  // a prefill's first token
+  int32_t* p_first = nullptr;  // a prefill's first tokens [max_batch]
   std::unordered_map<uint64_t, int32_t> slot_of;
   bool inflight = false;
   int32_t inflight_B = 0;
@@ -97,6 +98,7 @@ void exec_release(gdn_exec* x) {
   for (void* p : {(void*)x->p_dec, (void*)x->p_pre, (void*)x->p_next, (void*)x->p_first})
     if (p) (void)hipHostFree(p);
   if (x->done) (void)hipEventDestroy(x->done);
+  if (x->pre_copied) (void)hipEventDestroy(x->pre_copied);
   for (auto& kv : x->slot_of) (void)gdn_slot_free(x->pool, kv.second);
   delete x;
 }
@@ -113,17 +115,24 @@ struct DevScope {
   }
 };
 
+// Words of the pinned / device prefill block: nseq slots, nseq + 1 cu_seqlens,
+// nseq last-row indices (at most max_batch sequences each), then the packed
+// prompt tokens (at most max_prompt).
+size_t pre_words(int max_batch, int max_prompt) {
+  return 3 * (size_t)max_batch + 1 + (size_t)max_prompt;
+}
+
 // The model body over n rows of h that hold the embedded tokens: every GDN
-// layer with its residual seam, then the final norm into hn.
-gdn_status run_layers(gdn_exec* x, int n, bool prefill) {
+// layer with its residual seam. Prefill rows are nseq packed sequences.
+gdn_status run_layers(gdn_exec* x, int n, bool prefill, int nseq = 0) {
   const int32_t* slots = prefill ? x->d_pre : x->d_dec;
   for (size_t l = 0; l < x->layers.size(); ++l) {
     HIP_TRY(gdn::launch_add_norm(x->h, l == 0 ? nullptr : x->mix, n, x->hidden, x->norm_w[l],
                                  x->eps, x->hn, x->stream),
             "residual add + norm");
     if (prefill)
-      GDN_TRY(gdn_layer_prefill(x->layers[l], slots, x->d_pre + 1, 1, n, x->hn, x->hidden, x->mix,
-                                x->hidden, x->stream));
+      GDN_TRY(gdn_layer_prefill(x->layers[l], slots, x->d_pre + nseq, nseq, n, x->hn, x->hidden,
+                                x->mix, x->hidden, x->stream));
     else
       GDN_TRY(gdn_layer_decode(x->layers[l], slots, n, x->hn, x->hidden, x->mix, x->hidden,
                                x->stream));
@@ -189,7 +198,7 @@ gdn_status gdn_exec_create(const gdn_exec_desc* desc, void* stream, gdn_exec** o
   x->stream = static_cast<hipStream_t>(stream);
   const size_t act = (size_t)x->rows * hidden * sizeof(uint16_t);
   bool ok = hipMalloc(&x->d_dec, sizeof(int32_t) * 2 * d.max_batch) == hipSuccess &&
-            hipMalloc(&x->d_pre, sizeof(int32_t) * (3 + (size_t)d.max_prompt)) == hipSuccess &&
+            hipMalloc(&x->d_pre, sizeof(int32_t) * pre_words(d.max_batch, d.max_prompt)) == hipSuccess &&
             hipMalloc(&x->d_next, sizeof(int32_t) * d.max_batch) == hipSuccess &&
             hipMalloc(&x->h, act) == hipSuccess && hipMalloc(&x->hn, act) == hipSuccess &&
             hipMalloc(&x->mix, act) == hipSuccess &&
@@ -197,10 +206,11 @@ gdn_status gdn_exec_create(const gdn_exec_desc* desc, void* stream, gdn_exec** o
             hipMalloc(&x->d_pv, sizeof(float) * d.max_batch * gdn::argmax_chunks(vocab)) == hipSuccess &&
             hipMalloc(&x->d_pi, sizeof(int) * d.max_batch * gdn::argmax_chunks(vocab)) == hipSuccess &&
             hipHostMalloc(&x->p_dec, sizeof(int32_t) * 2 * d.max_batch, 0) == hipSuccess &&
-            hipHostMalloc(&x->p_pre, sizeof(int32_t) * (3 + (size_t)d.max_prompt), 0) == hipSuccess &&
+            hipHostMalloc(&x->p_pre, sizeof(int32_t) * pre_words(d.max_batch, d.max_prompt), 0) == hipSuccess &&
             hipHostMalloc(&x->p_next, sizeof(int32_t) * d.max_batch, 0) == hipSuccess &&
-            hipHostMalloc(&x->p_first, sizeof(int32_t), 0) == hipSuccess &&
-            hipEventCreateWithFlags(&x->done, hipEventDisableTiming) == hipSuccess;
+            hipHostMalloc(&x->p_first, sizeof(int32_t) * d.max_batch, 0) == hipSuccess &&
+            hipEventCreateWithFlags(&x->done, hipEventDisableTiming) == hipSuccess &&
+            hipEventCreateWithFlags(&x->pre_copied, hipEventDisableTiming) == hipSuccess;
   if (!ok) {
     (void)hipGetLastError();
     exec_release(x);
@@ -221,45 +231,99 @@ gdn_status gdn_exec_destroy(gdn_exec* x) {
   return GDN_OK;
 }
 
-gdn_status gdn_exec_prefill(gdn_exec* x, uint64_t seq_id, const int32_t* prompt, int32_t len,
-                            uint32_t* first_token) {
-  if (!x || !prompt || !first_token) return efail(GDN_ERR_INVALID, "gdn_exec_prefill: NULL argument");
-  if (len < 1 || len > x->max_prompt)
-    return efail(GDN_ERR_INVALID, "gdn_exec_prefill: prompt length %d outside [1, %d]", len,
-                 x->max_prompt);
-  for (int i = 0; i < len; ++i)
-    if (prompt[i] < 0 || prompt[i] >= x->vocab)
-      return efail(GDN_ERR_INVALID, "gdn_exec_prefill: token %d at %d outside [0, %d)", prompt[i],
-                   i, x->vocab);
-  DevScope dev(x->device);
-  // admit: a fresh sequence gets a free slot; a known one starts over
-  int32_t slot;
-  auto it = x->slot_of.find(seq_id);
-  if (it != x->slot_of.end()) {
-    slot = it->second;
-  } else {
-    if (gdn_slot_alloc(x->pool, &slot) != GDN_OK)
-      return efail(GDN_ERR_SLOTS, "gdn_exec_prefill: no free slot for sequence %llu",
-                   (unsigned long long)seq_id);
-    x->slot_of.emplace(seq_id, slot);
+gdn_status gdn_exec_prefill_batch(gdn_exec* x, int32_t nseq, const uint64_t* seq_ids,
+                                  const int32_t* prompts, const int32_t* lens,
+                                  uint32_t* first_tokens) {
+  if (!x || !seq_ids || !prompts || !lens || !first_tokens)
+    return efail(GDN_ERR_INVALID, "gdn_exec_prefill: NULL argument");
+  if (nseq < 1 || nseq > x->max_batch)
+    return efail(GDN_ERR_INVALID, "gdn_exec_prefill: %d sequences outside [1, %d]", nseq,
+                 x->max_batch);
+  int64_t total = 0;
+  std::unordered_set<uint64_t> seen;
+  for (int i = 0; i < nseq; ++i) {
+    if (lens[i] < 1)
+      return efail(GDN_ERR_INVALID, "gdn_exec_prefill: prompt %d has length %d < 1", i, lens[i]);
+    if (!seen.insert(seq_ids[i]).second)
+      return efail(GDN_ERR_INVALID, "gdn_exec_prefill: sequence %llu appears twice",
+                   (unsigned long long)seq_ids[i]);
+    total += lens[i];
   }
-  // the pinned prefill block may still feed an earlier prefill's copy only if
-  // that call failed half-way; prefill syncs at its end, so it is free here
-  x->p_pre[0] = slot;
-  x->p_pre[1] = 0;
-  x->p_pre[2] = len;
-  for (int i = 0; i < len; ++i) x->p_pre[3 + i] = prompt[i];
-  HIP_TRY(hipMemcpyAsync(x->d_pre, x->p_pre, sizeof(int32_t) * (3 + (size_t)len),
+  if (total > x->max_prompt)
+    return efail(GDN_ERR_INVALID, "gdn_exec_prefill: %lld prompt tokens > max_prompt %d",
+                 (long long)total, x->max_prompt);
+  for (int64_t t = 0; t < total; ++t)
+    if (prompts[t] < 0 || prompts[t] >= x->vocab)
+      return efail(GDN_ERR_INVALID, "gdn_exec_prefill: token %d at %lld outside [0, %d)",
+                   prompts[t], (long long)t, x->vocab);
+  DevScope dev(x->device);
+  // The pinned block is free once the previous prefill's copy has run (a
+  // prefill that failed after queueing it may not have waited).
+  HIP_TRY(hipEventSynchronize(x->pre_copied), "gdn_exec_prefill");
+  // admit: a fresh sequence gets a free slot, a known one starts over in its
+  // own; a call that runs out of slots gives back the ones it took
+  int32_t* slots = x->p_pre;
+  std::vector<int> fresh;
+  for (int i = 0; i < nseq; ++i) {
+    auto it = x->slot_of.find(seq_ids[i]);
+    if (it != x->slot_of.end()) {
+      slots[i] = it->second;
+      continue;
+    }
+    if (gdn_slot_alloc(x->pool, &slots[i]) != GDN_OK) {
+      for (int k : fresh) {
+        (void)gdn_slot_free(x->pool, slots[k]);
+        x->slot_of.erase(seq_ids[k]);
+      }
+      return efail(GDN_ERR_SLOTS, "gdn_exec_prefill: no free slot for sequence %llu",
+                   (unsigned long long)seq_ids[i]);
+    }
+    x->slot_of.emplace(seq_ids[i], slots[i]);
+    fresh.push_back(i);
+  }
+  int32_t* cu = x->p_pre + nseq;
+  int32_t* last = cu + nseq + 1;
+  int32_t* toks = last + nseq;
+  cu[0] = 0;
+  for (int i = 0; i < nseq; ++i) {
+    cu[i + 1] = cu[i] + lens[i];
+    last[i] = cu[i + 1] - 1;
+  }
+  for (int64_t t = 0; t < total; ++t) toks[t] = prompts[t];
+  const int32_t* d_cu = x->d_pre + nseq;
+  const int32_t* d_last = d_cu + nseq + 1;
+  const int32_t* d_toks = d_last + nseq;
+  HIP_TRY(hipMemcpyAsync(x->d_pre, x->p_pre, sizeof(int32_t) * (3 * (size_t)nseq + 1 + total),
                          hipMemcpyHostToDevice, x->stream),
           "prompt copy");
-  GDN_TRY(gdn_slots_zero(x->pool, GDN_ALL_LAYERS, x->d_pre, 1, x->stream));
-  HIP_TRY(gdn::launch_embed(x->embed, x->d_pre + 3, len, x->vocab, x->hidden, x->h, x->stream),
+  HIP_TRY(hipEventRecord(x->pre_copied, x->stream), "prompt copy event");
+  GDN_TRY(gdn_slots_zero(x->pool, GDN_ALL_LAYERS, x->d_pre, nseq, x->stream));
+  const int n = (int)total;
+  HIP_TRY(gdn::launch_embed(x->embed, d_toks, n, x->vocab, x->hidden, x->h, x->stream),
           "embedding");
-  GDN_TRY(run_layers(x, len, true));
-  GDN_TRY(pick(x, len - 1, 1, x->p_first));
+  GDN_TRY(run_layers(x, n, true, nseq));
+  // final residual add + norm of every row, then each prompt's last row
+  HIP_TRY(gdn::launch_add_norm(x->h, x->layers.empty() ? nullptr : x->mix, n, x->hidden,
+                               x->final_norm_w, x->eps, x->hn, x->stream),
+          "final norm");
+  HIP_TRY(gdn::launch_gather_rows(x->hn, d_last, nseq, x->hidden, x->mix, x->stream),
+          "last rows");
+  GDN_TRY(gdn_qlinear_forward(x->head, x->mix, x->hidden, nseq, x->logits, x->vocab, x->stream));
+  HIP_TRY(gdn::launch_argmax(x->logits, x->vocab, nseq, x->vocab, x->d_pv, x->d_pi, x->d_next,
+                             x->stream),
+          "argmax");
+  HIP_TRY(hipMemcpyAsync(x->p_first, x->d_next, sizeof(int32_t) * nseq, hipMemcpyDeviceToHost,
+                         x->stream),
+          "token copy");
+  x->logits_rows = nseq;
   HIP_TRY(hipStreamSynchronize(x->stream), "gdn_exec_prefill sync");
-  *first_token = (uint32_t)x->p_first[0];
+  for (int i = 0; i < nseq; ++i) first_tokens[i] = (uint32_t)x->p_first[i];
   return GDN_OK;
+}
+
+gdn_status gdn_exec_prefill(gdn_exec* x, uint64_t seq_id, const int32_t* prompt, int32_t len,
+                            uint32_t* first_token) {
+  return gdn_exec_prefill_batch(x, 1, &seq_id, prompt, &len, first_token);
 }
 
 gdn_status gdn_exec_submit_batch(gdn_exec* x, const uint64_t* seq_ids, const uint32_t* tokens,

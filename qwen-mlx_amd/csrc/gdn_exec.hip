@@ -167,6 +167,24 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restric
   if (threadIdx.x == 0) out[r] = bi == INT_MAX ? 0 : bi;
 }
 
+// dst[i, :] = src[idx[i], :] (the last row of each packed prompt). grid n,
+// block 256.
+__global__ __launch_bounds__(kRowThreads) void gather_rows_kernel(const uint16_t* __restrict__ src,
+                                                                  const int32_t* __restrict__ idx,
+                                                                  int hidden,
+                                                                  uint16_t* __restrict__ dst) {
+  const uint4* s = reinterpret_cast<const uint4*>(src + (size_t)idx[blockIdx.x] * hidden);
+  uint4* d = reinterpret_cast<uint4*>(dst + (size_t)blockIdx.x * hidden);
+  for (int c = threadIdx.x; c < hidden / 8; c += kRowThreads) d[c] = s[c];
+}
+
+hipError_t launch_gather_rows(const uint16_t* src, const int32_t* idx, int n, int hidden,
+                              uint16_t* dst, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(gather_rows_kernel, dim3(n), dim3(kRowThreads), 0, s, src, idx, hidden, dst);
+  return hipGetLastError();
+}
+
 hipError_t launch_embed(const uint16_t* table, const int32_t* tok, int n, int vocab, int hidden,
                         uint16_t* h, hipStream_t s) {
   if (n <= 0) return hipSuccess;

@@ -64,6 +64,7 @@ SIGNATURES = {
     "gdn_exec_destroy": ([_VP], ctypes.c_int),
     "gdn_exec_prefill": ([_VP, ctypes.c_uint64, _VP, _I32, ctypes.POINTER(ctypes.c_uint32)],
                          ctypes.c_int),
+    "gdn_exec_prefill_batch": ([_VP, _I32, _VP, _VP, _VP, _VP], ctypes.c_int),
     "gdn_exec_decode_batch": ([_VP, _VP, _VP, _I32, _VP], ctypes.c_int),
     "gdn_exec_submit_batch": ([_VP, _VP, _VP, _I32], ctypes.c_int),
     "gdn_exec_collect_batch": ([_VP, _VP, _I32], ctypes.c_int),
@@ -416,6 +417,19 @@ class Executor:
         t = ctypes.c_uint32()
         _check(self.lib.gdn_exec_prefill(self.handle, seq_id, p, len(prompt), ctypes.byref(t)))
         return t.value
+
+    def prefill_batch(self, seq_ids, prompts) -> list:
+        """Prefill several sequences in one pass; prompts: one token list each."""
+        n = len(seq_ids)
+        if len(prompts) != n:
+            raise ValueError("one prompt per sequence")
+        flat = [int(t) for p in prompts for t in p]
+        ids = (ctypes.c_uint64 * max(n, 1))(*[int(s) for s in seq_ids])
+        toks = (_I32 * max(len(flat), 1))(*flat)
+        lens = (_I32 * max(n, 1))(*[len(p) for p in prompts])
+        out = (ctypes.c_uint32 * max(n, 1))()
+        _check(self.lib.gdn_exec_prefill_batch(self.handle, n, ids, toks, lens, out))
+        return list(out[:n])
 
     @staticmethod
     def _batch(seq_ids, tokens):

@@ -330,3 +330,60 @@ def test_executor_errors_and_slots(weights):
     ex.close()
     assert pool.slots_in_use() == 0
     assert pool.check() == 0
+
+
+def test_executor_batched_prefill(weights):
+    """gdn_exec_prefill_batch against separate prefills on a twin executor:
+    bit-identical while the packed rows stay within the decode-sized projection
+    path (64 rows), within the projections' rounding beyond it; then decode
+    steps from the handed-off states. A batch that runs out of slots admits
+    none of its new sequences."""
+    import torch
+
+    import gdn_amd
+    say("gdn_exec", "batched prefill vs separate prefills")
+    rng = np.random.default_rng(1203)
+
+    def logits_rows(ex, n):
+        return ex.logits()[:n].view(torch.bfloat16).float().cpu().numpy()
+
+    for lens, exact in (([3, 20, 41], True), ([5, 40, 100, 1], False)):
+        prompts = [[int(t) for t in rng.integers(0, VOCAB, L)] for L in lens]
+        ids = [300 + i for i in range(len(lens))]
+        _, ea = weights.executor(8, max_batch=4, max_prompt=160)
+        _, eb = weights.executor(8, max_batch=4, max_prompt=160)
+        ta = ea.prefill_batch(ids, prompts)
+        la = logits_rows(ea, len(lens))
+        for i, (sid, p) in enumerate(zip(ids, prompts)):
+            tb = eb.prefill(sid, p)
+            lb = logits_rows(eb, 1)[0]
+            if exact:
+                assert tb == ta[i] and np.array_equal(la[i], lb), (lens, i)
+            else:
+                assert rel_l2(la[i], lb) <= 1e-2, (lens, i)
+            assert int(np.argmax(la[i])) == ta[i]
+        cur = ta
+        for step in range(3):
+            na = ea.decode_batch(ids, cur)
+            ga = logits_rows(ea, len(lens))
+            nb = eb.decode_batch(ids, cur)
+            gb = logits_rows(eb, len(lens))
+            if exact:
+                assert na == nb and np.array_equal(ga, gb), (lens, step)
+            else:
+                assert max(rel_l2(ga[i], gb[i]) for i in range(len(lens))) <= 1e-2, (lens, step)
+            cur = na
+        ea.close()
+        eb.close()
+    # out of slots: 3-slot pool, one sequence admitted, a batch of three new ones fails
+    pool, ex = weights.executor(3, max_batch=4)
+    ex.prefill(1, [1, 2])
+    with pytest.raises(gdn_amd.GdnError):
+        ex.prefill_batch([2, 3, 4], [[1], [2], [3]])
+    assert pool.slots_in_use() == 1
+    with pytest.raises(gdn_amd.GdnError):  # a sequence twice in one batch
+        ex.prefill_batch([2, 2], [[1], [2]])
+    t = ex.prefill_batch([1, 2], [[1, 2], [7]])  # a known sequence starts over, one new
+    assert t[0] == ex.prefill(1, [1, 2]) and pool.slots_in_use() == 2
+    ex.close()
+    assert pool.slots_in_use() == 0
