@@ -415,6 +415,79 @@ gdn_status gdn_exec_seq_slot(const gdn_exec* exec, uint64_t seq_id, int32_t* slo
 gdn_status gdn_exec_logits(const gdn_exec* exec, const uint16_t** logits, int32_t* rows,
                            int32_t* vocab);
 
+/* ------------------------------------------------------------------------
+ * Attention layers: paged KV cache and the attention step
+ * (Qwen35Attention::forward_with_cache, qwen3_5.rs:377-455).
+ *
+ * The reference grows one [1, Hkv, len, 256] key and value array per
+ * sequence and layer by concatenation (qwen3_5.rs:419-424) and batches them
+ * by zero-padding to the longest (mlx_executor.rs:57-88); its decode
+ * attention then has no mask and its RoPE one offset for the whole batch
+ * (qwen3_5.rs:410,443-447), so with B > 1 shorter sequences attend to padding
+ * at wrong positions. Here the cache is pages of 64 tokens (a page id covers
+ * the same positions in every layer), each sequence slot has a page table,
+ * and every token carries its own position: keys are masked at the
+ * sequence's length and RoPE uses the token's position.
+ *
+ * A step: gdn_kv_step plans the tokens appended for n sequences (they are
+ * packed in that order, ntok[i] rows each, in every tensor below), then each
+ * attention layer calls gdn_attn_forward on those rows, on the same stream.
+ * Per token: rms-norm of q and k with their weights, rotate-half RoPE over the
+ * first rotary_dim dimensions at the token's position (base rope_theta), K/V
+ * appended to the cache, causal attention over the sequence's cached keys
+ * (scale 1/sqrt(256)), out = attn * sigmoid(gate) per head. Head dim 256;
+ * num_q_heads / num_kv_heads = 4 or 8.
+ * ------------------------------------------------------------------------ */
+typedef struct gdn_kv gdn_kv;
+
+typedef struct gdn_kv_desc {
+  int32_t num_layers;          /* attention layers                               */
+  int32_t num_slots;           /* sequences the cache can hold                   */
+  int32_t num_pages;           /* 64-token pages shared by all slots             */
+  int32_t max_pages_per_slot;  /* longest context / 64                           */
+  int32_t num_q_heads;         /* num_attention_heads                            */
+  int32_t num_kv_heads;        /* num_key_value_heads                            */
+  int32_t head_dim;            /* must be 256                                    */
+  int32_t max_step_tokens;     /* most tokens one step appends (all sequences)   */
+  int32_t device;
+} gdn_kv_desc;
+
+/* Per layer num_pages x 128 KiB of bf16 K/V (at 2 kv heads), a page table,
+ * and staging for max_step_tokens tokens. */
+gdn_status gdn_kv_create(const gdn_kv_desc* desc, gdn_kv** out);
+gdn_status gdn_kv_destroy(gdn_kv* kv);
+
+/* A sequence leaves (or starts over): its pages go back to the free list. */
+gdn_status gdn_kv_release(gdn_kv* kv, int32_t slot);
+gdn_status gdn_kv_length(const gdn_kv* kv, int32_t slot, int64_t* len);
+gdn_status gdn_kv_free_pages(const gdn_kv* kv, int32_t* count);
+
+/* Plan one step: sequence slots[i] (HOST array, distinct) appends ntok[i] >= 1
+ * tokens at positions len .. len + ntok[i] - 1, taking pages from the free
+ * list; the per-token metadata is copied to the device on `stream`. Fails
+ * (changing nothing) when pages, max_pages_per_slot or max_step_tokens do not
+ * suffice. A step with one token per sequence is a decode step, a prompt is
+ * one sequence's ntok tokens. */
+gdn_status gdn_kv_step(gdn_kv* kv, int32_t n, const int32_t* slots, const int32_t* ntok,
+                       void* stream);
+
+/* One attention layer on the planned step's T packed tokens: q_full [T,
+ * q_stride] (per query head 256 query then 256 gate values, the q_proj output
+ * of qwen3_5.rs:385-389), k, v [T, stride] (Hkv x 256 each), q_norm_w /
+ * k_norm_w [256] bf16; out [T, out_stride] (Hq x 256 gated rows, the o_proj
+ * input). */
+gdn_status gdn_attn_forward(gdn_kv* kv, int32_t layer, const uint16_t* q_full, int64_t q_stride,
+                            const uint16_t* k, int64_t k_stride, const uint16_t* v,
+                            int64_t v_stride, const uint16_t* q_norm_w, const uint16_t* k_norm_w,
+                            float norm_eps, float rope_theta, int32_t rotary_dim, uint16_t* out,
+                            int64_t out_stride, void* stream);
+
+/* Copy a slot's cached keys and values of one layer (rows after norm and
+ * RoPE, as attention reads them) into k_out / v_out [Hkv, len, 256] bf16 (either
+ * may be NULL). For export and inspection. */
+gdn_status gdn_kv_read(gdn_kv* kv, int32_t layer, int32_t slot, uint16_t* k_out, uint16_t* v_out,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

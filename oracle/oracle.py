@@ -325,3 +325,86 @@ class BaselineStep:
             vp(self.mixed.ctypes.data), vp(self.ab.ctypes.data), vp(self.A_log.ctypes.data),
             vp(self.dt_bias.ctypes.data), vp(self.conv_w.ctypes.data), vp(self.y.ctypes.data),
             _c_int(self.Hk), _c_int(self.Hv), _c_int(self.Dk), _c_int(self.Dv), _c_int(self.K))
+
+
+# ------------------------------------------------- attention layers -----
+# Qwen35Attention::forward_with_cache (qwen3_5.rs:377-455) for one sequence,
+# restated in float64 with the bf16 roundings of its MLX ops: fast::rms_norm
+# (bf16(w * bf16(x * r))), fast::rope (rotate-half form over the first
+# rotary_dim dimensions, traditional = false, result rounded to bf16),
+# scaled_dot_product_attention (one rounding of the output), sigmoid gate
+# (bf16) and the gated product (bf16).
+
+def f64_to_bf16_array(x) -> np.ndarray:
+    """Correctly rounded (nearest even) bf16 bits of float64 values, in one
+    rounding step (no intermediate float32)."""
+    x = np.asarray(x, dtype=np.float64)
+    m, e = np.frexp(x)                      # x = m 2^e, 0.5 <= |m| < 1
+    y = np.ldexp(np.rint(np.ldexp(m, 8)), e - 8)  # 8 significant bits, ties to even
+    with np.errstate(over="ignore"):
+        return f32_to_bf16(y.astype(np.float32))  # exact: y has at most 8 bits
+
+
+def rms_norm_w(x, w, eps: float):
+    """fast::rms_norm(x, w, eps) over the last axis (qwen3_5.rs:399-407): x bf16
+    [..., d], w bf16 [d] -> bf16 bf16(w * bf16(x * (mean(x^2) + eps)^-1/2))."""
+    xf = bf16_to_f32(x).astype(np.float64)
+    wf = bf16_to_f32(w).astype(np.float64)
+    rn = 1.0 / np.sqrt(np.mean(xf * xf, axis=-1, keepdims=True) + eps)
+    return f64_to_bf16_array(wf * bf16_to_f32(f64_to_bf16_array(xf * rn)).astype(np.float64))
+
+
+def rope_half_f64(x, pos, rot_dim: int, theta: float) -> np.ndarray:
+    """fast::rope(x, rot_dim, traditional=false, base=theta, scale=1, offset)
+    (qwen3_5.rs:411-417) in float64, before rounding: dimension i < rot_dim/2
+    pairs with i + rot_dim/2 and turns by pos * theta^(-2i/rot_dim); the rest
+    pass through. x bf16 [..., hd]; pos broadcasts against x[..., 0]."""
+    xf = bf16_to_f32(x).astype(np.float64)
+    out = xf.copy()
+    h = rot_dim // 2
+    if h == 0:
+        return out
+    inv = theta ** (-2.0 * np.arange(h) / rot_dim)
+    ang = np.asarray(pos, np.float64)[..., None] * inv
+    c, s = np.cos(ang), np.sin(ang)
+    x1, x2 = xf[..., :h], xf[..., h:rot_dim]
+    out[..., :h] = x1 * c - x2 * s
+    out[..., h:rot_dim] = x1 * s + x2 * c
+    return out
+
+
+def attention_step(q_full, k, v, q_norm_w, k_norm_w, eps: float, theta: float, rot_dim: int,
+                   cache_k, cache_v, Hq: int, Hkv: int):
+    """One sequence's S new tokens through one attention layer: q_full bf16 [S,
+    Hq * 512] (per head 256 query then 256 gate values), k, v bf16 [S, Hkv *
+    256]; cache_k, cache_v bf16 [Hkv, L0, 256] (keys after norm and RoPE). The
+    new tokens sit at positions L0 .. L0 + S - 1 and attend causally.
+    Returns (out bf16 [S, Hq * 256], new cache_k, new cache_v)."""
+    hd = 256
+    G = Hq // Hkv
+    S = q_full.shape[0]
+    L0 = cache_k.shape[1]
+    qf = np.asarray(q_full, np.uint16).reshape(S, Hq, 2, hd)
+    pos = L0 + np.arange(S)
+    qn = rms_norm_w(qf[:, :, 0, :], q_norm_w, eps)                            # [S, Hq, hd]
+    qr = bf16_to_f32(f64_to_bf16_array(rope_half_f64(qn, pos[:, None], rot_dim, theta)))
+    kn = rms_norm_w(np.asarray(k, np.uint16).reshape(S, Hkv, hd), k_norm_w, eps)
+    kr = f64_to_bf16_array(rope_half_f64(kn, pos[:, None], rot_dim, theta))  # [S, Hkv, hd]
+    ck = np.concatenate([np.asarray(cache_k, np.uint16), kr.transpose(1, 0, 2)], axis=1)
+    cv = np.concatenate([np.asarray(cache_v, np.uint16),
+                         np.asarray(v, np.uint16).reshape(S, Hkv, hd).transpose(1, 0, 2)], axis=1)
+    kf = bf16_to_f32(ck).astype(np.float64)
+    vf = bf16_to_f32(cv).astype(np.float64)
+    gate = bf16_to_f32(qf[:, :, 1, :]).astype(np.float64)
+    sg = bf16_to_f32(f64_to_bf16_array(1.0 / (1.0 + np.exp(-gate))))
+    out = np.empty((S, Hq, hd), np.uint16)
+    for i in range(S):
+        n = L0 + i + 1
+        for h in range(Hq):
+            j = h // G
+            sc = kf[j, :n] @ qr[i, h].astype(np.float64) / np.sqrt(hd)
+            p = np.exp(sc - sc.max())
+            o = (p @ vf[j, :n]) / p.sum()
+            ob = bf16_to_f32(f64_to_bf16_array(o)).astype(np.float64)
+            out[i, h] = f64_to_bf16_array(ob * sg[i, h])
+    return out.reshape(S, Hq * hd), ck, cv

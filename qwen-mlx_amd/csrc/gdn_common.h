@@ -231,6 +231,30 @@ hipError_t launch_validate(const int32_t* slot_ids, int n, int num_slots, uint32
 size_t prefill_workspace_bytes(int R, int Hk, int total_tokens);
 hipError_t launch_prefill(const PrefillArgs& a);
 
+// Attention step on the paged KV cache (gdn_attn.hip).
+struct AttnArgs {
+  int T, Hq, Hkv, nsplit, max_pages, rot_dim;
+  float eps, log2_base;
+  const uint16_t* q_full;  // [T, qs]: per query head 256 query then 256 gate values
+  int64_t qs;
+  const uint16_t* k;       // [T, ks]: Hkv x 256
+  int64_t ks;
+  const uint16_t* v;       // [T, vs]
+  int64_t vs;
+  const uint16_t* q_norm_w;
+  const uint16_t* k_norm_w;
+  const int32_t* meta;     // [3][T]: slot, position, page of each token
+  int32_t* ptab;           // [num_slots][max_pages] page table
+  uint16_t* pages;         // this layer's pages [num_pages][2][Hkv][64][256]
+  uint16_t* out;           // [T, os]: Hq x 256 gated attention rows
+  int64_t os;
+  void* workspace;         // attn_workspace_bytes(T, Hq, Hkv, nsplit)
+  hipStream_t stream;
+};
+int attn_splits(int max_keys);
+size_t attn_workspace_bytes(int T, int Hq, int Hkv, int nsplit);
+hipError_t launch_attn(const AttnArgs& a);
+
 // Sets the calling thread's gdn_last_error() message and returns code.
 gdn_status set_error(gdn_status code, const char* msg);
 

@@ -74,6 +74,16 @@ SIGNATURES = {
     "gdn_exec_seq_slot": ([_VP, ctypes.c_uint64, ctypes.POINTER(_I32)], ctypes.c_int),
     "gdn_exec_logits": ([_VP, ctypes.POINTER(_VP), ctypes.POINTER(_I32), ctypes.POINTER(_I32)],
                         ctypes.c_int),
+    "gdn_kv_create": ([_VP, ctypes.POINTER(_VP)], ctypes.c_int),
+    "gdn_kv_destroy": ([_VP], ctypes.c_int),
+    "gdn_kv_release": ([_VP, _I32], ctypes.c_int),
+    "gdn_kv_length": ([_VP, _I32, ctypes.POINTER(ctypes.c_int64)], ctypes.c_int),
+    "gdn_kv_free_pages": ([_VP, ctypes.POINTER(_I32)], ctypes.c_int),
+    "gdn_kv_step": ([_VP, _I32, _VP, _VP, _VP], ctypes.c_int),
+    "gdn_attn_forward": ([_VP, _I32, _VP, ctypes.c_int64, _VP, ctypes.c_int64, _VP,
+                          ctypes.c_int64, _VP, _VP, ctypes.c_float, ctypes.c_float, _I32, _VP,
+                          ctypes.c_int64, _VP], ctypes.c_int),
+    "gdn_kv_read": ([_VP, _I32, _I32, _VP, _VP, _VP], ctypes.c_int),
     "gdn_layer_create": ([_VP, ctypes.POINTER(_VP)], ctypes.c_int),
     "gdn_layer_destroy": ([_VP], ctypes.c_int),
     "gdn_pool_reserve": ([_VP, _I32, _VP], ctypes.c_int),
@@ -94,6 +104,12 @@ class LayerDesc(ctypes.Structure):
     _fields_ = [("pool", _VP), ("layer", _I32), ("in_proj", _VP), ("out_proj", _VP),
                 ("A_log", _VP), ("dt_bias", _VP), ("conv_w", _VP), ("norm_w", _VP),
                 ("norm_eps", ctypes.c_float)]
+
+
+class KVDesc(ctypes.Structure):
+    _fields_ = [("num_layers", _I32), ("num_slots", _I32), ("num_pages", _I32),
+                ("max_pages_per_slot", _I32), ("num_q_heads", _I32), ("num_kv_heads", _I32),
+                ("head_dim", _I32), ("max_step_tokens", _I32), ("device", _I32)]
 
 
 class ExecDesc(ctypes.Structure):
@@ -382,6 +398,75 @@ class Layer:
     def close(self):
         if getattr(self, "handle", None):
             _check(self.lib.gdn_layer_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class KVCache:
+    """Paged KV cache of the attention layers (64-token pages) and the
+    attention step: step(slots, ntok) plans the packed tokens, then
+    forward(layer, ...) runs one attention layer on them."""
+
+    def __init__(self, num_layers: int, num_slots: int, num_pages: int, max_pages_per_slot: int,
+                 num_q_heads: int = 16, num_kv_heads: int = 2, max_step_tokens: int = 4096,
+                 device: int = 0):
+        self.lib = load()
+        d = KVDesc(num_layers, num_slots, num_pages, max_pages_per_slot, num_q_heads,
+                   num_kv_heads, 256, max_step_tokens, device)
+        h = _VP()
+        _check(self.lib.gdn_kv_create(ctypes.byref(d), ctypes.byref(h)))
+        self.handle = h
+        self.Hq, self.Hkv, self.device = num_q_heads, num_kv_heads, device
+
+    def step(self, slots, ntok, stream=None):
+        n = len(slots)
+        s = (_I32 * n)(*[int(x) for x in slots])
+        t = (_I32 * n)(*[int(x) for x in ntok])
+        _check(self.lib.gdn_kv_step(self.handle, n, s, t, _stream(stream)))
+
+    def forward(self, layer, q_full, k, v, q_norm_w, k_norm_w, eps, rope_theta, rotary_dim, out,
+                stream=None):
+        qp, qs = _rows(q_full)
+        kp, ks = _rows(k)
+        vp, vs = _rows(v)
+        op, os_ = _rows(out)
+        _check(self.lib.gdn_attn_forward(self.handle, layer, qp, qs, kp, ks, vp, vs,
+                                         _ptr(q_norm_w), _ptr(k_norm_w), float(eps),
+                                         float(rope_theta), int(rotary_dim), op, os_,
+                                         _stream(stream)))
+
+    def release(self, slot: int):
+        _check(self.lib.gdn_kv_release(self.handle, slot))
+
+    def length(self, slot: int) -> int:
+        n = ctypes.c_int64()
+        _check(self.lib.gdn_kv_length(self.handle, slot, ctypes.byref(n)))
+        return n.value
+
+    def free_pages(self) -> int:
+        c = _I32()
+        _check(self.lib.gdn_kv_free_pages(self.handle, ctypes.byref(c)))
+        return c.value
+
+    def read(self, layer: int, slot: int, stream=None):
+        """(k, v) int16 [Hkv, len, 256] device copies of a slot's cache."""
+        import torch
+        L = self.length(slot)
+        k = torch.empty((self.Hkv, L, 256), dtype=torch.int16, device=f"cuda:{self.device}")
+        v = torch.empty_like(k)
+        if L:
+            _check(self.lib.gdn_kv_read(self.handle, layer, slot, _ptr(k), _ptr(v),
+                                        _stream(stream)))
+        return k, v
+
+    def close(self):
+        if getattr(self, "handle", None):
+            _check(self.lib.gdn_kv_destroy(self.handle))
             self.handle = None
 
     def __del__(self):

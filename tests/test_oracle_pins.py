@@ -472,3 +472,128 @@ def test_qmatmul_w4_ties_round_once():
     y, ye, _ = O.qmatmul_w4(x, words, s, b)
     assert ye[0, 0] == 1.0 + 2.0**-8 and int(y[0, 0]) == 0x3F80
     assert ye[1, 0] == 1.0 + 2.0**-8 + 2.0**-40 and int(y[1, 0]) == 0x3F81
+
+
+# ------------------------------------------------------ attention layers --
+
+def test_f64_to_bf16_array_is_correctly_rounded():
+    """The one-step vectorised rounding equals the C oracle's scalar rounding,
+    including exact ties and values one f64 ulp either side of a tie."""
+    rng = np.random.default_rng(70)
+    base = O.bf16_to_f32(rng.integers(0x0080, 0x7F00, 4000).astype(np.uint16)).astype(np.float64)
+    half = np.ldexp(1.0, np.frexp(base)[1] - 9)  # half a bf16 ulp
+    xs = np.concatenate([base + half, base - half, np.nextafter(base + half, np.inf),
+                         np.nextafter(base + half, 0), -(base + half),
+                         rng.standard_normal(2000) * np.exp(rng.uniform(-30, 30, 2000))])
+    got = O.f64_to_bf16_array(xs)
+    want = np.array([O.f64_to_bf16(v) for v in xs], np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_rope_half_closed_forms():
+    """Rotate-half RoPE: position 0 is the identity; a unit vector in dimension
+    i (i < rot/2) turns into (cos a, sin a) on dimensions (i, i + rot/2) with
+    a = pos * theta^(-2i/rot), its partner into (-sin a, cos a); dimensions
+    past rot_dim pass through; scores depend on the position difference only."""
+    hd, rot, theta = 256, 64, 1.0e7
+    rng = np.random.default_rng(71)
+    x = O.f32_to_bf16(rng.standard_normal(hd).astype(np.float32))
+    assert np.array_equal(O.rope_half_f64(x, 0, rot, theta), O.bf16_to_f32(x).astype(np.float64))
+    h = rot // 2
+    for i in (0, 5, h - 1):
+        for p in (1, 37, 1000):
+            a = p * theta ** (-2.0 * i / rot)
+            e = np.zeros(hd, np.float32)
+            e[i] = 1.0
+            r = O.rope_half_f64(O.f32_to_bf16(e), p, rot, theta)
+            want = np.zeros(hd)
+            want[i], want[i + h] = np.cos(a), np.sin(a)
+            assert np.allclose(r, want, atol=1e-12), (i, p)
+            e2 = np.zeros(hd, np.float32)
+            e2[i + h] = 1.0
+            r2 = O.rope_half_f64(O.f32_to_bf16(e2), p, rot, theta)
+            want2 = np.zeros(hd)
+            want2[i], want2[i + h] = -np.sin(a), np.cos(a)
+            assert np.allclose(r2, want2, atol=1e-12), (i, p)
+    r = O.rope_half_f64(x, 123, rot, theta)
+    assert np.array_equal(r[rot:], O.bf16_to_f32(x[rot:]).astype(np.float64))
+    y = O.f32_to_bf16(rng.standard_normal(hd).astype(np.float32))
+    d1 = O.rope_half_f64(x, 17, rot, theta) @ O.rope_half_f64(y, 9, rot, theta)
+    d2 = O.rope_half_f64(x, 517, rot, theta) @ O.rope_half_f64(y, 509, rot, theta)
+    assert abs(d1 - d2) <= 1e-9 * (1 + abs(d1))
+    assert np.array_equal(O.rope_half_f64(x, 99, 0, theta), O.bf16_to_f32(x).astype(np.float64))
+
+
+def test_rms_norm_w_agrees_with_the_pinned_scalar_norm():
+    """With a constant weight the vector-weight norm equals the pinned
+    orc_rms_norm bit for bit; a constant row of 2 with eps 0 normalises to w."""
+    rng = np.random.default_rng(72)
+    x = O.f32_to_bf16(rng.standard_normal((40, 256)).astype(np.float32))
+    for w in (1.0, 0.08837890625, 0.5):
+        wv = O.f32_to_bf16(np.full(256, w, np.float32))
+        assert np.array_equal(O.rms_norm_w(x, wv, 1e-6), O.rms_norm(x, w, 1e-6))
+    w = O.f32_to_bf16(rng.standard_normal(256).astype(np.float32))
+    two = O.f32_to_bf16(np.full((1, 256), 2.0, np.float32))
+    assert np.array_equal(O.rms_norm_w(two, w, 0.0)[0], w)
+
+
+def _attn_inputs(rng, S, Hq, Hkv, hd=256):
+    q = O.f32_to_bf16(rng.standard_normal((S, Hq * 2 * hd)).astype(np.float32))
+    k = O.f32_to_bf16(rng.standard_normal((S, Hkv * hd)).astype(np.float32))
+    v = O.f32_to_bf16(rng.standard_normal((S, Hkv * hd)).astype(np.float32))
+    qw = O.f32_to_bf16((1 + 0.1 * rng.standard_normal(hd)).astype(np.float32))
+    kw = O.f32_to_bf16((1 + 0.1 * rng.standard_normal(hd)).astype(np.float32))
+    return q, k, v, qw, kw
+
+
+def test_attention_step_closed_forms_and_causality():
+    """One token with an empty cache attends to itself only: out = bf16(v *
+    bf16(sigmoid(gate))) exactly. Identical keys give the mean of the values.
+    A prompt processed at once equals the same tokens processed one by one
+    against the growing cache (positions and causal mask line up), and later
+    tokens cannot change earlier outputs. Query head h reads kv head h // G."""
+    rng = np.random.default_rng(73)
+    Hq, Hkv, hd, eps, theta, rot = 8, 2, 256, 1e-6, 1.0e7, 64
+    q, k, v, qw, kw = _attn_inputs(rng, 1, Hq, Hkv)
+    empty = np.zeros((Hkv, 0, hd), np.uint16)
+    out, ck, cv = O.attention_step(q, k, v, qw, kw, eps, theta, rot, empty, empty, Hq, Hkv)
+    gate = O.bf16_to_f32(q.reshape(Hq, 2, hd)[:, 1]).astype(np.float64)
+    sg = O.bf16_to_f32(O.f64_to_bf16_array(1 / (1 + np.exp(-gate))))
+    vf = O.bf16_to_f32(v.reshape(Hkv, hd)).astype(np.float64)
+    want = O.f64_to_bf16_array(np.stack([vf[h // (Hq // Hkv)] for h in range(Hq)]) * sg)
+    assert np.array_equal(out.reshape(Hq, hd), want)
+    assert ck.shape == (Hkv, 1, hd) and np.array_equal(cv[:, 0], v.reshape(Hkv, hd))
+    # the first token sits at position 0, where RoPE is the identity: its
+    # cached key is the normed key; the next one is rotated by position 1
+    assert np.array_equal(ck[:, 0], O.rms_norm_w(k.reshape(Hkv, hd), kw, eps))
+    q2, k2_, v2, _, _ = _attn_inputs(rng, 1, Hq, Hkv)
+    _, ck2, _ = O.attention_step(q2, k2_, v2, qw, kw, eps, theta, rot, ck, cv, Hq, Hkv)
+    kn2 = O.rms_norm_w(k2_.reshape(Hkv, hd), kw, eps)
+    assert np.array_equal(ck2[:, 1], O.f64_to_bf16_array(O.rope_half_f64(kn2, 1, rot, theta)))
+    # identical keys: uniform weights, the output is the mean of the values
+    S = 6
+    q, k, v, qw, kw = _attn_inputs(rng, S, Hq, Hkv)
+    same = O.f32_to_bf16(np.zeros((Hkv, 3, hd), np.float32))
+    vals = O.f32_to_bf16(rng.standard_normal((Hkv, 3, hd)).astype(np.float32))
+    kz = O.f32_to_bf16(np.zeros((1, Hkv * hd), np.float32))
+    o1, _, _ = O.attention_step(q[:1], kz, v[:1], qw, kw, eps, theta, rot, same, vals, Hq, Hkv)
+    allv = np.concatenate([O.bf16_to_f32(vals).astype(np.float64),
+                           O.bf16_to_f32(v[:1].reshape(Hkv, 1, hd)).astype(np.float64)], 1)
+    gate = O.bf16_to_f32(q[:1].reshape(Hq, 2, hd)[:, 1]).astype(np.float64)
+    sg = O.bf16_to_f32(O.f64_to_bf16_array(1 / (1 + np.exp(-gate))))
+    mean = O.bf16_to_f32(O.f64_to_bf16_array(allv.mean(1))).astype(np.float64)
+    want = O.f64_to_bf16_array(np.stack([mean[h // 4] for h in range(Hq)]) * sg)
+    assert np.array_equal(o1.reshape(Hq, hd), want)
+    # prompt at once == token by token; later tokens do not reach earlier outputs
+    ca, va = empty, empty
+    outs = []
+    for i in range(S):
+        o, ca, va = O.attention_step(q[i:i + 1], k[i:i + 1], v[i:i + 1], qw, kw, eps, theta, rot,
+                                     ca, va, Hq, Hkv)
+        outs.append(o)
+    ob, cb, vb = O.attention_step(q, k, v, qw, kw, eps, theta, rot, empty, empty, Hq, Hkv)
+    assert np.array_equal(np.concatenate(outs), ob) and np.array_equal(ca, cb)
+    k2 = k.copy()
+    k2[-1] ^= 0x0100
+    ob2, _, _ = O.attention_step(q, k2, v, qw, kw, eps, theta, rot, empty, empty, Hq, Hkv)
+    assert np.array_equal(ob2[:-1], ob[:-1]) and not np.array_equal(ob2[-1], ob[-1])
