@@ -78,6 +78,12 @@ def parse_args(argv=None):
                          "embedding, per layer norm + in_proj + fused decode + out_proj, "
                          "final norm, lm_head, greedy pick")
     ap.add_argument("--vocab", type=int, default=248320)
+    ap.add_argument("--attn", action="store_true",
+                    help="time the attention layers' decode step on the paged KV cache "
+                         "(gdn_kv_step + gdn_attn_forward) instead")
+    ap.add_argument("--attn-layers", type=int, default=10)
+    ap.add_argument("--context", type=int, default=4096,
+                    help="mean cached tokens per sequence (ragged, uniform in [C/2, 3C/2])")
     ap.add_argument("--seed", type=int, default=0)
     return ap.parse_args(argv)
 
@@ -416,6 +422,153 @@ def exec_bench(args):
     return 0
 
 
+# Qwen3.5-35B-A3B's full-attention layers (every fourth of 40): 16 query
+# heads (each 256 query + 256 gate outputs of q_proj), 2 kv heads, head dim
+# 256, RoPE over the first 64 dimensions with base 1e7.
+ATT_HQ, ATT_HKV, ATT_HD, ATT_ROT, ATT_THETA = 16, 2, 256, 64, 1.0e7
+ATT_PAGE = 64
+
+
+def attn_bench(args):
+    """The attention layers' decode step: B sequences with ragged cached
+    contexts (uniform in [C/2, 3C/2] tokens, written by chunked prefill steps
+    through the same path), each appending one token per step in every layer:
+    one gdn_kv_step, then one gdn_attn_forward per layer (q/k norm + RoPE and
+    the K/V append, split softmax over the pages, merge + output gate). Inputs
+    are synthetic bf16 projection outputs resident in HBM. Prints one JSON
+    line; the dominant traffic is every cached K and V byte read once per
+    layer."""
+    import numpy as np
+    import torch
+
+    import gdn_amd
+    dev = torch.device("cuda:0")
+    L, B, C = args.attn_layers, args.batch, args.context
+    Hq, Hkv, hd = ATT_HQ, ATT_HKV, ATT_HD
+    rng = np.random.default_rng(args.seed)
+    lens = rng.integers(C // 2, C + C // 2 + 1, B)
+    grow = args.warmup + args.steps + 1
+    pages = [int(-(-(n + grow) // ATT_PAGE)) for n in lens]
+    chunk = 2048
+    kv = gdn_amd.KVCache(L, B, sum(pages) + 4, max(pages), Hq, Hkv,
+                         max_step_tokens=max(chunk, B))
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    bf = torch.bfloat16
+    qn = [(1 + 0.1 * torch.randn(hd, generator=gen, device=dev)).to(bf) for _ in range(L)]
+    kn = [(1 + 0.1 * torch.randn(hd, generator=gen, device=dev)).to(bf) for _ in range(L)]
+    qbuf = torch.randn((chunk, Hq * 2 * hd), generator=gen, device=dev).to(bf)
+    kbuf = torch.randn((chunk, Hkv * hd), generator=gen, device=dev).to(bf)
+    vbuf = torch.randn((chunk, Hkv * hd), generator=gen, device=dev).to(bf)
+    obuf = torch.empty((chunk, Hq * hd), dtype=bf, device=dev)
+
+    def layers(T, events=None):
+        for l in range(L):
+            if events is not None:
+                events[l][0].record()
+            kv.forward(l, qbuf[:T], kbuf[:T], vbuf[:T], qn[l], kn[l], 1e-6, ATT_THETA, ATT_ROT,
+                       obuf[:T])
+            if events is not None:
+                events[l][1].record()
+
+    t0 = time.perf_counter()
+    for b in range(B):   # fill the caches: prompts in steps of at most `chunk` tokens
+        done = 0
+        while done < lens[b]:
+            n = int(min(chunk, lens[b] - done))
+            kv.step([b], [n])
+            layers(n)
+            done += n
+    torch.cuda.synchronize()
+    fill_s = time.perf_counter() - t0
+    ids = list(range(B))
+    ones = [1] * B
+    for _ in range(args.warmup):
+        kv.step(ids, ones)
+        layers(B)
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(L)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    keys0 = sum(kv.length(b) for b in ids)
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        kv.step(ids, ones)
+        layers(B, ev[i])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    avg_ms = sum(a.elapsed_time(b) for st in ev for a, b in st) / (args.steps * L)
+    # keys attended per layer per step, averaged over the timed steps (each
+    # sequence attends its cached keys plus the appended one)
+    keys = keys0 + B * (args.steps + 1) / 2.0
+    kv_bytes = keys * Hkv * hd * 2 * 2                       # K and V rows, bf16
+    io_bytes = B * (Hq * 2 * hd + 2 * Hkv * hd + Hq * hd) * 2  # q|gate, k, v in; out
+    achieved = (kv_bytes + io_bytes) / (avg_ms * 1e-3) / 1e9
+    out = {
+        "metric": "attention-layer decode tokens/s on the paged KV cache (B sequences, all "
+                  "attention layers)",
+        "value": round(B * args.steps / elapsed, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "dtype": "bf16 K/V, f32 softmax and accumulation",
+        "data": "synthetic",
+        "config": {"workload": f"{L} attention layers (16 q heads, 2 kv heads, head dim 256), "
+                               f"B={B} ragged contexts uniform in [{C // 2}, {C + C // 2}] "
+                               f"tokens, 64-token pages",
+                   "layers": L, "batch": B, "mean_context": round(keys0 / B, 1),
+                   "q_heads": Hq, "kv_heads": Hkv, "head_dim": hd},
+        "cache_fill_s": round(fill_s, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "gdn_attn_forward (attn_prep_kernel + attn_split_kernel<8> + "
+                               "attn_combine_kernel<8>)",
+                     "kernel_avg_us": round(avg_ms * 1e3, 2),
+                     "kernel_timing": "HIP events around each layer's gdn_attn_forward",
+                     "algorithmic_bytes_per_launch": int(kv_bytes + io_bytes)},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = attn_cpu_baseline(args.cpu_seconds, L, C)
+    kv.close()
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def attn_cpu_baseline(seconds: float, layers: int, context: int):
+    """The oracle's attention step (float64 numpy) decoding one sequence at
+    `context` cached tokens, one token per call, for about `seconds`;
+    reported per token through `layers` layers like the GPU figure."""
+    import numpy as np
+    from oracle import oracle as O
+    rng = np.random.default_rng(5)
+    hd = ATT_HD
+    bf = lambda a: O.f32_to_bf16(a.astype(np.float32))  # noqa: E731
+    ck = bf(rng.standard_normal((ATT_HKV, context, hd)))
+    cv = bf(rng.standard_normal((ATT_HKV, context, hd)))
+    w = bf(1 + 0.1 * rng.standard_normal(hd))
+    q = bf(rng.standard_normal((1, ATT_HQ * 2 * hd)))
+    k = bf(rng.standard_normal((1, ATT_HKV * hd)))
+    v = bf(rng.standard_normal((1, ATT_HKV * hd)))
+    n, t0 = 0, time.perf_counter()
+    while True:
+        O.attention_step(q, k, v, w, w, 1e-6, ATT_THETA, ATT_ROT, ck, cv, ATT_HQ, ATT_HKV)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 5000:
+            break
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
+    except Exception:
+        cores = 1
+    return {"value": round(n / el / layers, 3), "unit": "tokens/s", "cores": cores,
+            "kind": "port",
+            "sample": f"{n} single-token steps of one sequence at {context} cached tokens through "
+                      f"one layer ({el:.1f} s), scaled to {layers} layers, float64 oracle "
+                      f"(numpy, BLAS threads {cores}), {_cpu_model()}"}
+
+
 def qlinear_cpu_baseline(seconds: float, layers: int):
     """The oracle's quantized matmul (float64, OpenMP over outputs) on 8-row
     slices of the same layer shape, repeated for about `seconds`; reported per
@@ -587,6 +740,8 @@ def main(argv=None):
         return qlinear_bench(args)
     if args.exec:
         return exec_bench(args)
+    if args.attn:
+        return attn_bench(args)
     w = Workload(args)
     for _ in range(args.warmup):
         w.step()
