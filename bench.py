@@ -522,7 +522,7 @@ def attn_bench(args):
         "cache_fill_s": round(fill_s, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "gdn_attn_forward (attn_prep_kernel + attn_split_kernel<8> + "
+                     "kernel": "gdn_attn_forward (attn_prep_kernel + attn_block_kernel<8> + "
                                "attn_combine_kernel<8>)",
                      "kernel_avg_us": round(avg_ms * 1e3, 2),
                      "kernel_timing": "HIP events around each layer's gdn_attn_forward",

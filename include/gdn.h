@@ -436,7 +436,10 @@ gdn_status gdn_exec_logits(const gdn_exec* exec, const uint16_t** logits, int32_
  * first rotary_dim dimensions at the token's position (base rope_theta), K/V
  * appended to the cache, causal attention over the sequence's cached keys
  * (scale 1/sqrt(256)), out = attn * sigmoid(gate) per head. Head dim 256;
- * num_q_heads / num_kv_heads = 4 or 8.
+ * num_q_heads / num_kv_heads = 4 or 8. Results are deterministic for a given
+ * step; the same tokens in a step with other sequences may differ by one bf16
+ * ulp (the step's key blocks are split evenly over the workers, so a token's
+ * partial sums depend on the whole step).
  * ------------------------------------------------------------------------ */
 typedef struct gdn_kv gdn_kv;
 
@@ -450,6 +453,9 @@ typedef struct gdn_kv_desc {
   int32_t head_dim;            /* must be 256                                    */
   int32_t max_step_tokens;     /* most tokens one step appends (all sequences)   */
   int32_t device;
+  int32_t max_workers;         /* waves a step's attention is split over; 0 =
+                                  2048, the one-wave work-groups the chip keeps
+                                  resident (fewer when sharing the GPU)         */
 } gdn_kv_desc;
 
 /* Per layer num_pages x 128 KiB of bf16 K/V (at 2 kv heads), a page table,

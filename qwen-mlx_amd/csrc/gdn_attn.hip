@@ -7,27 +7,49 @@
 // whole batch (mlx_executor.rs:57-88, qwen3_5.rs:410,443-447), so with B > 1
 // a shorter sequence attends to padding and is rotated at the wrong
 // position. Here every token carries its own sequence, position and KV page,
-// keys are masked at the sequence's length, and RoPE uses the token's own
-// position.
+// keys are masked at each token's own position, and RoPE uses that position.
 //
 // Three launches per layer step (T tokens, Hq query heads, Hkv kv heads,
 // G = Hq/Hkv query heads per kv head, head dim 256, pages of 64 tokens):
 //   attn_prep_kernel    q, k rms-norm (qwen3_5.rs:399-407), partial RoPE
 //                       (:411-417), K/V rows into the token's page
-//   attn_split_kernel   per (token, kv head, 1024-key split): scores of the G
-//                       query heads against the split's keys, online softmax,
-//                       P.V (scaled_dot_product_attention, :427-446)
-//   attn_combine_kernel merge the splits, output gate sigmoid(gate) * attn
-//                       (:452-454), bf16 rows for o_proj
+//   attn_block_kernel   one wave per worker of an even split of all
+//                       (token group, kv head, 16-key block) work: scores and
+//                       P.V on MFMA, online softmax, one partial per piece
+//                       (scaled_dot_product_attention, :427-446)
+//   attn_combine_kernel merge a token's pieces, output gate sigmoid(gate) *
+//                       attn (:452-454), bf16 rows for o_proj
+//
+// Page layout. A page holds 64 positions of one layer: [2 (K, V)][Hkv][16384]
+// bf16, each 16384-element tile stored in the order the MFMA operands are
+// loaded, so that every load instruction of a wave reads 1 KiB (K) or 512 B
+// (V) of contiguous memory:
+//   K (key kk, dim d): [kk/16][d/32][(d/8)%4][kk%16][d%8]   -- A operand of
+//       v_mfma_f32_16x16x32_bf16, rows = 16 keys, 32-deep k = dims
+//   V (key kk, dim d): [kk/16][d/16][(kk/4)%4][d%16][kk%4]  -- A operand of
+//       v_mfma_f32_16x16x16_bf16, rows = 16 dims, 16-deep k = keys
 #include "gdn_common.h"
 
 namespace gdn {
 
 namespace {
 
-constexpr int kHd = 256;          // head dim = threads per work-group
-constexpr int kPage = 64;         // tokens per KV page
-constexpr int kSplitKeys = 1024;  // keys per attn_split_kernel work-group
+constexpr int kHd = 256;            // head dim = threads of the prep / combine work-groups
+constexpr int kPage = 64;           // tokens per KV page
+constexpr int kTile = kPage * kHd;  // elements of one page's K (or V) tile of one kv head
+constexpr int kPartLd = 4 + kHd;    // partial row: m, l, 2 pad, 256 outputs (f32)
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int k_off(int kk, int d) {
+  return ((((kk >> 4) * 8 + (d >> 5)) * 4 + ((d >> 3) & 3)) * 16 + (kk & 15)) * 8 + (d & 7);
+}
+__device__ __forceinline__ int v_off(int kk, int d) {
+  return ((((kk >> 4) * 16 + (d >> 4)) * 4 + ((kk >> 2) & 3)) * 16 + (d & 15)) * 4 + (kk & 3);
+}
 
 // Block-wide f32 sum over 256 threads (every thread gets the result).
 __device__ __forceinline__ float block_sum256(float v, float* red) {
@@ -39,10 +61,18 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
   return t;
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
+__device__ __forceinline__ f32x4 mfma32(uint4 a, uint4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+// 16-deep product: lane l holds row l%16, k = 4 (l/16) .. +3 of each operand
+__device__ __forceinline__ f32x4 mfma16(uint2 a, uint2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                   __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma32(uint4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
 }  // namespace
@@ -89,155 +119,218 @@ __global__ __launch_bounds__(kHd) void attn_prep_kernel(
   if (isq) {
     q_rot[((size_t)t * Hq + h) * kHd + d] = yb;
   } else {
-    const size_t row = (((size_t)page * 2 * Hkv + j) * kPage + (pos & (kPage - 1))) * kHd;
-    pages[row + d] = yb;                                                         // K
-    pages[row + (size_t)Hkv * kPage * kHd + d] = v[(size_t)t * vs + (size_t)j * kHd + d];  // V
-    if (j == 0 && d == 0 && (pos & (kPage - 1)) == 0) ptab[(size_t)slot * max_pages + pos / kPage] = page;
+    const int kk = pos & (kPage - 1);
+    const size_t tile = ((size_t)page * 2 * Hkv + j) * kTile;
+    pages[tile + k_off(kk, d)] = yb;  // K
+    pages[tile + (size_t)Hkv * kTile + v_off(kk, d)] = v[(size_t)t * vs + (size_t)j * kHd + d];
+    if (j == 0 && d == 0 && kk == 0) ptab[(size_t)slot * max_pages + pos / kPage] = page;
   }
 }
 
-// grid (T, Hkv, splits), block 256. Work-group (t, j, sp) takes keys
-// [1024 sp, min(1024 (sp + 1), pos_t + 1)) of token t's sequence for the G
-// query heads of kv head j: K and V pages staged in LDS (64 keys x 512 B
-// each; K rows padded to 528 B so that the 64 lanes reading 64 different
-// rows hit distinct banks), scores with the 64 keys on the lanes of a wave
-// (wave w: query heads w G/4 .. w G/4 + G/4 - 1), online softmax per head,
-// then P.V with thread d owning output dimension d. Writes the split's
-// running max, sum and unnormalised output (f32) to part.
+// One wave per work-group; work-group w is worker w of P. The flat list of
+// work is every (token group, kv head) segment's 16-key blocks in order
+// (segment s = group * Hkv + j); worker w takes blocks [w W / P, (w+1) W / P)
+// of the W in total, which may span several segments: each maximal run of
+// one segment's blocks is a piece and writes one partial.
+//
+// A token group is up to 16/G consecutive tokens of one sequence: the 16
+// columns of the MFMA tiles are (token, query head) pairs, column c = token
+// c / G of the group, head j G + c % G. Per 16-key block:
+//   S^T (16 keys x 16 columns) = K_blk (16 x 256) . Q^T (256 x 16): 8 MFMAs,
+//     K straight from the page, Q^T loaded once per piece;
+//   online softmax per column in the log2 domain (keys past the column's
+//     token position masked to -inf; a wave-uniform branch rescales the
+//     accumulators only when some column's running max grows);
+//   O^T (256 dims x 16 columns) += V^T_blk . P^T: three 16-deep MFMAs per
+//     16 dims, against P split into bf16 hi, mid and lo parts (together P's
+//     24 significant bits: the products are those of float32 P). The score accumulator of lane l holds keys 4 (l/16) .. +3 of
+//     column l%16: the B operand layout as it is. (The O accumulators only
+//     ever see the 16-deep opcode and the score accumulator only the 32-deep
+//     one.)
+// The next block's K and V are loaded while the current one computes. V of
+// keys past the group's last position is zeroed before use (those rows of a
+// page may hold anything).
+//
+// Schedule tables (int32, built by the host for the step):
+//   grp[NG][4]  first token, tokens, first position, sequence slot
+//   seg[NS][4]  first flat block, first partial, first worker, partials
+//   wseg[P]     segment of the worker's first block
+// Partials [pieces][16][kPartLd] f32: running max (log2 domain), sum, output.
 template <int G>
-__global__ __launch_bounds__(kHd) void attn_split_kernel(
-    const uint16_t* __restrict__ q_rot, int Hq, int Hkv, const int32_t* __restrict__ meta, int T,
+__global__ __launch_bounds__(64, 2) void attn_block_kernel(
+    const uint16_t* __restrict__ q_rot, int Hq, int Hkv, const int32_t* __restrict__ grp,
+    const int32_t* __restrict__ seg, const int32_t* __restrict__ wseg, int64_t W, int P,
     const int32_t* __restrict__ ptab, int max_pages, const uint16_t* __restrict__ pages,
-    float scale, int nsplit_max, float* __restrict__ part) {
-  static_assert(G % 4 == 0, "G/4 query heads per wave");
-  constexpr int GW = G / 4;
-  constexpr int KLD = kHd + 8;  // padded K row (bf16)
-  __shared__ __align__(16) float q[G][kHd];
-  __shared__ __align__(16) uint16_t Ks[kPage][KLD];
-  __shared__ __align__(16) uint16_t Vs[kPage][kHd];
-  __shared__ __align__(16) float p[G][kPage];
-  __shared__ float corr[G];
-  const int t = blockIdx.x, j = blockIdx.y, sp = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int slot = meta[t], pos = meta[T + t];
-  const int nkeys = pos + 1;
-  const int k0 = sp * kSplitKeys;
-  if (k0 >= nkeys) return;
-  const int k1 = min(k0 + kSplitKeys, nkeys);
+    float scale_log2, float* __restrict__ part) {
+  static_assert(16 % G == 0, "whole tokens per 16 columns");
+  __shared__ u32x4 qlds[8][64];  // this wave's Q^T operand
+  const int w = blockIdx.x, lane = threadIdx.x;
+  const int g4 = lane >> 4, c = lane & 15;
+  const int64_t fw1 = (int64_t)(w + 1) * W / P;
+  int64_t f = (int64_t)w * W / P;
+  int s = wseg[w];
+  const size_t page_stride = (size_t)2 * Hkv * kTile;
+  const size_t v_shift = (size_t)Hkv * kTile;
+  while (f < fw1) {
+    const int gi = s / Hkv, j = s - gi * Hkv;
+    const int t0 = grp[4 * gi], ntok = grp[4 * gi + 1], pos0 = grp[4 * gi + 2],
+              slot = grp[4 * gi + 3];
+    const int64_t sf0 = seg[4 * s];
+    const int nkeys = pos0 + ntok;  // the group's last position + 1
+    const int nblk = (nkeys + 15) >> 4;
+    const int kb0 = (int)(f - sf0);
+    const int kb1 = (int)min((int64_t)nblk, fw1 - sf0);
+    const int ctok = c / G;
+    const bool cvalid = ctok < ntok;
+    const int cpos = cvalid ? pos0 + ctok : -1;  // keys <= cpos are attended
+    // Q^T: lane l holds column c, dims 32 ks + 8 g4 .. +7, kept in LDS
+    {
+      const uint4* qsrc = reinterpret_cast<const uint4*>(
+          q_rot + ((size_t)(t0 + (cvalid ? ctok : 0)) * Hq + j * G + c % G) * kHd + 8 * g4);
 #pragma unroll
-  for (int g = 0; g < G; ++g) q[g][tid] = bf2f(q_rot[((size_t)t * Hq + j * G + g) * kHd + tid]);
-  float m[GW], l[GW];
-#pragma unroll
-  for (int u = 0; u < GW; ++u) {
-    m[u] = -INFINITY;
-    l[u] = 0.f;
-  }
-  float acc[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) acc[g] = 0.f;
-  const int32_t* prow = ptab + (size_t)slot * max_pages;
-  for (int kb = k0; kb < k1; kb += kPage) {
-    const int n = min(kPage, k1 - kb);
-    const size_t base = ((size_t)prow[kb / kPage] * 2 * Hkv + j) * kPage * kHd;
-    const uint4* ksrc = reinterpret_cast<const uint4*>(pages + base);
-    const uint4* vsrc = reinterpret_cast<const uint4*>(pages + base + (size_t)Hkv * kPage * kHd);
-    __syncthreads();  // the previous page's readers are done
-#pragma unroll
-    for (int r = 0; r < kPage * kHd / 8 / kHd; ++r) {  // 8 uint4 per thread per array
-      const int e = tid + kHd * r;  // row e / 32, 16-byte chunk e % 32
-      *reinterpret_cast<uint4*>(&Ks[e >> 5][8 * (e & 31)]) = ksrc[e];
-      reinterpret_cast<uint4*>(&Vs[0][0])[e] = vsrc[e];
-    }
-    __syncthreads();
-    // scores: lane = key, this wave's GW heads
-    float s[GW];
-#pragma unroll
-    for (int u = 0; u < GW; ++u) s[u] = 0.f;
-    const uint4* krow = reinterpret_cast<const uint4*>(&Ks[lane][0]);  // 528-byte rows
-#pragma unroll 4
-    for (int c = 0; c < kHd / 8; ++c) {
-      const uint4 kv = krow[c];
-      const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
-#pragma unroll
-      for (int u = 0; u < GW; ++u) {
-        const float4 qa = *reinterpret_cast<const float4*>(&q[wave * GW + u][8 * c]);
-        const float4 qb = *reinterpret_cast<const float4*>(&q[wave * GW + u][8 * c + 4]);
-        s[u] = fmaf(qa.x, bf_lo(kw[0]), s[u]);
-        s[u] = fmaf(qa.y, bf_hi(kw[0]), s[u]);
-        s[u] = fmaf(qa.z, bf_lo(kw[1]), s[u]);
-        s[u] = fmaf(qa.w, bf_hi(kw[1]), s[u]);
-        s[u] = fmaf(qb.x, bf_lo(kw[2]), s[u]);
-        s[u] = fmaf(qb.y, bf_hi(kw[2]), s[u]);
-        s[u] = fmaf(qb.z, bf_lo(kw[3]), s[u]);
-        s[u] = fmaf(qb.w, bf_hi(kw[3]), s[u]);
+      for (int ks = 0; ks < 8; ++ks) {
+        const uint4 q = cvalid ? qsrc[4 * ks] : make_uint4(0, 0, 0, 0);
+        qlds[ks][lane] = (u32x4){q.x, q.y, q.z, q.w};
       }
     }
+    // the piece's page ids, one per lane (64 pages = 4096 keys per reload)
+    const int32_t* prow = ptab + (size_t)slot * max_pages;
+    const int npages = (nblk + 3) >> 2;
+    int pbase = kb0 >> 2;
+    int pid = pbase + lane < npages ? prow[pbase + lane] : 0;
+    const uint16_t* kv_head = pages + (size_t)j * kTile;
+
+    float m = -INFINITY, lsum = 0.f;
+    f32x4 O[16];
 #pragma unroll
-    for (int u = 0; u < GW; ++u) {
-      const float sc = lane < n ? s[u] * scale : -INFINITY;
-      const float mnew = fmaxf(m[u], wave_max(sc));
-      const float pe = lane < n ? expf(sc - mnew) : 0.f;
-      const float c = expf(m[u] - mnew);  // 0 for the first page (m = -inf)
-      l[u] = l[u] * c + wave_sum(pe);
-      m[u] = mnew;
-      p[wave * GW + u][lane] = pe;
-      if (lane == 0) corr[wave * GW + u] = c;
-    }
-    __syncthreads();
-    // P.V: thread tid owns dimension tid of every query head
-#pragma unroll
-    for (int g = 0; g < G; ++g) acc[g] *= corr[g];
-    // keys past n have p = 0 (their V rows may hold anything but are finite
-    // or not, so they are skipped, four keys at a time up to n)
-    for (int key = 0; key < n; key += 4) {
-      float vv[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) vv[e] = key + e < n ? bf2f(Vs[key + e][tid]) : 0.f;
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float4 pp = *reinterpret_cast<const float4*>(&p[g][key]);
-        acc[g] = fmaf(pp.x, vv[0], acc[g]);
-        acc[g] = fmaf(pp.y, vv[1], acc[g]);
-        acc[g] = fmaf(pp.z, vv[2], acc[g]);
-        acc[g] = fmaf(pp.w, vv[3], acc[g]);
+    for (int db = 0; db < 16; ++db) O[db] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+    auto load = [&](int kb, uint4(&kf)[8], uint2(&vf)[16]) {
+      int idx = (kb >> 2) - pbase;
+      if (idx >= 64) {  // wave-uniform: the next 64 page ids
+        pbase += 64;
+        idx -= 64;
+        pid = pbase + lane < npages ? prow[pbase + lane] : 0;
       }
-    }
-  }
-  // partials [T][Hkv][nsplit_max][G][2 + 256]: m, l, then the output
-  const size_t pb = (((size_t)t * Hkv + j) * nsplit_max + sp) * G * (2 + kHd);
+      const int page = __builtin_amdgcn_readlane(pid, idx);
+      const uint16_t* kt = kv_head + (size_t)page * page_stride + (size_t)(kb & 3) * 4096;
+      const uint4* ksrc = reinterpret_cast<const uint4*>(kt) + lane;
+      const uint2* vsrc = reinterpret_cast<const uint2*>(kt + v_shift) + lane;
 #pragma unroll
-  for (int g = 0; g < G; ++g) part[pb + (size_t)g * (2 + kHd) + 2 + tid] = acc[g];
-  if (lane == 0) {
+      for (int ks = 0; ks < 8; ++ks) kf[ks] = ksrc[64 * ks];
 #pragma unroll
-    for (int u = 0; u < GW; ++u) {
-      part[pb + (size_t)(wave * GW + u) * (2 + kHd)] = m[u];
-      part[pb + (size_t)(wave * GW + u) * (2 + kHd) + 1] = l[u];
+      for (int db = 0; db < 16; ++db) vf[db] = vsrc[64 * db];
+    };
+
+    auto compute = [&](int kb, const uint4(&kf)[8], uint2(&vf)[16]) {
+      f32x4 S = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks)  // volatile: re-read per block, not held in registers
+        S = mfma32(kf[ks], *const_cast<const volatile u32x4*>(&qlds[ks][lane]), S);
+      const int key0 = 16 * kb + 4 * g4;  // this lane's keys key0 .. key0 + 3
+      float x[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[r] = key0 + r <= cpos ? S[r] * scale_log2 : -INFINITY;
+      float bm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+      bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+      bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+      const float mnew = fmaxf(m, bm);
+      if (__any(mnew > m)) {
+        const float corr = mnew > m ? exp2f(m - mnew) : 1.0f;  // m = -inf: 0
+        lsum *= corr;
+#pragma unroll
+        for (int db = 0; db < 16; ++db) O[db] *= corr;
+        m = mnew;
+      }
+      const float mref = m == -INFINITY ? 0.f : m;
+      float p[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) p[r] = exp2f(x[r] - mref);  // masked: exp2(-inf) = 0
+      lsum += (p[0] + p[1]) + (p[2] + p[3]);
+      // p = hi + mid + lo exactly: each part takes the next 8 significant bits
+      uint32_t hi[4], mid[4], lo[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        hi[r] = f2bf(p[r]);
+        const float r1 = p[r] - bf2f((uint16_t)hi[r]);
+        mid[r] = f2bf(r1);
+        lo[r] = f2bf(r1 - bf2f((uint16_t)mid[r]));
+      }
+      const uint2 ph = make_uint2(hi[0] | hi[1] << 16, hi[2] | hi[3] << 16);
+      const uint2 pm = make_uint2(mid[0] | mid[1] << 16, mid[2] | mid[3] << 16);
+      const uint2 pl = make_uint2(lo[0] | lo[1] << 16, lo[2] | lo[3] << 16);
+      if (key0 + 3 >= nkeys) {  // rows past the group's last key: zero
+        const uint32_t m0 = (key0 < nkeys ? 0xffffu : 0u) | (key0 + 1 < nkeys ? 0xffff0000u : 0u);
+        const uint32_t m1 =
+            (key0 + 2 < nkeys ? 0xffffu : 0u) | (key0 + 3 < nkeys ? 0xffff0000u : 0u);
+#pragma unroll
+        for (int db = 0; db < 16; ++db) {
+          vf[db].x &= m0;
+          vf[db].y &= m1;
+        }
+      }
+#pragma unroll
+      for (int db = 0; db < 16; ++db) {
+        O[db] = mfma16(vf[db], ph, O[db]);
+        O[db] = mfma16(vf[db], pm, O[db]);
+        O[db] = mfma16(vf[db], pl, O[db]);
+      }
+    };
+
+    uint4 kA[8], kB[8];
+    uint2 vA[16], vB[16];
+    load(kb0, kA, vA);
+    for (int kb = kb0; kb < kb1; kb += 2) {
+      if (kb + 1 < kb1) load(kb + 1, kB, vB);
+      compute(kb, kA, vA);
+      if (kb + 1 >= kb1) break;
+      if (kb + 2 < kb1) load(kb + 2, kA, vA);
+      compute(kb + 1, kB, vB);
     }
+
+    lsum += __shfl_xor(lsum, 16, 64);
+    lsum += __shfl_xor(lsum, 32, 64);
+    const int piece = seg[4 * s + 1] + (w - seg[4 * s + 2]);
+    if (cvalid) {
+      float* pr = part + ((size_t)piece * 16 + c) * kPartLd;
+      if (g4 == 0) {
+        pr[0] = m;
+        pr[1] = lsum;
+      }
+#pragma unroll
+      for (int db = 0; db < 16; ++db)
+        *reinterpret_cast<float4*>(pr + 4 + 16 * db + 4 * g4) =
+            make_float4(O[db][0], O[db][1], O[db][2], O[db][3]);
+    }
+    f = sf0 + kb1;
+    ++s;
   }
 }
 
 // grid (T, Hkv), block 256: out[t, (j G + g) 256 + d] = bf16(bf16(o) *
-// bf16(sigmoid(gate))) with o the normalised merge of the splits; gate is the
-// second half of the head's q_proj outputs.
+// bf16(sigmoid(gate))) with o the normalised merge of the token's pieces;
+// gate is the second half of the head's q_proj outputs. tokseg[t] = the
+// token's group, tokseg[T + t] = its first column.
 template <int G>
 __global__ __launch_bounds__(kHd) void attn_combine_kernel(
-    const float* __restrict__ part, const int32_t* __restrict__ meta, int T, int Hkv,
-    int nsplit_max, const uint16_t* __restrict__ q_full, int64_t qs, uint16_t* __restrict__ out,
-    int64_t os) {
+    const float* __restrict__ part, const int32_t* __restrict__ tokseg,
+    const int32_t* __restrict__ seg, int T, int Hkv, const uint16_t* __restrict__ q_full,
+    int64_t qs, uint16_t* __restrict__ out, int64_t os) {
   const int t = blockIdx.x, j = blockIdx.y, d = threadIdx.x;
-  const int nkeys = meta[T + t] + 1;
-  const int ns = (nkeys + kSplitKeys - 1) / kSplitKeys;
-  const size_t pb = ((size_t)t * Hkv + j) * nsplit_max * G * (2 + kHd);
+  const int s = tokseg[t] * Hkv + j;
+  const int col0 = tokseg[T + t];
+  const int p0 = seg[4 * s + 1], np = seg[4 * s + 3];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
+    const float* pc = part + ((size_t)p0 * 16 + col0 + g) * kPartLd;
     float M = -INFINITY;
-    for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, part[pb + ((size_t)sp * G + g) * (2 + kHd)]);
+    for (int i = 0; i < np; ++i) M = fmaxf(M, pc[(size_t)i * 16 * kPartLd]);
     float L = 0.f, A = 0.f;
-    for (int sp = 0; sp < ns; ++sp) {
-      const float* ps = part + pb + ((size_t)sp * G + g) * (2 + kHd);
-      const float e = expf(ps[0] - M);
+    for (int i = 0; i < np; ++i) {
+      const float* ps = pc + (size_t)i * 16 * kPartLd;
+      const float e = exp2f(ps[0] - M);  // a piece with no key of this token: 0
       L = fmaf(ps[1], e, L);
-      A = fmaf(ps[2 + d], e, A);
+      A = fmaf(ps[4 + d], e, A);
     }
     const int hq = j * G + g;
     const float o = rbf(A / L);
@@ -246,43 +339,67 @@ __global__ __launch_bounds__(kHd) void attn_combine_kernel(
   }
 }
 
-int attn_splits(int max_keys) { return (max_keys + kSplitKeys - 1) / kSplitKeys; }
+// grid (pages of the sequence, Hkv, 2), block 256: a sequence's cached K (z =
+// 0) or V (z = 1) rows of one layer into dst [Hkv][len][256].
+__global__ __launch_bounds__(kHd) void kv_gather_kernel(const uint16_t* __restrict__ pages,
+                                                       const int32_t* __restrict__ prow, int Hkv,
+                                                       int64_t len, uint16_t* __restrict__ k_out,
+                                                       uint16_t* __restrict__ v_out) {
+  const int p = blockIdx.x, j = blockIdx.y, isv = blockIdx.z, d = threadIdx.x;
+  uint16_t* dst = isv ? v_out : k_out;
+  if (!dst) return;
+  const uint16_t* tile = pages + ((size_t)prow[p] * 2 * Hkv + (size_t)isv * Hkv + j) * kTile;
+  for (int kk = 0; kk < kPage; ++kk) {
+    const int64_t pos = (int64_t)p * kPage + kk;
+    if (pos >= len) break;
+    dst[((size_t)j * len + pos) * kHd + d] = tile[isv ? v_off(kk, d) : k_off(kk, d)];
+  }
+}
 
-size_t attn_workspace_bytes(int T, int Hq, int Hkv, int nsplit) {
-  const size_t qrot = ((size_t)T * Hq * kHd * 2 + 255) & ~(size_t)255;
-  const size_t part = (size_t)T * Hq * nsplit * (2 + kHd) * sizeof(float);
-  return qrot + part;
+size_t attn_part_offset(int T, int Hq) { return ((size_t)T * Hq * kHd * 2 + 255) & ~(size_t)255; }
+
+size_t attn_workspace_bytes(int T, int Hq, int64_t pieces) {
+  return attn_part_offset(T, Hq) + (size_t)pieces * 16 * kPartLd * sizeof(float);
 }
 
 hipError_t launch_attn(const AttnArgs& a) {
   if (a.T <= 0) return hipSuccess;
   const int G = a.Hq / a.Hkv;
   uint16_t* q_rot = static_cast<uint16_t*>(a.workspace);
-  float* part = reinterpret_cast<float*>(static_cast<char*>(a.workspace) +
-                                         (((size_t)a.T * a.Hq * kHd * 2 + 255) & ~(size_t)255));
+  float* part =
+      reinterpret_cast<float*>(static_cast<char*>(a.workspace) + attn_part_offset(a.T, a.Hq));
   hipLaunchKernelGGL(attn_prep_kernel, dim3(a.T, a.Hq + a.Hkv), dim3(kHd), 0, a.stream, a.q_full,
                      a.qs, a.k, a.ks, a.v, a.vs, a.q_norm_w, a.k_norm_w, a.eps, a.rot_dim,
                      a.log2_base, a.Hq, a.Hkv, a.meta, a.T, a.ptab, a.max_pages, a.pages, q_rot);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const float scale = 1.0f / sqrtf((float)kHd);
+  const float scale_log2 = 1.4426950408889634f / sqrtf((float)kHd);  // log2(e) / sqrt(256)
   if (G == 8) {
-    hipLaunchKernelGGL((attn_split_kernel<8>), dim3(a.T, a.Hkv, a.nsplit), dim3(kHd), 0, a.stream,
-                       q_rot, a.Hq, a.Hkv, a.meta, a.T, a.ptab, a.max_pages, a.pages, scale,
-                       a.nsplit, part);
+    hipLaunchKernelGGL((attn_block_kernel<8>), dim3(a.P), dim3(64), 0, a.stream, q_rot, a.Hq,
+                       a.Hkv, a.grp, a.seg, a.wseg, a.W, a.P, a.ptab, a.max_pages, a.pages,
+                       scale_log2, part);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL((attn_combine_kernel<8>), dim3(a.T, a.Hkv), dim3(kHd), 0, a.stream, part,
-                       a.meta, a.T, a.Hkv, a.nsplit, a.q_full, a.qs, a.out, a.os);
+                       a.tokseg, a.seg, a.T, a.Hkv, a.q_full, a.qs, a.out, a.os);
   } else if (G == 4) {
-    hipLaunchKernelGGL((attn_split_kernel<4>), dim3(a.T, a.Hkv, a.nsplit), dim3(kHd), 0, a.stream,
-                       q_rot, a.Hq, a.Hkv, a.meta, a.T, a.ptab, a.max_pages, a.pages, scale,
-                       a.nsplit, part);
+    hipLaunchKernelGGL((attn_block_kernel<4>), dim3(a.P), dim3(64), 0, a.stream, q_rot, a.Hq,
+                       a.Hkv, a.grp, a.seg, a.wseg, a.W, a.P, a.ptab, a.max_pages, a.pages,
+                       scale_log2, part);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL((attn_combine_kernel<4>), dim3(a.T, a.Hkv), dim3(kHd), 0, a.stream, part,
-                       a.meta, a.T, a.Hkv, a.nsplit, a.q_full, a.qs, a.out, a.os);
+                       a.tokseg, a.seg, a.T, a.Hkv, a.q_full, a.qs, a.out, a.os);
   } else {
     return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_kv_gather(const uint16_t* pages, const int32_t* prow, int Hkv, int64_t len,
+                            uint16_t* k_out, uint16_t* v_out, hipStream_t s) {
+  if (len <= 0) return hipSuccess;
+  const int np = (int)((len + kPage - 1) / kPage);
+  hipLaunchKernelGGL(kv_gather_kernel, dim3(np, Hkv, 2), dim3(kHd), 0, s, pages, prow, Hkv, len,
+                     k_out, v_out);
   return hipGetLastError();
 }
 

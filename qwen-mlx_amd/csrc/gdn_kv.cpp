@@ -8,10 +8,22 @@
 // covering the same positions in every layer, handed out by a host free list;
 // a sequence's page table maps position / 64 to its pages. A step first
 // plans the tokens it appends (gdn_kv_step: per token its sequence slot,
-// position and page, staged to the device once for all layers), then each
-// attention layer runs gdn_attn_forward on the same packed tokens.
+// position and page, and the attention schedule, staged to the device once
+// for all layers), then each attention layer runs gdn_attn_forward on the
+// same packed tokens.
+//
+// The schedule: the step's tokens form groups of up to 16 / G consecutive
+// tokens of one sequence (G query heads per kv head: a group's (token, head)
+// pairs fill the 16 columns of an MFMA tile); each (group, kv head) segment
+// is its keys' 16-key blocks. All segments' blocks, in order, are split
+// evenly over P one-wave workers, P up to max_workers (default: the waves
+// the chip keeps resident), at least kMinBlocks blocks each; a worker writes one
+// partial per segment it touches and the combine kernel merges a segment's
+// partials, which come from consecutive workers.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -38,6 +50,11 @@ gdn_status khip(hipError_t e, const char* what) {
 
 constexpr int kPageTokens = 64;
 constexpr int kHeadDim = 256;
+constexpr int kMaxWorkers = 2048;  // 256 CUs x 8 resident one-wave work-groups
+constexpr int kMinBlocks = 8;      // 16-key blocks per worker at least
+
+// int32 words of the step metadata for up to T tokens and P workers
+size_t meta_words(int T, int Hkv, int P) { return (size_t)T * (5 + 4 + 4 * (size_t)Hkv) + P; }
 
 struct Dev {
   int prev = -1;
@@ -59,12 +76,16 @@ struct gdn_kv {
   std::vector<int32_t> free_pages;
   std::vector<int64_t> len;                  // tokens cached per slot
   std::vector<std::vector<int32_t>> owned;   // pages per slot, in position order
-  int32_t* d_meta = nullptr;     // [3][max_step_tokens]
+  // step metadata: [3][T] slot, position, page; [2][T] group, first column;
+  // grp [NG][4]; seg [NG * Hkv][4]; wseg [P]
+  int32_t* d_meta = nullptr;
   int32_t* p_meta = nullptr;     // pinned staging
   hipEvent_t meta_copied = nullptr;
   void* workspace = nullptr;
   size_t ws_bytes = 0;
-  int T = 0, nsplit = 0;         // the planned step
+  // the planned step
+  int T = 0, NG = 0, P = 0;
+  int64_t W = 0;
   bool planned = false;
 };
 
@@ -99,11 +120,14 @@ gdn_status gdn_kv_create(const gdn_kv_desc* desc, gdn_kv** out) {
       (d.num_q_heads / d.num_kv_heads != 4 && d.num_q_heads / d.num_kv_heads != 8))
     return kfail(GDN_ERR_UNSUPPORTED, "gdn_kv_create: %d query heads per kv head (4 or 8 supported)",
                  d.num_q_heads / d.num_kv_heads);
+  if (d.max_workers < 0 || d.max_workers > 65536)
+    return kfail(GDN_ERR_INVALID, "gdn_kv_create: max_workers %d outside [0, 65536]", d.max_workers);
   if ((int64_t)d.max_pages_per_slot * kPageTokens > (int64_t)1 << 30)
     return kfail(GDN_ERR_INVALID, "gdn_kv_create: max_pages_per_slot too large");
   Dev dev(d.device);
   gdn_kv* kv = new gdn_kv;
   kv->d = d;
+  if (kv->d.max_workers == 0) kv->d.max_workers = kMaxWorkers;
   const size_t page_bytes = (size_t)2 * d.num_kv_heads * kPageTokens * kHeadDim * 2;
   bool ok = true;
   for (int l = 0; l < d.num_layers && ok; ++l) {
@@ -111,9 +135,10 @@ gdn_status gdn_kv_create(const gdn_kv_desc* desc, gdn_kv** out) {
     ok = hipMalloc(&p, page_bytes * d.num_pages) == hipSuccess;
     kv->pages.push_back(p);
   }
+  const size_t mwords = meta_words(d.max_step_tokens, d.num_kv_heads, kv->d.max_workers);
   ok = ok && hipMalloc(&kv->ptab, sizeof(int32_t) * d.num_slots * d.max_pages_per_slot) == hipSuccess &&
-       hipMalloc(&kv->d_meta, sizeof(int32_t) * 3 * (size_t)d.max_step_tokens) == hipSuccess &&
-       hipHostMalloc(&kv->p_meta, sizeof(int32_t) * 3 * (size_t)d.max_step_tokens, 0) == hipSuccess &&
+       hipMalloc(&kv->d_meta, sizeof(int32_t) * mwords) == hipSuccess &&
+       hipHostMalloc(&kv->p_meta, sizeof(int32_t) * mwords, 0) == hipSuccess &&
        hipEventCreateWithFlags(&kv->meta_copied, hipEventDisableTiming) == hipSuccess;
   if (!ok) {
     (void)hipGetLastError();
@@ -193,12 +218,56 @@ gdn_status gdn_kv_step(gdn_kv* kv, int32_t n, const int32_t* slots, const int32_
                  kv->free_pages.size());
   Dev dev(d.device);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // the attention workspace for this step, sized before any state changes
-  int64_t max_keys = 0;
-  for (int i = 0; i < n; ++i)
-    if (kv->len[slots[i]] + ntok[i] > max_keys) max_keys = kv->len[slots[i]] + ntok[i];
-  const int nsplit = gdn::attn_splits((int)max_keys);
-  const size_t ws = gdn::attn_workspace_bytes((int)T, d.num_q_heads, d.num_kv_heads, nsplit);
+  // the attention schedule and workspace for this step, sized before any
+  // state changes
+  const int G = d.num_q_heads / d.num_kv_heads, Hkv = d.num_kv_heads;
+  const int tpg = 16 / G;
+  struct Group {
+    int32_t t0, ntok, pos0, slot;
+  };
+  std::vector<Group> groups;
+  {
+    int32_t t0 = 0;
+    for (int i = 0; i < n; ++i) {
+      for (int32_t k = 0; k < ntok[i]; k += tpg) {
+        const int32_t nt = ntok[i] - k < tpg ? ntok[i] - k : tpg;
+        groups.push_back({t0 + k, nt, (int32_t)(kv->len[slots[i]] + k), slots[i]});
+      }
+      t0 += ntok[i];
+    }
+  }
+  const int NG = (int)groups.size(), NS = NG * Hkv;
+  std::vector<int64_t> sf0(NS + 1);
+  sf0[0] = 0;
+  for (int gi = 0; gi < NG; ++gi) {
+    const int64_t nblk = ((int64_t)groups[gi].pos0 + groups[gi].ntok + 15) / 16;
+    for (int j = 0; j < Hkv; ++j) sf0[gi * Hkv + j + 1] = sf0[gi * Hkv + j] + nblk;
+  }
+  const int64_t W = sf0[NS];
+  if (W > INT32_MAX) return kfail(GDN_ERR_INVALID, "gdn_kv_step: %lld key blocks", (long long)W);
+  const int P = (int)std::min<int64_t>(d.max_workers, (W + kMinBlocks - 1) / kMinBlocks);
+  // worker w owns flat blocks [a(w), a(w + 1)), a(w) = w W / P
+  auto a = [&](int64_t w) { return w * W / P; };
+  std::vector<int32_t> seg_wf(NS), seg_np(NS), seg_pb(NS), wseg(P);
+  int64_t pieces = 0;
+  {
+    int w = 0;
+    for (int sg = 0; sg < NS; ++sg) {
+      while (a(w + 1) <= sf0[sg]) ++w;
+      int wl = w;
+      while (a(wl + 1) <= sf0[sg + 1] - 1) ++wl;
+      seg_wf[sg] = w;
+      seg_np[sg] = wl - w + 1;
+      seg_pb[sg] = (int32_t)pieces;
+      pieces += seg_np[sg];
+    }
+    int sg = 0;
+    for (int ww = 0; ww < P; ++ww) {
+      while (sf0[sg + 1] <= a(ww)) ++sg;
+      wseg[ww] = sg;
+    }
+  }
+  const size_t ws = gdn::attn_workspace_bytes((int)T, d.num_q_heads, pieces);
   hipError_t e;
   if (ws > kv->ws_bytes) {
     if (kv->workspace) {
@@ -219,6 +288,29 @@ gdn_status gdn_kv_step(gdn_kv* kv, int32_t n, const int32_t* slots, const int32_
   int32_t* m_slot = kv->p_meta;
   int32_t* m_pos = kv->p_meta + T;
   int32_t* m_page = kv->p_meta + 2 * T;
+  int32_t* m_tokseg = kv->p_meta + 3 * T;
+  int32_t* m_grp = kv->p_meta + 5 * T;
+  int32_t* m_seg = m_grp + 4 * NG;
+  int32_t* m_wseg = m_seg + 4 * NS;
+  for (int gi = 0; gi < NG; ++gi) {
+    const Group& g = groups[gi];
+    m_grp[4 * gi] = g.t0;
+    m_grp[4 * gi + 1] = g.ntok;
+    m_grp[4 * gi + 2] = g.pos0;
+    m_grp[4 * gi + 3] = g.slot;
+    for (int k = 0; k < g.ntok; ++k) {
+      m_tokseg[g.t0 + k] = gi;
+      m_tokseg[T + g.t0 + k] = k * G;
+    }
+  }
+  for (int sg = 0; sg < NS; ++sg) {
+    m_seg[4 * sg] = (int32_t)sf0[sg];
+    m_seg[4 * sg + 1] = seg_pb[sg];
+    m_seg[4 * sg + 2] = seg_wf[sg];
+    m_seg[4 * sg + 3] = seg_np[sg];
+  }
+  for (int ww = 0; ww < P; ++ww) m_wseg[ww] = wseg[ww];
+  const size_t words = (size_t)5 * T + 4 * (size_t)NG + 4 * (size_t)NS + P;
   int64_t t = 0;
   for (int i = 0; i < n; ++i) {
     const int32_t sl = slots[i];
@@ -234,14 +326,16 @@ gdn_status gdn_kv_step(gdn_kv* kv, int32_t n, const int32_t* slots, const int32_
     }
     kv->len[sl] += ntok[i];
   }
-  if ((e = hipMemcpyAsync(kv->d_meta, kv->p_meta, sizeof(int32_t) * 3 * T, hipMemcpyHostToDevice,
+  if ((e = hipMemcpyAsync(kv->d_meta, kv->p_meta, sizeof(int32_t) * words, hipMemcpyHostToDevice,
                           s)) != hipSuccess ||
       (e = hipEventRecord(kv->meta_copied, s)) != hipSuccess) {
     kv->planned = false;
     return khip(e, "gdn_kv_step copy");
   }
   kv->T = (int)T;
-  kv->nsplit = nsplit;
+  kv->NG = NG;
+  kv->P = P;
+  kv->W = W;
   kv->planned = true;
   return GDN_OK;
 }
@@ -270,7 +364,8 @@ gdn_status gdn_attn_forward(gdn_kv* kv, int32_t layer, const uint16_t* q_full, i
   a.T = kv->T;
   a.Hq = d.num_q_heads;
   a.Hkv = d.num_kv_heads;
-  a.nsplit = kv->nsplit;
+  a.P = kv->P;
+  a.W = kv->W;
   a.max_pages = d.max_pages_per_slot;
   a.rot_dim = rotary_dim;
   a.eps = norm_eps;
@@ -284,6 +379,10 @@ gdn_status gdn_attn_forward(gdn_kv* kv, int32_t layer, const uint16_t* q_full, i
   a.q_norm_w = q_norm_w;
   a.k_norm_w = k_norm_w;
   a.meta = kv->d_meta;
+  a.tokseg = kv->d_meta + 3 * (size_t)kv->T;
+  a.grp = kv->d_meta + 5 * (size_t)kv->T;
+  a.seg = a.grp + 4 * (size_t)kv->NG;
+  a.wseg = a.seg + 4 * (size_t)kv->NG * d.num_kv_heads;
   a.ptab = kv->ptab;
   a.pages = kv->pages[layer];
   a.out = out;
@@ -304,21 +403,10 @@ gdn_status gdn_kv_read(gdn_kv* kv, int32_t layer, int32_t slot, uint16_t* k_out,
   Dev dev(d.device);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t L = kv->len[slot];
-  const size_t row = (size_t)kHeadDim * 2;
-  for (int64_t p0 = 0; p0 < L; p0 += kPageTokens) {
-    const int page = kv->owned[slot][p0 / kPageTokens];
-    const int64_t rows = L - p0 < kPageTokens ? L - p0 : kPageTokens;
-    for (int j = 0; j < d.num_kv_heads; ++j)
-      for (int kvsel = 0; kvsel < 2; ++kvsel) {
-        uint16_t* dst = kvsel == 0 ? k_out : v_out;
-        if (!dst) continue;
-        const uint16_t* src =
-            kv->pages[layer] + (((size_t)page * 2 + kvsel) * d.num_kv_heads + j) * kPageTokens * kHeadDim;
-        hipError_t e = hipMemcpyAsync(dst + ((size_t)j * L + p0) * kHeadDim, src, rows * row,
-                                      hipMemcpyDeviceToDevice, s);
-        if (e != hipSuccess) return khip(e, "gdn_kv_read");
-      }
-  }
+  hipError_t e = gdn::launch_kv_gather(kv->pages[layer],
+                                       kv->ptab + (size_t)slot * d.max_pages_per_slot,
+                                       d.num_kv_heads, L, k_out, v_out, s);
+  if (e != hipSuccess) return khip(e, "gdn_kv_read");
   return GDN_OK;
 }
 

@@ -109,7 +109,8 @@ class LayerDesc(ctypes.Structure):
 class KVDesc(ctypes.Structure):
     _fields_ = [("num_layers", _I32), ("num_slots", _I32), ("num_pages", _I32),
                 ("max_pages_per_slot", _I32), ("num_q_heads", _I32), ("num_kv_heads", _I32),
-                ("head_dim", _I32), ("max_step_tokens", _I32), ("device", _I32)]
+                ("head_dim", _I32), ("max_step_tokens", _I32), ("device", _I32),
+                ("max_workers", _I32)]
 
 
 class ExecDesc(ctypes.Structure):
@@ -414,10 +415,10 @@ class KVCache:
 
     def __init__(self, num_layers: int, num_slots: int, num_pages: int, max_pages_per_slot: int,
                  num_q_heads: int = 16, num_kv_heads: int = 2, max_step_tokens: int = 4096,
-                 device: int = 0):
+                 device: int = 0, max_workers: int = 0):
         self.lib = load()
         d = KVDesc(num_layers, num_slots, num_pages, max_pages_per_slot, num_q_heads,
-                   num_kv_heads, 256, max_step_tokens, device)
+                   num_kv_heads, 256, max_step_tokens, device, max_workers)
         h = _VP()
         _check(self.lib.gdn_kv_create(ctypes.byref(d), ctypes.byref(h)))
         self.handle = h

@@ -2,13 +2,18 @@
 (gdn_kv_step + gdn_attn_forward: Qwen35Attention::forward_with_cache,
 qwen3_5.rs:377-455) against the oracle's per-sequence restatement.
 
-Bars: gated outputs within 2e-2 absolute and 1e-2 relative L2 of the oracle
+Bars: gated outputs within 2e-2 (absolute below 1, relative above) and 1e-2
+relative L2 of the oracle
 (float32 softmax and accumulation against float64); cached values bit-exact;
 cached keys (norm and RoPE in float32) within one bf16 ulp of the key plus one
-of its RoPE pair's magnitude. A token's work
-reads only its own sequence, so a batched step equals the same sequences
-stepped alone bit for bit -- the property the reference's padded, unmasked,
-single-offset batching (mlx_executor.rs:57-88, qwen3_5.rs:410,443-447) lacks.
+of its RoPE pair's magnitude. A token's work reads only its own sequence, so a
+batched step equals the same sequences stepped alone -- caches bit for bit,
+outputs up to float32 reassociation (the step's key blocks are split evenly
+over the workers, so where a token's keys are cut into partials depends on the
+whole step, and the float32 merge order with it) -- the property the
+reference's
+padded, unmasked, single-offset batching (mlx_executor.rs:57-88,
+qwen3_5.rs:410,443-447) lacks.
 """
 import numpy as np
 import pytest
@@ -69,7 +74,7 @@ def _run_step(kv, seqs, slots, ntok, gpu, check=True, label=""):
                 ref = seqs.oracle(layer, s, q[r0:r0 + n], k[r0:r0 + n], v[r0:r0 + n])
                 g = O.bf16_to_f32(outs[layer][r0:r0 + n])
                 rf = O.bf16_to_f32(ref)
-                worst_abs = max(worst_abs, float(np.max(np.abs(g - rf))))
+                worst_abs = max(worst_abs, float(np.max(np.abs(g - rf) / np.maximum(1.0, np.abs(rf)))))
                 worst_rel = max(worst_rel, rel_l2(g, rf))
                 r0 += n
         say(label, f"|d out| {worst_abs:.2e} relL2 {worst_rel:.2e}")
@@ -131,7 +136,11 @@ def test_attention_prefill_then_decode_matches_oracle(gpu, Hq, Hkv):
 
 def test_attention_batched_step_equals_sequences_alone(gpu):
     """Three sequences of different lengths stepped together and, on a twin
-    cache, each alone: outputs and caches bit-identical."""
+    cache, each alone: caches bit-identical; outputs within two bf16 ulps or
+    2^-12 absolute (float32 reassociation moves o by ~1e-7 of the sum of
+    |p v|, which can flip bf16 roundings of o and of the gated product). A
+    key of another sequence, or padding, in a token's softmax would move its
+    output by about p |v|, orders of magnitude more."""
     import torch
 
     import gdn_amd
@@ -158,7 +167,13 @@ def test_attention_batched_step_equals_sequences_alone(gpu):
                        ob[r0:r0 + n])
             r0 += n
         torch.cuda.synchronize()
-        assert torch.equal(oa, ob), ntok
+        a = O.bf16_to_f32(host(oa)).astype(np.float64)
+        b = O.bf16_to_f32(host(ob)).astype(np.float64)
+        bound = 2.0 * _ulp(np.maximum(np.abs(a), np.abs(b))) + 2.0 ** -12
+        ratio = np.abs(a - b) / bound
+        say("batched vs alone", f"ntok {ntok}: {int(np.sum(a != b))} of {a.size} differ, "
+                                f"worst |d| / bound {ratio.max():.2f}")
+        assert np.all(ratio <= 1.0), ntok
     for s in slots:
         for x, y in zip(ka.read(0, s), kb.read(0, s)):
             assert torch.equal(x, y)
@@ -185,6 +200,27 @@ def test_attention_long_context_splits(gpu):
     for step in range(2):
         _run_step(kv, seqs, [1], [1], gpu, label=f"decode at {kv.length(1)} keys")
     assert kv.length(1) == 2502
+    kv.close()
+
+
+@pytest.mark.parametrize("workers", [1, 3])
+def test_attention_few_workers(gpu, workers):
+    """All of a step's key blocks on one or three workers: pieces run over
+    many segments and past 64 pages (the page-id reload), then a mixed step
+    of a 40-token prompt and a decode, against the oracle."""
+    import gdn_amd
+    say("gdn_attn_forward", f"max_workers={workers}")
+    rng = np.random.default_rng(1430 + workers)
+    Hq, Hkv = 16, 2
+    kv = gdn_amd.KVCache(1, 2, 96, 96, Hq, Hkv, max_step_tokens=2500, max_workers=workers)
+    seqs = _Seqs(rng, Hq, Hkv, 1)
+    _run_step(kv, seqs, [0], [2500], gpu, check=False)
+    _run_step(kv, seqs, [0], [2500], gpu, check=False)
+    kg, vg = kv.read(0, 0)
+    seqs.cache[(0, 0)] = (host(kg), host(vg))
+    _run_step(kv, seqs, [0], [1], gpu, label=f"decode at {kv.length(0)} keys")
+    _run_step(kv, seqs, [1, 0], [40, 1], gpu, label="40-token prompt + decode")
+    _check_cache(kv, seqs, [1], gpu)
     kv.close()
 
 
