@@ -61,10 +61,12 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
   return t;
 }
 
-__device__ __forceinline__ f32x4 mfma32(uint4 a, uint4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
 }
+
 // 16-deep product: lane l holds row l%16, k = 4 (l/16) .. +3 of each operand
 __device__ __forceinline__ f32x4 mfma16(uint2 a, uint2 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
@@ -307,36 +309,65 @@ __global__ __launch_bounds__(64, 2) void attn_block_kernel(
   }
 }
 
-// grid (T, Hkv), block 256: out[t, (j G + g) 256 + d] = bf16(bf16(o) *
-// bf16(sigmoid(gate))) with o the normalised merge of the token's pieces;
-// gate is the second half of the head's q_proj outputs. tokseg[t] = the
-// token's group, tokseg[T + t] = its first column.
+// grid (T, Hq), block 256: out[t, hq 256 + d] = bf16(bf16(o) *
+// bf16(sigmoid(gate))) with o the normalised merge of the token's pieces for
+// query head hq; gate is the second half of the head's q_proj outputs.
+// tokseg[t] = the token's group, tokseg[T + t] = its first column. The 256
+// threads first take the pieces' maxima, then work as 8 groups of 32 over the
+// pieces (group i: pieces i, i + 8, ...; a thread 8 output dimensions), and
+// the groups' sums meet in LDS, in a fixed order.
 template <int G>
 __global__ __launch_bounds__(kHd) void attn_combine_kernel(
     const float* __restrict__ part, const int32_t* __restrict__ tokseg,
     const int32_t* __restrict__ seg, int T, int Hkv, const uint16_t* __restrict__ q_full,
     int64_t qs, uint16_t* __restrict__ out, int64_t os) {
-  const int t = blockIdx.x, j = blockIdx.y, d = threadIdx.x;
+  __shared__ float red[8][kHd];
+  __shared__ float redl[8];
+  __shared__ float redm[4];
+  const int t = blockIdx.x, hq = blockIdx.y, tid = threadIdx.x;
+  const int j = hq / G, g = hq - j * G;
   const int s = tokseg[t] * Hkv + j;
-  const int col0 = tokseg[T + t];
   const int p0 = seg[4 * s + 1], np = seg[4 * s + 3];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float* pc = part + ((size_t)p0 * 16 + col0 + g) * kPartLd;
-    float M = -INFINITY;
-    for (int i = 0; i < np; ++i) M = fmaxf(M, pc[(size_t)i * 16 * kPartLd]);
-    float L = 0.f, A = 0.f;
-    for (int i = 0; i < np; ++i) {
-      const float* ps = pc + (size_t)i * 16 * kPartLd;
-      const float e = exp2f(ps[0] - M);  // a piece with no key of this token: 0
-      L = fmaf(ps[1], e, L);
-      A = fmaf(ps[4 + d], e, A);
-    }
-    const int hq = j * G + g;
-    const float o = rbf(A / L);
-    const float gate = bf2f(q_full[(size_t)t * qs + (size_t)hq * 2 * kHd + kHd + d]);
-    out[(size_t)t * os + (size_t)hq * kHd + d] = f2bf(o * rbf(sigmoid_f32(gate)));
+  const float* pc = part + ((size_t)p0 * 16 + tokseg[T + t] + g) * kPartLd;
+  constexpr size_t kStride = (size_t)16 * kPartLd;  // consecutive pieces
+  float mx = -INFINITY;
+  for (int i = tid; i < np; i += kHd) mx = fmaxf(mx, pc[i * kStride]);
+  mx = wave_max(mx);
+  if ((tid & 63) == 0) redm[tid >> 6] = mx;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(redm[0], redm[1]), fmaxf(redm[2], redm[3]));
+  const int grp = tid >> 5, d8 = 8 * (tid & 31);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float L = 0.f;
+#pragma unroll 4
+  for (int i = grp; i < np; i += 8) {
+    const float* ps = pc + i * kStride;
+    const float e = exp2f(ps[0] - M);  // a piece with no key of this token: 0
+    L = fmaf(ps[1], e, L);
+    const float4 a = *reinterpret_cast<const float4*>(ps + 4 + d8);
+    const float4 b = *reinterpret_cast<const float4*>(ps + 8 + d8);
+    acc[0] = fmaf(a.x, e, acc[0]);
+    acc[1] = fmaf(a.y, e, acc[1]);
+    acc[2] = fmaf(a.z, e, acc[2]);
+    acc[3] = fmaf(a.w, e, acc[3]);
+    acc[4] = fmaf(b.x, e, acc[4]);
+    acc[5] = fmaf(b.y, e, acc[5]);
+    acc[6] = fmaf(b.z, e, acc[6]);
+    acc[7] = fmaf(b.w, e, acc[7]);
   }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) red[grp][d8 + k] = acc[k];
+  if ((tid & 31) == 0) redl[grp] = L;
+  __syncthreads();
+  float A = 0.f, Lt = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    A += red[i][tid];
+    Lt += redl[i];
+  }
+  const float o = rbf(A / Lt);
+  const float gate = bf2f(q_full[(size_t)t * qs + (size_t)hq * 2 * kHd + kHd + tid]);
+  out[(size_t)t * os + (size_t)hq * kHd + tid] = f2bf(o * rbf(sigmoid_f32(gate)));
 }
 
 // grid (pages of the sequence, Hkv, 2), block 256: a sequence's cached K (z =
@@ -379,14 +410,14 @@ hipError_t launch_attn(const AttnArgs& a) {
                        a.Hkv, a.grp, a.seg, a.wseg, a.W, a.P, a.ptab, a.max_pages, a.pages,
                        scale_log2, part);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL((attn_combine_kernel<8>), dim3(a.T, a.Hkv), dim3(kHd), 0, a.stream, part,
+    hipLaunchKernelGGL((attn_combine_kernel<8>), dim3(a.T, a.Hq), dim3(kHd), 0, a.stream, part,
                        a.tokseg, a.seg, a.T, a.Hkv, a.q_full, a.qs, a.out, a.os);
   } else if (G == 4) {
     hipLaunchKernelGGL((attn_block_kernel<4>), dim3(a.P), dim3(64), 0, a.stream, q_rot, a.Hq,
                        a.Hkv, a.grp, a.seg, a.wseg, a.W, a.P, a.ptab, a.max_pages, a.pages,
                        scale_log2, part);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL((attn_combine_kernel<4>), dim3(a.T, a.Hkv), dim3(kHd), 0, a.stream, part,
+    hipLaunchKernelGGL((attn_combine_kernel<4>), dim3(a.T, a.Hq), dim3(kHd), 0, a.stream, part,
                        a.tokseg, a.seg, a.T, a.Hkv, a.q_full, a.qs, a.out, a.os);
   } else {
     return hipErrorInvalidValue;

@@ -3,17 +3,15 @@
 qwen3_5.rs:377-455) against the oracle's per-sequence restatement.
 
 Bars: gated outputs within 2e-2 (absolute below 1, relative above) and 1e-2
-relative L2 of the oracle
-(float32 softmax and accumulation against float64); cached values bit-exact;
-cached keys (norm and RoPE in float32) within one bf16 ulp of the key plus one
-of its RoPE pair's magnitude. A token's work reads only its own sequence, so a
-batched step equals the same sequences stepped alone -- caches bit for bit,
-outputs up to float32 reassociation (the step's key blocks are split evenly
-over the workers, so where a token's keys are cut into partials depends on the
-whole step, and the float32 merge order with it) -- the property the
-reference's
-padded, unmasked, single-offset batching (mlx_executor.rs:57-88,
-qwen3_5.rs:410,443-447) lacks.
+relative L2 of the oracle (float32 softmax and accumulation against float64);
+cached values bit-exact; cached keys (norm and RoPE in float32) within one
+bf16 ulp of the key plus one of its RoPE pair's magnitude. A token's work
+reads only its own sequence, so a batched step equals the same sequences
+stepped alone -- caches bit for bit, outputs up to float32 reassociation (the
+step's key blocks are split evenly over the workers, so where a token's keys
+are cut into partials depends on the whole step, and the float32 merge order
+with it) -- the property the reference's padded, unmasked, single-offset
+batching (mlx_executor.rs:57-88, qwen3_5.rs:410,443-447) lacks.
 """
 import numpy as np
 import pytest
