@@ -454,8 +454,9 @@ typedef struct gdn_kv_desc {
   int32_t max_step_tokens;     /* most tokens one step appends (all sequences)   */
   int32_t device;
   int32_t max_workers;         /* waves a step's attention is split over; 0 =
-                                  2048, the one-wave work-groups the chip keeps
-                                  resident (fewer when sharing the GPU)         */
+                                  1024 when each key is read about once (decode
+                                  steps), 2048 when a step re-reads its keys
+                                  (prompts); fewer when sharing the GPU        */
 } gdn_kv_desc;
 
 /* Per layer num_pages x 128 KiB of bf16 K/V (at 2 kv heads), a page table,

@@ -42,6 +42,7 @@ constexpr int kPartLd = 4 + kHd;    // partial row: m, l, 2 pad, 256 outputs (f3
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int k_off(int kk, int d) {
@@ -158,7 +159,7 @@ __global__ __launch_bounds__(kHd) void attn_prep_kernel(
 //   seg[NS][4]  first flat block, first partial, first worker, partials
 //   wseg[P]     segment of the worker's first block
 // Partials [pieces][16][kPartLd] f32: running max (log2 domain), sum, output.
-template <int G>
+template <int G, bool STREAM>
 __global__ __launch_bounds__(64, 2) void attn_block_kernel(
     const uint16_t* __restrict__ q_rot, int Hq, int Hkv, const int32_t* __restrict__ grp,
     const int32_t* __restrict__ seg, const int32_t* __restrict__ wseg, int64_t W, int P,
@@ -216,12 +217,21 @@ __global__ __launch_bounds__(64, 2) void attn_block_kernel(
       }
       const int page = __builtin_amdgcn_readlane(pid, idx);
       const uint16_t* kt = kv_head + (size_t)page * page_stride + (size_t)(kb & 3) * 4096;
-      const uint4* ksrc = reinterpret_cast<const uint4*>(kt) + lane;
-      const uint2* vsrc = reinterpret_cast<const uint2*>(kt + v_shift) + lane;
+      // STREAM (each block read about once in the step): non-temporal loads
+      // stream past the caches; otherwise plain loads keep the blocks that
+      // later token groups of the same prompt read again
+      const u32x4* ksrc = reinterpret_cast<const u32x4*>(kt) + lane;
+      const u32x2* vsrc = reinterpret_cast<const u32x2*>(kt + v_shift) + lane;
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) kf[ks] = ksrc[64 * ks];
+      for (int ks = 0; ks < 8; ++ks) {
+        const u32x4 x = STREAM ? __builtin_nontemporal_load(ksrc + 64 * ks) : ksrc[64 * ks];
+        kf[ks] = make_uint4(x[0], x[1], x[2], x[3]);
+      }
 #pragma unroll
-      for (int db = 0; db < 16; ++db) vf[db] = vsrc[64 * db];
+      for (int db = 0; db < 16; ++db) {
+        const u32x2 x = STREAM ? __builtin_nontemporal_load(vsrc + 64 * db) : vsrc[64 * db];
+        vf[db] = make_uint2(x[0], x[1]);
+      }
     };
 
     auto compute = [&](int kb, const uint4(&kf)[8], uint2(&vf)[16]) {
@@ -405,17 +415,23 @@ hipError_t launch_attn(const AttnArgs& a) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const float scale_log2 = 1.4426950408889634f / sqrtf((float)kHd);  // log2(e) / sqrt(256)
+  auto blocks = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(a.P), dim3(64), 0, a.stream, q_rot, a.Hq, a.Hkv, a.grp, a.seg,
+                       a.wseg, a.W, a.P, a.ptab, a.max_pages, a.pages, scale_log2, part);
+  };
   if (G == 8) {
-    hipLaunchKernelGGL((attn_block_kernel<8>), dim3(a.P), dim3(64), 0, a.stream, q_rot, a.Hq,
-                       a.Hkv, a.grp, a.seg, a.wseg, a.W, a.P, a.ptab, a.max_pages, a.pages,
-                       scale_log2, part);
+    if (a.stream_keys)
+      blocks(attn_block_kernel<8, true>);
+    else
+      blocks(attn_block_kernel<8, false>);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL((attn_combine_kernel<8>), dim3(a.T, a.Hq), dim3(kHd), 0, a.stream, part,
                        a.tokseg, a.seg, a.T, a.Hkv, a.q_full, a.qs, a.out, a.os);
   } else if (G == 4) {
-    hipLaunchKernelGGL((attn_block_kernel<4>), dim3(a.P), dim3(64), 0, a.stream, q_rot, a.Hq,
-                       a.Hkv, a.grp, a.seg, a.wseg, a.W, a.P, a.ptab, a.max_pages, a.pages,
-                       scale_log2, part);
+    if (a.stream_keys)
+      blocks(attn_block_kernel<4, true>);
+    else
+      blocks(attn_block_kernel<4, false>);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL((attn_combine_kernel<4>), dim3(a.T, a.Hq), dim3(kHd), 0, a.stream, part,
                        a.tokseg, a.seg, a.T, a.Hkv, a.q_full, a.qs, a.out, a.os);

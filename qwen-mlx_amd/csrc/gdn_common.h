@@ -235,6 +235,7 @@ hipError_t launch_prefill(const PrefillArgs& a);
 struct AttnArgs {
   int T, Hq, Hkv, P, max_pages, rot_dim;
   int64_t W;               // 16-key blocks of work in the step
+  bool stream_keys;        // each block read about once (non-temporal loads)
   float eps, log2_base;
   const uint16_t* q_full;  // [T, qs]: per query head 256 query then 256 gate values
   int64_t qs;

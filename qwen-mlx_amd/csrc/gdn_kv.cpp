@@ -16,8 +16,8 @@
 // tokens of one sequence (G query heads per kv head: a group's (token, head)
 // pairs fill the 16 columns of an MFMA tile); each (group, kv head) segment
 // is its keys' 16-key blocks. All segments' blocks, in order, are split
-// evenly over P one-wave workers, P up to max_workers (default: the waves
-// the chip keeps resident), at least kMinBlocks blocks each; a worker writes one
+// evenly over P one-wave workers, P up to max_workers (default below), at
+// least kMinBlocks blocks each; a worker writes one
 // partial per segment it touches and the combine kernel merges a segment's
 // partials, which come from consecutive workers.
 #include <hip/hip_runtime.h>
@@ -50,11 +50,18 @@ gdn_status khip(hipError_t e, const char* what) {
 
 constexpr int kPageTokens = 64;
 constexpr int kHeadDim = 256;
-constexpr int kMaxWorkers = 2048;  // 256 CUs x 8 resident one-wave work-groups
+// Workers per step: a step whose key blocks are each read about once (decode)
+// streams from HBM and runs best at one wave per SIMD (256 CUs x 4); one that
+// re-reads them from cache (a prompt's token groups share its keys) wants the
+// two resident waves per SIMD the block kernel's registers allow.
+constexpr int kStreamWorkers = 1024;
+constexpr int kReuseWorkers = 2048;
 constexpr int kMinBlocks = 8;      // 16-key blocks per worker at least
 
 // int32 words of the step metadata for up to T tokens and P workers
 size_t meta_words(int T, int Hkv, int P) { return (size_t)T * (5 + 4 + 4 * (size_t)Hkv) + P; }
+
+int max_workers(const gdn_kv_desc& d) { return d.max_workers > 0 ? d.max_workers : kReuseWorkers; }
 
 struct Dev {
   int prev = -1;
@@ -86,6 +93,7 @@ struct gdn_kv {
   // the planned step
   int T = 0, NG = 0, P = 0;
   int64_t W = 0;
+  bool stream_keys = false;
   bool planned = false;
 };
 
@@ -127,7 +135,7 @@ gdn_status gdn_kv_create(const gdn_kv_desc* desc, gdn_kv** out) {
   Dev dev(d.device);
   gdn_kv* kv = new gdn_kv;
   kv->d = d;
-  if (kv->d.max_workers == 0) kv->d.max_workers = kMaxWorkers;
+
   const size_t page_bytes = (size_t)2 * d.num_kv_heads * kPageTokens * kHeadDim * 2;
   bool ok = true;
   for (int l = 0; l < d.num_layers && ok; ++l) {
@@ -135,7 +143,7 @@ gdn_status gdn_kv_create(const gdn_kv_desc* desc, gdn_kv** out) {
     ok = hipMalloc(&p, page_bytes * d.num_pages) == hipSuccess;
     kv->pages.push_back(p);
   }
-  const size_t mwords = meta_words(d.max_step_tokens, d.num_kv_heads, kv->d.max_workers);
+  const size_t mwords = meta_words(d.max_step_tokens, d.num_kv_heads, max_workers(d));
   ok = ok && hipMalloc(&kv->ptab, sizeof(int32_t) * d.num_slots * d.max_pages_per_slot) == hipSuccess &&
        hipMalloc(&kv->d_meta, sizeof(int32_t) * mwords) == hipSuccess &&
        hipHostMalloc(&kv->p_meta, sizeof(int32_t) * mwords, 0) == hipSuccess &&
@@ -245,7 +253,14 @@ gdn_status gdn_kv_step(gdn_kv* kv, int32_t n, const int32_t* slots, const int32_
   }
   const int64_t W = sf0[NS];
   if (W > INT32_MAX) return kfail(GDN_ERR_INVALID, "gdn_kv_step: %lld key blocks", (long long)W);
-  const int P = (int)std::min<int64_t>(d.max_workers, (W + kMinBlocks - 1) / kMinBlocks);
+  // distinct blocks: each sequence's keys once per kv head (its last group's)
+  int64_t distinct = 0;
+  for (int gi = 0; gi < NG; ++gi)
+    if (gi + 1 == NG || groups[gi + 1].slot != groups[gi].slot)
+      distinct += ((int64_t)groups[gi].pos0 + groups[gi].ntok + 15) / 16 * Hkv;
+  const bool stream_keys = W < 2 * distinct;
+  const int pmax = d.max_workers > 0 ? d.max_workers : (stream_keys ? kStreamWorkers : kReuseWorkers);
+  const int P = (int)std::min<int64_t>(pmax, (W + kMinBlocks - 1) / kMinBlocks);
   // worker w owns flat blocks [a(w), a(w + 1)), a(w) = w W / P
   auto a = [&](int64_t w) { return w * W / P; };
   std::vector<int32_t> seg_wf(NS), seg_np(NS), seg_pb(NS), wseg(P);
@@ -336,6 +351,7 @@ gdn_status gdn_kv_step(gdn_kv* kv, int32_t n, const int32_t* slots, const int32_
   kv->NG = NG;
   kv->P = P;
   kv->W = W;
+  kv->stream_keys = stream_keys;
   kv->planned = true;
   return GDN_OK;
 }
@@ -366,6 +382,7 @@ gdn_status gdn_attn_forward(gdn_kv* kv, int32_t layer, const uint16_t* q_full, i
   a.Hkv = d.num_kv_heads;
   a.P = kv->P;
   a.W = kv->W;
+  a.stream_keys = kv->stream_keys;
   a.max_pages = d.max_pages_per_slot;
   a.rot_dim = rotary_dim;
   a.eps = norm_eps;
