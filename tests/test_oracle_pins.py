@@ -597,3 +597,30 @@ def test_attention_step_closed_forms_and_causality():
     k2[-1] ^= 0x0100
     ob2, _, _ = O.attention_step(q, k2, v, qw, kw, eps, theta, rot, empty, empty, Hq, Hkv)
     assert np.array_equal(ob2[:-1], ob[:-1]) and not np.array_equal(ob2[-1], ob[-1])
+
+
+def test_attention_step_score_scale_and_softmax():
+    """Scores are q.k / sqrt(256) under a softmax: with cached keys k1 =
+    q_hat / 8 (q_hat the token's normed, rotated query, bf16) and k2 = 0, and
+    a zero new key (its norm is 0), the weights are e^s, 1, 1 over e^s + 2
+    with s = |q_hat|^2 / 128. A scale of 1 or 1/256 fails it."""
+    rng = np.random.default_rng(74)
+    Hq = Hkv = 1
+    hd, eps, theta, rot = 256, 1e-6, 1.0e7, 64
+    q, _, v, qw, kw = _attn_inputs(rng, 1, Hq, Hkv)
+    kzero = O.f32_to_bf16(np.zeros((1, hd), np.float32))
+    qn = O.rms_norm_w(q.reshape(1, 2, hd)[:, 0], qw, eps)
+    qhat = O.bf16_to_f32(O.f64_to_bf16_array(O.rope_half_f64(qn, 2, rot, theta))).astype(np.float64)
+    k1 = O.f64_to_bf16_array(qhat / 8.0)                      # exact: a power-of-two scale
+    ck = np.stack([k1[0], O.f32_to_bf16(np.zeros(hd, np.float32))])[None]  # [1, 2, hd]
+    cv = O.f32_to_bf16(rng.standard_normal((1, 2, hd)).astype(np.float32))
+    out, _, _ = O.attention_step(q, kzero, v, qw, kw, eps, theta, rot, ck, cv, Hq, Hkv)
+    s = float(np.sum(qhat ** 2)) / 128.0
+    assert 1.0 < s < 4.0                                     # weights well inside (0, 1)
+    vals = np.concatenate([O.bf16_to_f32(cv[0]).astype(np.float64),
+                           O.bf16_to_f32(v.reshape(1, hd)).astype(np.float64)])
+    w = np.array([np.exp(s), 1.0, 1.0]) / (np.exp(s) + 2.0)
+    o = O.bf16_to_f32(O.f64_to_bf16_array(w @ vals)).astype(np.float64)
+    gate = O.bf16_to_f32(q.reshape(1, 2, hd)[:, 1]).astype(np.float64)
+    sg = O.bf16_to_f32(O.f64_to_bf16_array(1 / (1 + np.exp(-gate))))
+    assert np.array_equal(out, O.f64_to_bf16_array(o * sg))
