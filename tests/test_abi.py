@@ -117,3 +117,40 @@ def test_layer_and_executor_entries_reject_null_on_host():
     assert lib.gdn_exec_release(None, 1) == E
     assert lib.gdn_exec_max_batch_size(None) == 0
     assert lib.gdn_exec_supports_pipeline(None) == 0
+
+
+def test_kv_entries_reject_bad_arguments_on_host():
+    """The paged-KV entries check handles and descriptors before touching a
+    device: unsupported head dim or query-head ratio, bad worker limits, NULL
+    handles."""
+    lib = gdn_amd.load()
+    h = ctypes.c_void_p()
+    E = gdn_amd.GDN_ERR_INVALID
+    assert lib.gdn_kv_create(None, ctypes.byref(h)) == E
+
+    def desc(**kw):
+        f = dict(num_layers=1, num_slots=2, num_pages=4, max_pages_per_slot=2, num_q_heads=16,
+                 num_kv_heads=2, head_dim=256, max_step_tokens=8, device=0, max_workers=0)
+        f.update(kw)
+        return gdn_amd.KVDesc(**f)
+
+    for bad, code in ((dict(head_dim=128), gdn_amd.GDN_ERR_UNSUPPORTED),
+                      (dict(num_q_heads=6), gdn_amd.GDN_ERR_UNSUPPORTED),
+                      (dict(num_q_heads=32), gdn_amd.GDN_ERR_UNSUPPORTED),
+                      (dict(num_pages=0), E), (dict(max_step_tokens=0), E),
+                      (dict(max_workers=-1), E), (dict(max_workers=1 << 20), E)):
+        d = desc(**bad)
+        assert lib.gdn_kv_create(ctypes.byref(d), ctypes.byref(h)) == code, bad
+        assert h.value is None
+    assert lib.gdn_kv_destroy(None) == gdn_amd.GDN_OK
+    one = (ctypes.c_int32 * 1)(1)
+    n64 = ctypes.c_int64()
+    n32 = ctypes.c_int32()
+    assert lib.gdn_kv_release(None, 0) == E
+    assert lib.gdn_kv_length(None, 0, ctypes.byref(n64)) == E
+    assert lib.gdn_kv_free_pages(None, ctypes.byref(n32)) == E
+    assert lib.gdn_kv_step(None, 1, one, one, None) == E
+    assert lib.gdn_attn_forward(None, 0, None, 0, None, 0, None, 0, None, None,
+                                ctypes.c_float(1e-6), ctypes.c_float(1e7), 64, None, 0,
+                                None) == E
+    assert lib.gdn_kv_read(None, 0, 0, None, None, None) == E
