@@ -106,6 +106,8 @@ const char* gdn_version(void);
  * state and [num_slots,K-1,D] bf16 conv state (both start at +0.0). */
 gdn_status gdn_pool_create(const gdn_pool_desc* desc, gdn_pool** out);
 gdn_status gdn_pool_destroy(gdn_pool* pool);
+/* The pool's descriptor as created. */
+gdn_status gdn_pool_describe(const gdn_pool* pool, gdn_pool_desc* desc);
 
 /* Device pointers of one layer's state arrays (for inspection / export). */
 gdn_status gdn_pool_layer_state(gdn_pool* pool, int32_t layer, float** state,
@@ -333,13 +335,15 @@ gdn_status gdn_layer_prefill(gdn_layer* layer, const int32_t* slot_ids,
  * dropped), submit / collect pipeline one batch against the host
  * (mlx_executor.rs:195-254 as driven by qwen_mlx_serve.rs:110-177).
  *
- * The model the executor runs is the GDN half of the Qwen3.5 decoder stack:
- *   h = embed[token]; per layer l: h = h + layer_l(rms_norm(h, input_norm_w[l]));
+ * The model the executor runs is the Qwen3.5 decoder stack without its MLPs:
+ *   h = embed[token]; per layer l: h = h + mixer_l(rms_norm(h, input_norm_w[l]));
  *   token = argmax(lm_head(rms_norm(h, final_norm_w)))
- * (Qwen35Model::forward, qwen3_5.rs:826-880, over its GatedDeltaNet decoder
- * layers, DecoderLayer::forward_with_cache :723-743 without the MLP half).
- * Attention layers, MoE MLPs and temperature sampling are outside this
- * library; the greedy pick keeps runs reproducible.
+ * (Qwen35Model::forward, qwen3_5.rs:826-880; DecoderLayer::forward_with_cache
+ * :723-743 without the MLP half). A mixer is a GatedDeltaNet layer or, at the
+ * positions attn_layers name, an attention layer (qwen3_5.rs:377-455: merged
+ * q|k|v projection, gdn_attn_forward on the executor's gdn_kv, o_proj). The
+ * KV cache uses the pool's slot ids. MoE MLPs and temperature sampling are
+ * outside this library; the greedy pick keeps runs reproducible.
  *
  * One thread owns an executor (qwen_mlx_serve.rs:96-99). All its device work
  * runs on the stream given at creation, in call order. Sequence ids are the
@@ -347,12 +351,24 @@ gdn_status gdn_layer_prefill(gdn_layer* layer, const int32_t* slot_ids,
  * vocabulary on the host.
  * ------------------------------------------------------------------------ */
 typedef struct gdn_exec gdn_exec;
+typedef struct gdn_kv gdn_kv;
+
+/* One attention layer of the stack (Qwen35Attention, qwen3_5.rs:377-455). */
+typedef struct gdn_exec_attn_layer {
+  int32_t position;              /* index in the decoder stack                      */
+  const gdn_qlinear* qkv_proj;   /* hidden -> Hq*512 + 2*Hkv*256: per query head 256
+                                    query then 256 gate outputs, then k, then v   */
+  const gdn_qlinear* o_proj;     /* Hq*256 -> hidden                                */
+  const uint16_t* q_norm_w;      /* [256] bf16                                      */
+  const uint16_t* k_norm_w;      /* [256] bf16                                      */
+} gdn_exec_attn_layer;
 
 typedef struct gdn_exec_desc {
   gdn_pool* pool;                       /* every sequence's GDN state, one slot each     */
   int32_t num_layers;
   gdn_layer* const* layers;             /* the GDN layers in model order (on `pool`)     */
-  const uint16_t* const* input_norm_w;  /* per layer [hidden] bf16 input_layernorm       */
+  const uint16_t* const* input_norm_w;  /* per decoder layer, GDN and attention, in stack
+                                           order: [hidden] bf16 input_layernorm         */
   const uint16_t* final_norm_w;         /* [hidden] bf16                                 */
   float rms_eps;
   const uint16_t* embed;                /* [vocab, hidden] bf16, 16-byte aligned         */
@@ -360,6 +376,14 @@ typedef struct gdn_exec_desc {
   int32_t max_batch;                    /* decode batch bound (max_batch_size)           */
   int32_t max_prompt;                   /* longest prompt one prefill takes              */
   int32_t device;                       /* HIP device of the pool and weights            */
+  /* attention layers: num_attn_layers = 0 for a GDN-only stack */
+  int32_t num_attn_layers;
+  const gdn_exec_attn_layer* attn_layers; /* increasing positions; attention layer i uses
+                                           kv layer i                                  */
+  gdn_kv* kv;                           /* num_slots >= the pool's, max_step_tokens >=
+                                           max(max_batch, max_prompt)                   */
+  float rope_theta;
+  int32_t rotary_dim;
 } gdn_exec_desc;
 
 /* Allocates the executor's buffers (activations for max(max_batch,
@@ -441,8 +465,6 @@ gdn_status gdn_exec_logits(const gdn_exec* exec, const uint16_t** logits, int32_
  * ulp (the step's key blocks are split evenly over the workers, so a token's
  * partial sums depend on the whole step).
  * ------------------------------------------------------------------------ */
-typedef struct gdn_kv gdn_kv;
-
 typedef struct gdn_kv_desc {
   int32_t num_layers;          /* attention layers                               */
   int32_t num_slots;           /* sequences the cache can hold                   */
@@ -463,6 +485,8 @@ typedef struct gdn_kv_desc {
  * and staging for max_step_tokens tokens. */
 gdn_status gdn_kv_create(const gdn_kv_desc* desc, gdn_kv** out);
 gdn_status gdn_kv_destroy(gdn_kv* kv);
+/* The cache's descriptor as created (max_workers as given). */
+gdn_status gdn_kv_describe(const gdn_kv* kv, gdn_kv_desc* desc);
 
 /* A sequence leaves (or starts over): its pages go back to the free list. */
 gdn_status gdn_kv_release(gdn_kv* kv, int32_t slot);

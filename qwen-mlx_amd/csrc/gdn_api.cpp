@@ -111,6 +111,12 @@ const char* gdn_last_error(void) { return g_err.c_str(); }
 
 const char* gdn_version(void) { return "gdn 0.1 gfx950"; }
 
+gdn_status gdn_pool_describe(const gdn_pool* pool, gdn_pool_desc* desc) {
+  if (!pool || !desc) return fail(GDN_ERR_INVALID, "gdn_pool_describe: NULL argument");
+  *desc = pool->d;
+  return GDN_OK;
+}
+
 gdn_status gdn_pool_create(const gdn_pool_desc* desc, gdn_pool** out) {
   if (!desc || !out) return fail(GDN_ERR_INVALID, "desc/out is NULL");
   *out = nullptr;

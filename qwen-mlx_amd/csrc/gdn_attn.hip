@@ -23,10 +23,10 @@
 // Page layout. A page holds 64 positions of one layer: [2 (K, V)][Hkv][16384]
 // bf16, each 16384-element tile stored in the order the MFMA operands are
 // loaded, so that every load instruction of a wave reads 1 KiB (K) or 512 B
-// (V) of contiguous memory:
-//   K (key kk, dim d): [kk/16][d/32][(d/8)%4][kk%16][d%8]   -- A operand of
+// (V) of contiguous memory (s = (kk/16) XOR (page % 4), the block's slot):
+//   K (key kk, dim d): [s][d/32][(d/8)%4][kk%16][d%8]   -- A operand of
 //       v_mfma_f32_16x16x32_bf16, rows = 16 keys, 32-deep k = dims
-//   V (key kk, dim d): [kk/16][d/16][(kk/4)%4][d%16][kk%4]  -- A operand of
+//   V (key kk, dim d): [s][d/16][(kk/4)%4][d%16][kk%4]  -- A operand of
 //       v_mfma_f32_16x16x16_bf16, rows = 16 dims, 16-deep k = keys
 #include "gdn_common.h"
 
@@ -38,6 +38,8 @@ constexpr int kHd = 256;            // head dim = threads of the prep / combine 
 constexpr int kPage = 64;           // tokens per KV page
 constexpr int kTile = kPage * kHd;  // elements of one page's K (or V) tile of one kv head
 constexpr int kPartLd = 4 + kHd;    // partial row: m, l, 2 pad, 256 outputs (f32)
+constexpr int kChunkBlocks = 24;    // 16-key blocks per chunk (384 keys, even): one partial each
+static_assert(kChunkBlocks % 2 == 0, "chunks end after the second block of a pair");
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -45,11 +47,17 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ int k_off(int kk, int d) {
-  return ((((kk >> 4) * 8 + (d >> 5)) * 4 + ((d >> 3) & 3)) * 16 + (kk & 15)) * 8 + (d & 7);
+// Slot of 16-key block b in page `page`: the four blocks' 8 KiB slots are
+// XOR-swizzled by the page id, so that workers which start at the same block
+// of different pages (and move in step) read different slots.
+__device__ __forceinline__ int block_slot(int b, int page) { return b ^ (page & 3); }
+__device__ __forceinline__ int k_off(int kk, int d, int page) {
+  return (((block_slot(kk >> 4, page) * 8 + (d >> 5)) * 4 + ((d >> 3) & 3)) * 16 + (kk & 15)) * 8 +
+         (d & 7);
 }
-__device__ __forceinline__ int v_off(int kk, int d) {
-  return ((((kk >> 4) * 16 + (d >> 4)) * 4 + ((kk >> 2) & 3)) * 16 + (d & 15)) * 4 + (kk & 3);
+__device__ __forceinline__ int v_off(int kk, int d, int page) {
+  return (((block_slot(kk >> 4, page) * 16 + (d >> 4)) * 4 + ((kk >> 2) & 3)) * 16 + (d & 15)) * 4 +
+         (kk & 3);
 }
 
 // Block-wide f32 sum over 256 threads (every thread gets the result).
@@ -124,17 +132,21 @@ __global__ __launch_bounds__(kHd) void attn_prep_kernel(
   } else {
     const int kk = pos & (kPage - 1);
     const size_t tile = ((size_t)page * 2 * Hkv + j) * kTile;
-    pages[tile + k_off(kk, d)] = yb;  // K
-    pages[tile + (size_t)Hkv * kTile + v_off(kk, d)] = v[(size_t)t * vs + (size_t)j * kHd + d];
+    pages[tile + k_off(kk, d, page)] = yb;  // K
+    pages[tile + (size_t)Hkv * kTile + v_off(kk, d, page)] =
+        v[(size_t)t * vs + (size_t)j * kHd + d];
     if (j == 0 && d == 0 && kk == 0) ptab[(size_t)slot * max_pages + pos / kPage] = page;
   }
 }
 
-// One wave per work-group; work-group w is worker w of P. The flat list of
-// work is every (token group, kv head) segment's 16-key blocks in order
-// (segment s = group * Hkv + j); worker w takes blocks [w W / P, (w+1) W / P)
-// of the W in total, which may span several segments: each maximal run of
-// one segment's blocks is a piece and writes one partial.
+// One wave per work-group; work-group w is worker w of P. The work is every
+// (token group, kv head) segment's keys (segment s = group * Hkv + j) cut at
+// fixed points into chunks of kChunkBlocks 16-key blocks; the flat list of
+// all chunks, in segment order, goes to the workers in equal runs of k
+// (worker w: chunks [w k, (w+1) k)), which may span several segments. Every
+// chunk writes its own partial, so a token's result depends only on its own
+// keys: the same in any batch, and when a prompt's tokens are grouped
+// differently.
 //
 // A token group is up to 16/G consecutive tokens of one sequence: the 16
 // columns of the MFMA tiles are (token, query head) pairs, column c = token
@@ -146,43 +158,45 @@ __global__ __launch_bounds__(kHd) void attn_prep_kernel(
 //     accumulators only when some column's running max grows);
 //   O^T (256 dims x 16 columns) += V^T_blk . P^T: three 16-deep MFMAs per
 //     16 dims, against P split into bf16 hi, mid and lo parts (together P's
-//     24 significant bits: the products are those of float32 P). The score accumulator of lane l holds keys 4 (l/16) .. +3 of
-//     column l%16: the B operand layout as it is. (The O accumulators only
+////     24 significant bits: the products are those of float32 P). The score
+//     accumulator of lane l holds keys 4 (l/16) .. +3 of column l%16: the B
+//     operand layout as it is. (The O accumulators only
 //     ever see the 16-deep opcode and the score accumulator only the 32-deep
 //     one.)
-// The next block's K and V are loaded while the current one computes. V of
-// keys past the group's last position is zeroed before use (those rows of a
-// page may hold anything).
+// The next block's K and V are loaded while the current one computes, across
+// chunk boundaries within a segment. V of keys past the group's last
+// position is zeroed before use (those rows of a page may hold anything).
 //
 // Schedule tables (int32, built by the host for the step):
 //   grp[NG][4]  first token, tokens, first position, sequence slot
-//   seg[NS][4]  first flat block, first partial, first worker, partials
-//   wseg[P]     segment of the worker's first block
-// Partials [pieces][16][kPartLd] f32: running max (log2 domain), sum, output.
+//   seg[NS][4]  first chunk (= its partial), chunks, -, -
+//   wseg[P]     segment of the worker's first chunk
+// Partials [chunks][16][kPartLd] f32: running max (log2 domain), sum, output.
 template <int G, bool STREAM>
 __global__ __launch_bounds__(64, 2) void attn_block_kernel(
     const uint16_t* __restrict__ q_rot, int Hq, int Hkv, const int32_t* __restrict__ grp,
-    const int32_t* __restrict__ seg, const int32_t* __restrict__ wseg, int64_t W, int P,
+    const int32_t* __restrict__ seg, const int32_t* __restrict__ wseg, int NC, int k,
     const int32_t* __restrict__ ptab, int max_pages, const uint16_t* __restrict__ pages,
     float scale_log2, float* __restrict__ part) {
   static_assert(16 % G == 0, "whole tokens per 16 columns");
   __shared__ u32x4 qlds[8][64];  // this wave's Q^T operand
   const int w = blockIdx.x, lane = threadIdx.x;
   const int g4 = lane >> 4, c = lane & 15;
-  const int64_t fw1 = (int64_t)(w + 1) * W / P;
-  int64_t f = (int64_t)w * W / P;
+  const int gw1 = min(NC, (w + 1) * k);
+  int g = w * k;  // next chunk
   int s = wseg[w];
   const size_t page_stride = (size_t)2 * Hkv * kTile;
   const size_t v_shift = (size_t)Hkv * kTile;
-  while (f < fw1) {
+  while (g < gw1) {
     const int gi = s / Hkv, j = s - gi * Hkv;
     const int t0 = grp[4 * gi], ntok = grp[4 * gi + 1], pos0 = grp[4 * gi + 2],
               slot = grp[4 * gi + 3];
-    const int64_t sf0 = seg[4 * s];
+    const int cs0 = seg[4 * s], nch = seg[4 * s + 1];
     const int nkeys = pos0 + ntok;  // the group's last position + 1
     const int nblk = (nkeys + 15) >> 4;
-    const int kb0 = (int)(f - sf0);
-    const int kb1 = (int)min((int64_t)nblk, fw1 - sf0);
+    const int gend = min(gw1, cs0 + nch);  // this worker's chunks of the segment: [g, gend)
+    const int kb0 = (g - cs0) * kChunkBlocks;
+    const int kb1 = min(nblk, (gend - cs0) * kChunkBlocks);
     const int ctok = c / G;
     const bool cvalid = ctok < ntok;
     const int cpos = cvalid ? pos0 + ctok : -1;  // keys <= cpos are attended
@@ -216,7 +230,8 @@ __global__ __launch_bounds__(64, 2) void attn_block_kernel(
         pid = pbase + lane < npages ? prow[pbase + lane] : 0;
       }
       const int page = __builtin_amdgcn_readlane(pid, idx);
-      const uint16_t* kt = kv_head + (size_t)page * page_stride + (size_t)(kb & 3) * 4096;
+      const uint16_t* kt =
+          kv_head + (size_t)page * page_stride + (size_t)block_slot(kb & 3, page) * 4096;
       // STREAM (each block read about once in the step): non-temporal loads
       // stream past the caches; otherwise plain loads keep the blocks that
       // later token groups of the same prompt read again
@@ -289,32 +304,42 @@ __global__ __launch_bounds__(64, 2) void attn_block_kernel(
       }
     };
 
+    // the partial of the chunk that block kb ends, then a fresh state
+    auto flush = [&](int kb) {
+      const float l4 = lsum + __shfl_xor(lsum, 16, 64);
+      const float lt = l4 + __shfl_xor(l4, 32, 64);
+      if (cvalid) {
+        float* pr = part + ((size_t)(cs0 + kb / kChunkBlocks) * 16 + c) * kPartLd;
+        if (g4 == 0) {
+          pr[0] = m;
+          pr[1] = lt;
+        }
+#pragma unroll
+        for (int db = 0; db < 16; ++db)
+          *reinterpret_cast<float4*>(pr + 4 + 16 * db + 4 * g4) =
+              make_float4(O[db][0], O[db][1], O[db][2], O[db][3]);
+      }
+      m = -INFINITY;
+      lsum = 0.f;
+#pragma unroll
+      for (int db = 0; db < 16; ++db) O[db] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    };
+
     uint4 kA[8], kB[8];
     uint2 vA[16], vB[16];
     load(kb0, kA, vA);
+    // kb0 and the chunk size are even, so a chunk ends inside the range only
+    // after the second block of a pair; the range's own end is flushed after
     for (int kb = kb0; kb < kb1; kb += 2) {
       if (kb + 1 < kb1) load(kb + 1, kB, vB);
       compute(kb, kA, vA);
       if (kb + 1 >= kb1) break;
       if (kb + 2 < kb1) load(kb + 2, kA, vA);
       compute(kb + 1, kB, vB);
+      if ((kb + 2) % kChunkBlocks == 0 && kb + 2 < kb1) flush(kb + 1);
     }
-
-    lsum += __shfl_xor(lsum, 16, 64);
-    lsum += __shfl_xor(lsum, 32, 64);
-    const int piece = seg[4 * s + 1] + (w - seg[4 * s + 2]);
-    if (cvalid) {
-      float* pr = part + ((size_t)piece * 16 + c) * kPartLd;
-      if (g4 == 0) {
-        pr[0] = m;
-        pr[1] = lsum;
-      }
-#pragma unroll
-      for (int db = 0; db < 16; ++db)
-        *reinterpret_cast<float4*>(pr + 4 + 16 * db + 4 * g4) =
-            make_float4(O[db][0], O[db][1], O[db][2], O[db][3]);
-    }
-    f = sf0 + kb1;
+    flush(kb1 - 1);
+    g = gend;
     ++s;
   }
 }
@@ -337,7 +362,7 @@ __global__ __launch_bounds__(kHd) void attn_combine_kernel(
   const int t = blockIdx.x, hq = blockIdx.y, tid = threadIdx.x;
   const int j = hq / G, g = hq - j * G;
   const int s = tokseg[t] * Hkv + j;
-  const int p0 = seg[4 * s + 1], np = seg[4 * s + 3];
+  const int p0 = seg[4 * s], np = seg[4 * s + 1];
   const float* pc = part + ((size_t)p0 * 16 + tokseg[T + t] + g) * kPartLd;
   constexpr size_t kStride = (size_t)16 * kPartLd;  // consecutive pieces
   float mx = -INFINITY;
@@ -389,19 +414,22 @@ __global__ __launch_bounds__(kHd) void kv_gather_kernel(const uint16_t* __restri
   const int p = blockIdx.x, j = blockIdx.y, isv = blockIdx.z, d = threadIdx.x;
   uint16_t* dst = isv ? v_out : k_out;
   if (!dst) return;
-  const uint16_t* tile = pages + ((size_t)prow[p] * 2 * Hkv + (size_t)isv * Hkv + j) * kTile;
+  const int page = prow[p];
+  const uint16_t* tile = pages + ((size_t)page * 2 * Hkv + (size_t)isv * Hkv + j) * kTile;
   for (int kk = 0; kk < kPage; ++kk) {
     const int64_t pos = (int64_t)p * kPage + kk;
     if (pos >= len) break;
-    dst[((size_t)j * len + pos) * kHd + d] = tile[isv ? v_off(kk, d) : k_off(kk, d)];
+    dst[((size_t)j * len + pos) * kHd + d] = tile[isv ? v_off(kk, d, page) : k_off(kk, d, page)];
   }
 }
 
 size_t attn_part_offset(int T, int Hq) { return ((size_t)T * Hq * kHd * 2 + 255) & ~(size_t)255; }
 
-size_t attn_workspace_bytes(int T, int Hq, int64_t pieces) {
-  return attn_part_offset(T, Hq) + (size_t)pieces * 16 * kPartLd * sizeof(float);
+size_t attn_workspace_bytes(int T, int Hq, int64_t chunks) {
+  return attn_part_offset(T, Hq) + (size_t)chunks * 16 * kPartLd * sizeof(float);
 }
+
+int attn_chunk_blocks() { return kChunkBlocks; }
 
 hipError_t launch_attn(const AttnArgs& a) {
   if (a.T <= 0) return hipSuccess;
@@ -417,7 +445,7 @@ hipError_t launch_attn(const AttnArgs& a) {
   const float scale_log2 = 1.4426950408889634f / sqrtf((float)kHd);  // log2(e) / sqrt(256)
   auto blocks = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3(a.P), dim3(64), 0, a.stream, q_rot, a.Hq, a.Hkv, a.grp, a.seg,
-                       a.wseg, a.W, a.P, a.ptab, a.max_pages, a.pages, scale_log2, part);
+                       a.wseg, a.NC, a.kpw, a.ptab, a.max_pages, a.pages, scale_log2, part);
   };
   if (G == 8) {
     if (a.stream_keys)

@@ -234,7 +234,7 @@ hipError_t launch_prefill(const PrefillArgs& a);
 // Attention step on the paged KV cache (gdn_attn.hip).
 struct AttnArgs {
   int T, Hq, Hkv, P, max_pages, rot_dim;
-  int64_t W;               // 16-key blocks of work in the step
+  int NC, kpw;             // chunks of work in the step, chunks per worker
   bool stream_keys;        // each block read about once (non-temporal loads)
   float eps, log2_base;
   const uint16_t* q_full;  // [T, qs]: per query head 256 query then 256 gate values
@@ -248,16 +248,17 @@ struct AttnArgs {
   const int32_t* meta;     // [3][T]: slot, position, page of each token
   const int32_t* tokseg;   // [2][T]: token group, first column in the group
   const int32_t* grp;      // [groups][4]: first token, tokens, first position, slot
-  const int32_t* seg;      // [groups * Hkv][4]: first block, first partial, first worker, partials
-  const int32_t* wseg;     // [P]: segment of each worker's first block
+  const int32_t* seg;      // [groups * Hkv][4]: first chunk, chunks, -, -
+  const int32_t* wseg;     // [P]: segment of each worker's first chunk
   int32_t* ptab;           // [num_slots][max_pages] page table
   uint16_t* pages;         // this layer's pages [num_pages][2][Hkv][16384]
   uint16_t* out;           // [T, os]: Hq x 256 gated attention rows
   int64_t os;
-  void* workspace;         // attn_workspace_bytes(T, Hq, pieces)
+  void* workspace;         // attn_workspace_bytes(T, Hq, NC)
   hipStream_t stream;
 };
-size_t attn_workspace_bytes(int T, int Hq, int64_t pieces);
+size_t attn_workspace_bytes(int T, int Hq, int64_t chunks);
+int attn_chunk_blocks();  // 16-key blocks per chunk
 hipError_t launch_attn(const AttnArgs& a);
 // A sequence's cached rows of one layer into [Hkv][len][256] K and V arrays.
 hipError_t launch_kv_gather(const uint16_t* pages, const int32_t* prow, int Hkv, int64_t len,

@@ -1,17 +1,20 @@
 // gdn_exec.cpp -- the executor: ModelExecutor (src/scheduler/executor.rs:21-49)
 // over pool slots, written against the public C ABI of the layers it drives
-// (gdn_layer_*, gdn_qlinear_*, gdn_slot_*), the way a host-language executor
-// would bind it.
+// (gdn_layer_*, gdn_qlinear_*, gdn_slot_*, gdn_kv_*, gdn_attn_forward), the
+// way a host-language executor would bind it.
 //
 // Per sequence the reference keeps Qwen35State { caches: Vec<(conv, state)> }
 // (mlx_executor.rs:19-21) and copies every active sequence's caches into a
 // batch and back on every step (stack_caches / unstack_caches, :92-130).
 // Here a sequence is one slot id, the same in every layer: a decode step
 // stages B (slot, token) pairs, and the layers read and write the slots in
-// place. Device work of a step, in stream order:
-//   H2D of the (slot, token) block -> embedding rows -> per layer: residual
-//   add + rms-norm, gdn_layer_decode -> final add + norm -> lm_head -> argmax
-//   -> D2H of the B picked tokens, then an event that collect waits for.
+// place; the attention layers' KV cache (when the stack has attention layers)
+// is keyed by the same slot ids and planned once per step (gdn_kv_step).
+// Device work of a step, in stream order:
+//   H2D of the (slot, token) block -> embedding rows -> per decoder layer:
+//   residual add + rms-norm, then gdn_layer_decode (GDN) or q|k|v projection,
+//   gdn_attn_forward and o_proj (attention) -> final add + norm -> lm_head ->
+//   argmax -> D2H of the B picked tokens, then an event that collect waits for.
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -53,9 +56,21 @@ gdn_status hfail(hipError_t e, const char* what) {
 }  // namespace
 
 struct gdn_exec {
+  struct Attn {
+    const gdn_qlinear* qkv;
+    const gdn_qlinear* o;
+    const uint16_t* q_norm_w;
+    const uint16_t* k_norm_w;
+  };
   gdn_pool* pool = nullptr;
   std::vector<gdn_layer*> layers;
-  std::vector<const uint16_t*> norm_w;
+  std::vector<Attn> attn;
+  // decoder stack: entry >= 0 is GDN layer entry, < 0 attention layer -entry - 1
+  std::vector<int> stack;
+  std::vector<const uint16_t*> norm_w;  // per stack position
+  gdn_kv* kv = nullptr;
+  float rope_theta = 0.f;
+  int rotary_dim = 0, Hq = 0, Hkv = 0, nqkv = 0;
   const uint16_t* final_norm_w = nullptr;
   float eps = 0.f;
   const uint16_t* embed = nullptr;
@@ -73,6 +88,8 @@ struct gdn_exec {
   uint16_t* hn = nullptr;     // normed rows fed to a layer
   uint16_t* mix = nullptr;    // layer output rows
   uint16_t* logits = nullptr; // [max_batch, vocab]
+  uint16_t* qkv = nullptr;    // attention q|gate, k, v rows [rows, nqkv]
+  uint16_t* att = nullptr;    // gated attention rows [rows, Hq * 256]
   float* d_pv = nullptr;      // greedy-pick partials [max_batch, argmax_chunks(vocab)]
   int* d_pi = nullptr;
   // pinned host staging (one region per direction and kind, so a prefill
@@ -81,6 +98,7 @@ struct gdn_exec {
   int32_t* p_pre = nullptr;
   int32_t* p_next = nullptr;   // a batch's picked tokens
   int32_t* p_first = nullptr;  // a prefill's first tokens [max_batch]
+  std::vector<int32_t> ones;   // ntok = 1 per decode sequence
   std::unordered_map<uint64_t, int32_t> slot_of;
   bool inflight = false;
   int32_t inflight_B = 0;
@@ -93,13 +111,17 @@ void exec_release(gdn_exec* x) {
   if (!x) return;
   if (x->stream) (void)hipStreamSynchronize(x->stream);
   for (void* p : {(void*)x->d_dec, (void*)x->d_pre, (void*)x->d_next, (void*)x->h, (void*)x->hn,
-                  (void*)x->mix, (void*)x->logits, (void*)x->d_pv, (void*)x->d_pi})
+                  (void*)x->mix, (void*)x->logits, (void*)x->d_pv, (void*)x->d_pi, (void*)x->qkv,
+                  (void*)x->att})
     if (p) (void)hipFree(p);
   for (void* p : {(void*)x->p_dec, (void*)x->p_pre, (void*)x->p_next, (void*)x->p_first})
     if (p) (void)hipHostFree(p);
   if (x->done) (void)hipEventDestroy(x->done);
   if (x->pre_copied) (void)hipEventDestroy(x->pre_copied);
-  for (auto& kv : x->slot_of) (void)gdn_slot_free(x->pool, kv.second);
+  for (auto& sv : x->slot_of) {
+    (void)gdn_slot_free(x->pool, sv.second);
+    if (x->kv) (void)gdn_kv_release(x->kv, sv.second);
+  }
   delete x;
 }
 
@@ -122,20 +144,32 @@ size_t pre_words(int max_batch, int max_prompt) {
   return 3 * (size_t)max_batch + 1 + (size_t)max_prompt;
 }
 
-// The model body over n rows of h that hold the embedded tokens: every GDN
-// layer with its residual seam. Prefill rows are nseq packed sequences.
+// The model body over n rows of h that hold the embedded tokens: every
+// decoder layer with its residual seam. Prefill rows are nseq packed
+// sequences. The KV step for these rows is planned before this runs.
 gdn_status run_layers(gdn_exec* x, int n, bool prefill, int nseq = 0) {
   const int32_t* slots = prefill ? x->d_pre : x->d_dec;
-  for (size_t l = 0; l < x->layers.size(); ++l) {
-    HIP_TRY(gdn::launch_add_norm(x->h, l == 0 ? nullptr : x->mix, n, x->hidden, x->norm_w[l],
+  const int qw = 2 * x->Hq * 256, kw = x->Hkv * 256;  // q|gate and k widths of a qkv row
+  for (size_t p = 0; p < x->stack.size(); ++p) {
+    HIP_TRY(gdn::launch_add_norm(x->h, p == 0 ? nullptr : x->mix, n, x->hidden, x->norm_w[p],
                                  x->eps, x->hn, x->stream),
             "residual add + norm");
-    if (prefill)
-      GDN_TRY(gdn_layer_prefill(x->layers[l], slots, x->d_pre + nseq, nseq, n, x->hn, x->hidden,
+    const int e = x->stack[p];
+    if (e < 0) {
+      const int ai = -e - 1;
+      const gdn_exec::Attn& a = x->attn[ai];
+      GDN_TRY(gdn_qlinear_forward(a.qkv, x->hn, x->hidden, n, x->qkv, x->nqkv, x->stream));
+      GDN_TRY(gdn_attn_forward(x->kv, ai, x->qkv, x->nqkv, x->qkv + qw, x->nqkv, x->qkv + qw + kw,
+                               x->nqkv, a.q_norm_w, a.k_norm_w, x->eps, x->rope_theta,
+                               x->rotary_dim, x->att, x->Hq * 256, x->stream));
+      GDN_TRY(gdn_qlinear_forward(a.o, x->att, x->Hq * 256, n, x->mix, x->hidden, x->stream));
+    } else if (prefill) {
+      GDN_TRY(gdn_layer_prefill(x->layers[e], slots, x->d_pre + nseq, nseq, n, x->hn, x->hidden,
                                 x->mix, x->hidden, x->stream));
-    else
-      GDN_TRY(gdn_layer_decode(x->layers[l], slots, n, x->hn, x->hidden, x->mix, x->hidden,
+    } else {
+      GDN_TRY(gdn_layer_decode(x->layers[e], slots, n, x->hn, x->hidden, x->mix, x->hidden,
                                x->stream));
+    }
   }
   return GDN_OK;
 }
@@ -144,7 +178,7 @@ gdn_status run_layers(gdn_exec* x, int n, bool prefill, int nseq = 0) {
 // layer's residual add), picked tokens into d_next and the pinned `dst`.
 gdn_status pick(gdn_exec* x, int r0, int n, int32_t* dst) {
   uint16_t* hr = x->h + (size_t)r0 * x->hidden;
-  const uint16_t* mr = x->layers.empty() ? nullptr : x->mix + (size_t)r0 * x->hidden;
+  const uint16_t* mr = x->stack.empty() ? nullptr : x->mix + (size_t)r0 * x->hidden;
   uint16_t* nr = x->hn + (size_t)r0 * x->hidden;
   HIP_TRY(gdn::launch_add_norm(hr, mr, n, x->hidden, x->final_norm_w, x->eps, nr, x->stream),
           "final norm");
@@ -167,11 +201,30 @@ gdn_status gdn_exec_create(const gdn_exec_desc* desc, void* stream, gdn_exec** o
   *out = nullptr;
   const gdn_exec_desc& d = *desc;
   if (!d.pool || !d.embed || !d.head || !d.final_norm_w || d.num_layers < 0 ||
-      (d.num_layers > 0 && (!d.layers || !d.input_norm_w)))
-    return efail(GDN_ERR_INVALID, "gdn_exec_create: NULL pool / embed / head / norm / layers");
+      d.num_attn_layers < 0 || (d.num_layers > 0 && !d.layers) ||
+      (d.num_layers + d.num_attn_layers > 0 && !d.input_norm_w) ||
+      (d.num_attn_layers > 0 && (!d.attn_layers || !d.kv)))
+    return efail(GDN_ERR_INVALID,
+                 "gdn_exec_create: NULL pool / embed / head / norm / layers / attention / kv");
+  const int depth = d.num_layers + d.num_attn_layers;
   for (int l = 0; l < d.num_layers; ++l)
-    if (!d.layers[l] || !d.input_norm_w[l])
-      return efail(GDN_ERR_INVALID, "gdn_exec_create: layer %d or its norm weight is NULL", l);
+    if (!d.layers[l]) return efail(GDN_ERR_INVALID, "gdn_exec_create: GDN layer %d is NULL", l);
+  for (int p = 0; p < depth; ++p)
+    if (!d.input_norm_w[p])
+      return efail(GDN_ERR_INVALID, "gdn_exec_create: norm weight of decoder layer %d is NULL", p);
+  std::vector<int> stack(depth, 0);
+  for (int i = 0; i < d.num_attn_layers; ++i) {
+    const gdn_exec_attn_layer& a = d.attn_layers[i];
+    if (a.position < 0 || a.position >= depth || (i > 0 && a.position <= d.attn_layers[i - 1].position))
+      return efail(GDN_ERR_INVALID,
+                   "gdn_exec_create: attention layer %d at position %d (increasing, < %d)", i,
+                   a.position, depth);
+    if (!a.qkv_proj || !a.o_proj || !a.q_norm_w || !a.k_norm_w)
+      return efail(GDN_ERR_INVALID, "gdn_exec_create: attention layer %d has a NULL weight", i);
+    stack[a.position] = -i - 1;
+  }
+  for (int p = 0, g = 0; p < depth; ++p)
+    if (stack[p] == 0) stack[p] = g++;  // attention positions hold negative entries
   if (d.max_batch < 1 || d.max_prompt < 1)
     return efail(GDN_ERR_INVALID, "gdn_exec_create: max_batch and max_prompt must be >= 1");
   if (!(d.rms_eps >= 0.0f)) return efail(GDN_ERR_INVALID, "gdn_exec_create: rms_eps < 0");
@@ -180,11 +233,52 @@ gdn_status gdn_exec_create(const gdn_exec_desc* desc, void* stream, gdn_exec** o
   int32_t hidden = 0, vocab = 0;
   GDN_TRY(gdn_qlinear_dims(d.head, &hidden, &vocab));
   if (hidden > 4096) return efail(GDN_ERR_UNSUPPORTED, "gdn_exec_create: hidden %d > 4096", hidden);
+  const int rows = d.max_batch > d.max_prompt ? d.max_batch : d.max_prompt;
+  int Hq = 0, Hkv = 0, nqkv = 0;
+  if (d.num_attn_layers > 0) {
+    gdn_kv_desc kd{};
+    gdn_pool_desc pd{};
+    GDN_TRY(gdn_kv_describe(d.kv, &kd));
+    GDN_TRY(gdn_pool_describe(d.pool, &pd));
+    if (kd.num_layers < d.num_attn_layers || kd.num_slots < pd.num_slots ||
+        kd.max_step_tokens < rows || kd.device != d.device)
+      return efail(GDN_ERR_INVALID,
+                   "gdn_exec_create: kv cache (%d layers, %d slots, %d step tokens, device %d) "
+                   "does not fit %d attention layers, %d slots, %d rows, device %d",
+                   kd.num_layers, kd.num_slots, kd.max_step_tokens, kd.device, d.num_attn_layers,
+                   pd.num_slots, rows, d.device);
+    if (d.rotary_dim < 0 || d.rotary_dim > 256 || d.rotary_dim % 2 != 0 || !(d.rope_theta > 0.0f))
+      return efail(GDN_ERR_INVALID, "gdn_exec_create: rotary_dim %d / rope_theta", d.rotary_dim);
+    Hq = kd.num_q_heads;
+    Hkv = kd.num_kv_heads;
+    nqkv = 2 * Hq * 256 + 2 * Hkv * 256;
+    for (int i = 0; i < d.num_attn_layers; ++i) {
+      int32_t k1 = 0, n1 = 0, k2 = 0, n2 = 0;
+      GDN_TRY(gdn_qlinear_dims(d.attn_layers[i].qkv_proj, &k1, &n1));
+      GDN_TRY(gdn_qlinear_dims(d.attn_layers[i].o_proj, &k2, &n2));
+      if (k1 != hidden || n1 != nqkv || k2 != Hq * 256 || n2 != hidden)
+        return efail(GDN_ERR_INVALID,
+                     "gdn_exec_create: attention layer %d projections %d->%d, %d->%d (want "
+                     "%d->%d, %d->%d)",
+                     i, k1, n1, k2, n2, hidden, nqkv, Hq * 256, hidden);
+    }
+  }
   DevScope dev(d.device);
   gdn_exec* x = new gdn_exec;
   x->pool = d.pool;
   x->layers.assign(d.layers, d.layers + d.num_layers);
-  x->norm_w.assign(d.input_norm_w, d.input_norm_w + d.num_layers);
+  x->norm_w.assign(d.input_norm_w, d.input_norm_w + depth);
+  x->stack = stack;
+  for (int i = 0; i < d.num_attn_layers; ++i)
+    x->attn.push_back({d.attn_layers[i].qkv_proj, d.attn_layers[i].o_proj,
+                       d.attn_layers[i].q_norm_w, d.attn_layers[i].k_norm_w});
+  x->kv = d.num_attn_layers > 0 ? d.kv : nullptr;
+  x->rope_theta = d.rope_theta;
+  x->rotary_dim = d.rotary_dim;
+  x->Hq = Hq;
+  x->Hkv = Hkv;
+  x->nqkv = nqkv;
+  x->ones.assign(d.max_batch, 1);
   x->final_norm_w = d.final_norm_w;
   x->eps = d.rms_eps;
   x->embed = d.embed;
@@ -193,7 +287,7 @@ gdn_status gdn_exec_create(const gdn_exec_desc* desc, void* stream, gdn_exec** o
   x->vocab = vocab;
   x->max_batch = d.max_batch;
   x->max_prompt = d.max_prompt;
-  x->rows = d.max_batch > d.max_prompt ? d.max_batch : d.max_prompt;
+  x->rows = rows;
   x->device = d.device;
   x->stream = static_cast<hipStream_t>(stream);
   const size_t act = (size_t)x->rows * hidden * sizeof(uint16_t);
@@ -210,7 +304,10 @@ gdn_status gdn_exec_create(const gdn_exec_desc* desc, void* stream, gdn_exec** o
             hipHostMalloc(&x->p_next, sizeof(int32_t) * d.max_batch, 0) == hipSuccess &&
             hipHostMalloc(&x->p_first, sizeof(int32_t) * d.max_batch, 0) == hipSuccess &&
             hipEventCreateWithFlags(&x->done, hipEventDisableTiming) == hipSuccess &&
-            hipEventCreateWithFlags(&x->pre_copied, hipEventDisableTiming) == hipSuccess;
+            hipEventCreateWithFlags(&x->pre_copied, hipEventDisableTiming) == hipSuccess &&
+            (nqkv == 0 ||
+             (hipMalloc(&x->qkv, (size_t)x->rows * nqkv * sizeof(uint16_t)) == hipSuccess &&
+              hipMalloc(&x->att, (size_t)x->rows * Hq * 256 * sizeof(uint16_t)) == hipSuccess));
   if (!ok) {
     (void)hipGetLastError();
     exec_release(x);
@@ -260,6 +357,25 @@ gdn_status gdn_exec_prefill_batch(gdn_exec* x, int32_t nseq, const uint64_t* seq
   // The pinned block is free once the previous prefill's copy has run (a
   // prefill that failed after queueing it may not have waited).
   HIP_TRY(hipEventSynchronize(x->pre_copied), "gdn_exec_prefill");
+  if (x->kv) {
+    // the KV pages the prompts need against those free plus those the
+    // restarting (known) sequences give back: checked before anything changes
+    int32_t free_pages = 0;
+    GDN_TRY(gdn_kv_free_pages(x->kv, &free_pages));
+    int64_t avail = free_pages, need = 0;
+    for (int i = 0; i < nseq; ++i) {
+      need += (lens[i] + 63) / 64;
+      auto it = x->slot_of.find(seq_ids[i]);
+      if (it != x->slot_of.end()) {
+        int64_t len = 0;
+        GDN_TRY(gdn_kv_length(x->kv, it->second, &len));
+        avail += (len + 63) / 64;
+      }
+    }
+    if (need > avail)
+      return efail(GDN_ERR_OOM, "gdn_exec_prefill: %lld KV pages needed, %lld available",
+                   (long long)need, (long long)avail);
+  }
   // admit: a fresh sequence gets a free slot, a known one starts over in its
   // own; a call that runs out of slots gives back the ones it took
   int32_t* slots = x->p_pre;
@@ -280,6 +396,18 @@ gdn_status gdn_exec_prefill_batch(gdn_exec* x, int32_t nseq, const uint64_t* seq
     }
     x->slot_of.emplace(seq_ids[i], slots[i]);
     fresh.push_back(i);
+  }
+  if (x->kv) {
+    // every prompt starts at position 0 of its slot's KV cache
+    for (int i = 0; i < nseq; ++i) GDN_TRY(gdn_kv_release(x->kv, slots[i]));
+    gdn_status st = gdn_kv_step(x->kv, nseq, slots, lens, x->stream);
+    if (st != GDN_OK) {
+      for (int k : fresh) {
+        (void)gdn_slot_free(x->pool, slots[k]);
+        x->slot_of.erase(seq_ids[k]);
+      }
+      return st;
+    }
   }
   int32_t* cu = x->p_pre + nseq;
   int32_t* last = cu + nseq + 1;
@@ -303,7 +431,7 @@ gdn_status gdn_exec_prefill_batch(gdn_exec* x, int32_t nseq, const uint64_t* seq
           "embedding");
   GDN_TRY(run_layers(x, n, true, nseq));
   // final residual add + norm of every row, then each prompt's last row
-  HIP_TRY(gdn::launch_add_norm(x->h, x->layers.empty() ? nullptr : x->mix, n, x->hidden,
+  HIP_TRY(gdn::launch_add_norm(x->h, x->stack.empty() ? nullptr : x->mix, n, x->hidden,
                                x->final_norm_w, x->eps, x->hn, x->stream),
           "final norm");
   HIP_TRY(gdn::launch_gather_rows(x->hn, d_last, nseq, x->hidden, x->mix, x->stream),
@@ -351,6 +479,9 @@ gdn_status gdn_exec_submit_batch(gdn_exec* x, const uint64_t* seq_ids, const uin
     x->p_dec[x->max_batch + b] = (int32_t)tokens[b];
   }
   DevScope dev(x->device);
+  // plan the attention layers' KV step first: it fails (changing nothing)
+  // when the cache is out of pages, before any device work is queued
+  if (x->kv) GDN_TRY(gdn_kv_step(x->kv, B, x->p_dec, x->ones.data(), x->stream));
   HIP_TRY(hipMemcpyAsync(x->d_dec, x->p_dec, sizeof(int32_t) * 2 * x->max_batch,
                          hipMemcpyHostToDevice, x->stream),
           "batch copy");
@@ -392,6 +523,7 @@ gdn_status gdn_exec_release(gdn_exec* x, uint64_t seq_id) {
   // Work already queued on the slot runs before any later prefill re-zeroes
   // it (one stream), so the slot can be handed out again at once.
   GDN_TRY(gdn_slot_free(x->pool, it->second));
+  if (x->kv) GDN_TRY(gdn_kv_release(x->kv, it->second));
   x->slot_of.erase(it);
   return GDN_OK;
 }

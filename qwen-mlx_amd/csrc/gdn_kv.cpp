@@ -15,11 +15,11 @@
 // The schedule: the step's tokens form groups of up to 16 / G consecutive
 // tokens of one sequence (G query heads per kv head: a group's (token, head)
 // pairs fill the 16 columns of an MFMA tile); each (group, kv head) segment
-// is its keys' 16-key blocks. All segments' blocks, in order, are split
-// evenly over P one-wave workers, P up to max_workers (default below), at
-// least kMinBlocks blocks each; a worker writes one
-// partial per segment it touches and the combine kernel merges a segment's
-// partials, which come from consecutive workers.
+// is its keys, cut into chunks of 384 keys at fixed points. All segments'
+// chunks, in order, go to P one-wave workers in equal runs of kpw, P up to
+// max_workers (default below). Every chunk writes one partial and the
+// combine kernel merges a segment's partials in order, so a token's result
+// does not depend on the rest of the step.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -51,12 +51,11 @@ gdn_status khip(hipError_t e, const char* what) {
 constexpr int kPageTokens = 64;
 constexpr int kHeadDim = 256;
 // Workers per step: a step whose key blocks are each read about once (decode)
-// streams from HBM and runs best at one wave per SIMD (256 CUs x 4); one that
-// re-reads them from cache (a prompt's token groups share its keys) wants the
-// two resident waves per SIMD the block kernel's registers allow.
-constexpr int kStreamWorkers = 1024;
+// streams from HBM and runs best near one wave per SIMD (256 CUs x 4); one
+// that re-reads them from cache (a prompt's token groups share its keys)
+// wants the two resident waves per SIMD the block kernel's registers allow.
+constexpr int kStreamWorkers = 1536;  // equal runs of chunks: 768 .. 1536 workers
 constexpr int kReuseWorkers = 2048;
-constexpr int kMinBlocks = 8;      // 16-key blocks per worker at least
 
 // int32 words of the step metadata for up to T tokens and P workers
 size_t meta_words(int T, int Hkv, int P) { return (size_t)T * (5 + 4 + 4 * (size_t)Hkv) + P; }
@@ -91,8 +90,7 @@ struct gdn_kv {
   void* workspace = nullptr;
   size_t ws_bytes = 0;
   // the planned step
-  int T = 0, NG = 0, P = 0;
-  int64_t W = 0;
+  int T = 0, NG = 0, P = 0, NC = 0, kpw = 0;
   bool stream_keys = false;
   bool planned = false;
 };
@@ -166,6 +164,12 @@ gdn_status gdn_kv_destroy(gdn_kv* kv) {
   if (!kv) return GDN_OK;
   Dev dev(kv->d.device);
   kv_release_all(kv);
+  return GDN_OK;
+}
+
+gdn_status gdn_kv_describe(const gdn_kv* kv, gdn_kv_desc* desc) {
+  if (!kv || !desc) return kfail(GDN_ERR_INVALID, "gdn_kv_describe: NULL argument");
+  *desc = kv->d;
   return GDN_OK;
 }
 
@@ -245,43 +249,34 @@ gdn_status gdn_kv_step(gdn_kv* kv, int32_t n, const int32_t* slots, const int32_
     }
   }
   const int NG = (int)groups.size(), NS = NG * Hkv;
-  std::vector<int64_t> sf0(NS + 1);
-  sf0[0] = 0;
+  // each segment's keys in chunks of C 16-key blocks, numbered in segment order
+  const int C = gdn::attn_chunk_blocks();
+  std::vector<int64_t> cs0(NS + 1);
+  cs0[0] = 0;
+  int64_t W = 0, distinct = 0;
   for (int gi = 0; gi < NG; ++gi) {
     const int64_t nblk = ((int64_t)groups[gi].pos0 + groups[gi].ntok + 15) / 16;
-    for (int j = 0; j < Hkv; ++j) sf0[gi * Hkv + j + 1] = sf0[gi * Hkv + j] + nblk;
+    for (int j = 0; j < Hkv; ++j) cs0[gi * Hkv + j + 1] = cs0[gi * Hkv + j] + (nblk + C - 1) / C;
+    W += nblk * Hkv;
+    // distinct blocks: each sequence's keys once per kv head (its last group's)
+    if (gi + 1 == NG || groups[gi + 1].slot != groups[gi].slot) distinct += nblk * Hkv;
   }
-  const int64_t W = sf0[NS];
-  if (W > INT32_MAX) return kfail(GDN_ERR_INVALID, "gdn_kv_step: %lld key blocks", (long long)W);
-  // distinct blocks: each sequence's keys once per kv head (its last group's)
-  int64_t distinct = 0;
-  for (int gi = 0; gi < NG; ++gi)
-    if (gi + 1 == NG || groups[gi + 1].slot != groups[gi].slot)
-      distinct += ((int64_t)groups[gi].pos0 + groups[gi].ntok + 15) / 16 * Hkv;
+  const int64_t NC = cs0[NS];
+  if (NC > INT32_MAX / 2) return kfail(GDN_ERR_INVALID, "gdn_kv_step: %lld key chunks", (long long)NC);
   const bool stream_keys = W < 2 * distinct;
   const int pmax = d.max_workers > 0 ? d.max_workers : (stream_keys ? kStreamWorkers : kReuseWorkers);
-  const int P = (int)std::min<int64_t>(pmax, (W + kMinBlocks - 1) / kMinBlocks);
-  // worker w owns flat blocks [a(w), a(w + 1)), a(w) = w W / P
-  auto a = [&](int64_t w) { return w * W / P; };
-  std::vector<int32_t> seg_wf(NS), seg_np(NS), seg_pb(NS), wseg(P);
-  int64_t pieces = 0;
+  // equal runs of kpw chunks: kpw = ceil(NC / pmax), P = ceil(NC / kpw) <= pmax
+  const int kpw = (int)((NC + pmax - 1) / pmax);
+  const int P = (int)((NC + kpw - 1) / kpw);
+  std::vector<int32_t> wseg(P);
   {
-    int w = 0;
-    for (int sg = 0; sg < NS; ++sg) {
-      while (a(w + 1) <= sf0[sg]) ++w;
-      int wl = w;
-      while (a(wl + 1) <= sf0[sg + 1] - 1) ++wl;
-      seg_wf[sg] = w;
-      seg_np[sg] = wl - w + 1;
-      seg_pb[sg] = (int32_t)pieces;
-      pieces += seg_np[sg];
-    }
     int sg = 0;
     for (int ww = 0; ww < P; ++ww) {
-      while (sf0[sg + 1] <= a(ww)) ++sg;
+      while (cs0[sg + 1] <= (int64_t)ww * kpw) ++sg;
       wseg[ww] = sg;
     }
   }
+  const int64_t pieces = NC;
   const size_t ws = gdn::attn_workspace_bytes((int)T, d.num_q_heads, pieces);
   hipError_t e;
   if (ws > kv->ws_bytes) {
@@ -319,10 +314,10 @@ gdn_status gdn_kv_step(gdn_kv* kv, int32_t n, const int32_t* slots, const int32_
     }
   }
   for (int sg = 0; sg < NS; ++sg) {
-    m_seg[4 * sg] = (int32_t)sf0[sg];
-    m_seg[4 * sg + 1] = seg_pb[sg];
-    m_seg[4 * sg + 2] = seg_wf[sg];
-    m_seg[4 * sg + 3] = seg_np[sg];
+    m_seg[4 * sg] = (int32_t)cs0[sg];
+    m_seg[4 * sg + 1] = (int32_t)(cs0[sg + 1] - cs0[sg]);
+    m_seg[4 * sg + 2] = 0;
+    m_seg[4 * sg + 3] = 0;
   }
   for (int ww = 0; ww < P; ++ww) m_wseg[ww] = wseg[ww];
   const size_t words = (size_t)5 * T + 4 * (size_t)NG + 4 * (size_t)NS + P;
@@ -350,7 +345,8 @@ gdn_status gdn_kv_step(gdn_kv* kv, int32_t n, const int32_t* slots, const int32_
   kv->T = (int)T;
   kv->NG = NG;
   kv->P = P;
-  kv->W = W;
+  kv->NC = (int)NC;
+  kv->kpw = kpw;
   kv->stream_keys = stream_keys;
   kv->planned = true;
   return GDN_OK;
@@ -381,7 +377,8 @@ gdn_status gdn_attn_forward(gdn_kv* kv, int32_t layer, const uint16_t* q_full, i
   a.Hq = d.num_q_heads;
   a.Hkv = d.num_kv_heads;
   a.P = kv->P;
-  a.W = kv->W;
+  a.NC = kv->NC;
+  a.kpw = kv->kpw;
   a.stream_keys = kv->stream_keys;
   a.max_pages = d.max_pages_per_slot;
   a.rot_dim = rotary_dim;

@@ -75,6 +75,8 @@ SIGNATURES = {
     "gdn_exec_logits": ([_VP, ctypes.POINTER(_VP), ctypes.POINTER(_I32), ctypes.POINTER(_I32)],
                         ctypes.c_int),
     "gdn_kv_create": ([_VP, ctypes.POINTER(_VP)], ctypes.c_int),
+    "gdn_kv_describe": ([_VP, _VP], ctypes.c_int),
+    "gdn_pool_describe": ([_VP, _VP], ctypes.c_int),
     "gdn_kv_destroy": ([_VP], ctypes.c_int),
     "gdn_kv_release": ([_VP, _I32], ctypes.c_int),
     "gdn_kv_length": ([_VP, _I32, ctypes.POINTER(ctypes.c_int64)], ctypes.c_int),
@@ -113,11 +115,18 @@ class KVDesc(ctypes.Structure):
                 ("max_workers", _I32)]
 
 
+class ExecAttnLayer(ctypes.Structure):
+    _fields_ = [("position", _I32), ("qkv_proj", _VP), ("o_proj", _VP), ("q_norm_w", _VP),
+                ("k_norm_w", _VP)]
+
+
 class ExecDesc(ctypes.Structure):
     _fields_ = [("pool", _VP), ("num_layers", _I32), ("layers", ctypes.POINTER(_VP)),
                 ("input_norm_w", ctypes.POINTER(_VP)), ("final_norm_w", _VP),
                 ("rms_eps", ctypes.c_float), ("embed", _VP), ("head", _VP),
-                ("max_batch", _I32), ("max_prompt", _I32), ("device", _I32)]
+                ("max_batch", _I32), ("max_prompt", _I32), ("device", _I32),
+                ("num_attn_layers", _I32), ("attn_layers", ctypes.POINTER(ExecAttnLayer)),
+                ("kv", _VP), ("rope_theta", ctypes.c_float), ("rotary_dim", _I32)]
 
 
 class PoolDesc(ctypes.Structure):
@@ -478,21 +487,33 @@ class KVCache:
 
 
 class Executor:
-    """ModelExecutor (src/scheduler/executor.rs:21-49) over pool slots: the GDN
-    decoder stack h = embed[tok]; h += layer_l(rms_norm(h, w_l)) per layer;
-    greedy token of lm_head(rms_norm(h, w_final)). layers: Layer objects on
-    `pool`; embed [vocab, hidden] bf16 device tensor; head: QLinear hidden ->
-    vocab. Sequence ids are caller-chosen integers."""
+    """ModelExecutor (src/scheduler/executor.rs:21-49) over pool slots: the
+    decoder stack h = embed[tok]; h += mixer_l(rms_norm(h, w_l)) per layer;
+    greedy token of lm_head(rms_norm(h, w_final)). layers: GDN Layer objects on
+    `pool`, in order; attn_layers: (position, qkv QLinear, o_proj QLinear,
+    q_norm_w, k_norm_w) per attention layer, on the KVCache `kv`; input_norm_w:
+    one per decoder layer in stack order; embed [vocab, hidden] bf16 device
+    tensor; head: QLinear hidden -> vocab. Sequence ids are caller-chosen
+    integers."""
 
     def __init__(self, pool, layers, input_norm_w, final_norm_w, embed, head, rms_eps=1e-6,
-                 max_batch=64, max_prompt=4096, device=0, stream=None):
+                 max_batch=64, max_prompt=4096, device=0, stream=None, attn_layers=(), kv=None,
+                 rope_theta=1.0e7, rotary_dim=64):
         self.lib = load()
-        self._keep = (pool, list(layers), list(input_norm_w), final_norm_w, embed, head)
+        attn_layers = list(attn_layers)
+        self._keep = (pool, list(layers), list(input_norm_w), final_norm_w, embed, head,
+                      attn_layers, kv)
         n = len(layers)
+        na = len(attn_layers)
         self._layers = (_VP * max(n, 1))(*[l.handle.value for l in layers])
-        self._norms = (_VP * max(n, 1))(*[_ptr(w) for w in input_norm_w])
+        self._norms = (_VP * max(len(input_norm_w), 1))(*[_ptr(w) for w in input_norm_w])
+        self._attn = (ExecAttnLayer * max(na, 1))(
+            *[ExecAttnLayer(int(p), qkv.handle, o.handle, _ptr(qn), _ptr(kn))
+              for p, qkv, o, qn, kn in attn_layers])
         d = ExecDesc(pool.handle, n, self._layers, self._norms, _ptr(final_norm_w),
-                     float(rms_eps), _ptr(embed), head.handle, max_batch, max_prompt, device)
+                     float(rms_eps), _ptr(embed), head.handle, max_batch, max_prompt, device,
+                     na, self._attn, kv.handle if kv is not None else None, float(rope_theta),
+                     int(rotary_dim))
         h = _VP()
         self._stream = stream
         _check(self.lib.gdn_exec_create(ctypes.byref(d), _stream(stream), ctypes.byref(h)))

@@ -6,12 +6,11 @@ Bars: gated outputs within 2e-2 (absolute below 1, relative above) and 1e-2
 relative L2 of the oracle (float32 softmax and accumulation against float64);
 cached values bit-exact; cached keys (norm and RoPE in float32) within one
 bf16 ulp of the key plus one of its RoPE pair's magnitude. A token's work
-reads only its own sequence, so a batched step equals the same sequences
-stepped alone -- caches bit for bit, outputs up to float32 reassociation (the
-step's key blocks are split evenly over the workers, so where a token's keys
-are cut into partials depends on the whole step, and the float32 merge order
-with it) -- the property the reference's padded, unmasked, single-offset
-batching (mlx_executor.rs:57-88, qwen3_5.rs:410,443-447) lacks.
+reads only its own sequence and its keys are cut into partials at fixed
+points, so a batched step equals the same sequences stepped alone bit for bit
+-- the property the reference's padded, unmasked, single-offset batching
+(mlx_executor.rs:57-88, qwen3_5.rs:410,443-447) lacks -- and a prompt
+processed in one step equals the same tokens spread over several.
 """
 import numpy as np
 import pytest
@@ -134,11 +133,7 @@ def test_attention_prefill_then_decode_matches_oracle(gpu, Hq, Hkv):
 
 def test_attention_batched_step_equals_sequences_alone(gpu):
     """Three sequences of different lengths stepped together and, on a twin
-    cache, each alone: caches bit-identical; outputs within two bf16 ulps or
-    2^-12 absolute (float32 reassociation moves o by ~1e-7 of the sum of
-    |p v|, which can flip bf16 roundings of o and of the gated product). A
-    key of another sequence, or padding, in a token's softmax would move its
-    output by about p |v|, orders of magnitude more."""
+    cache, each alone: outputs and caches bit-identical."""
     import torch
 
     import gdn_amd
@@ -165,16 +160,49 @@ def test_attention_batched_step_equals_sequences_alone(gpu):
                        ob[r0:r0 + n])
             r0 += n
         torch.cuda.synchronize()
-        a = O.bf16_to_f32(host(oa)).astype(np.float64)
-        b = O.bf16_to_f32(host(ob)).astype(np.float64)
-        bound = 2.0 * _ulp(np.maximum(np.abs(a), np.abs(b))) + 2.0 ** -12
-        ratio = np.abs(a - b) / bound
-        say("batched vs alone", f"ntok {ntok}: {int(np.sum(a != b))} of {a.size} differ, "
-                                f"worst |d| / bound {ratio.max():.2f}")
-        assert np.all(ratio <= 1.0), ntok
+        assert torch.equal(oa, ob), ntok
     for s in slots:
         for x, y in zip(ka.read(0, s), kb.read(0, s)):
             assert torch.equal(x, y)
+    ka.close()
+    kb.close()
+
+
+def test_attention_prompt_split_over_steps_is_bit_identical(gpu):
+    """A 600-token prompt in one step against the same rows in steps of 1, 5,
+    331 and 263 tokens (other token groupings, other chunk owners, other
+    step sizes), then two decode steps: outputs and caches bit-identical."""
+    import torch
+
+    import gdn_amd
+    say("gdn_attn_forward", "prompt at once vs split over steps")
+    rng = np.random.default_rng(1415)
+    Hq, Hkv, n = 16, 2, 600
+    ka, kb = (gdn_amd.KVCache(1, 2, 32, 16, Hq, Hkv, max_step_tokens=n) for _ in range(2))
+    w = (dev(O.f32_to_bf16((1 + 0.1 * rng.standard_normal(HD)).astype(np.float32))),
+         dev(O.f32_to_bf16((1 + 0.1 * rng.standard_normal(HD)).astype(np.float32))))
+    q = dev(O.f32_to_bf16(rng.standard_normal((n + 2, Hq * 2 * HD)).astype(np.float32)))
+    k = dev(O.f32_to_bf16(rng.standard_normal((n + 2, Hkv * HD)).astype(np.float32)))
+    v = dev(O.f32_to_bf16(rng.standard_normal((n + 2, Hkv * HD)).astype(np.float32)))
+    oa = torch.empty((n + 2, Hq * HD), dtype=torch.int16, device=gpu)
+    ob = torch.empty_like(oa)
+    ka.step([1], [n])
+    ka.forward(0, q[:n], k[:n], v[:n], *w, EPS, THETA, ROT, oa[:n])
+    r0 = 0
+    for m in (1, 5, 331, 263):
+        kb.step([1], [m])
+        kb.forward(0, q[r0:r0 + m], k[r0:r0 + m], v[r0:r0 + m], *w, EPS, THETA, ROT, ob[r0:r0 + m])
+        r0 += m
+    for cache, out in ((ka, oa), (kb, ob)):
+        for t in (n, n + 1):
+            cache.step([1], [1])
+            cache.forward(0, q[t:t + 1], k[t:t + 1], v[t:t + 1], *w, EPS, THETA, ROT, out[t:t + 1])
+    torch.cuda.synchronize()
+    diff = int((oa != ob).sum())
+    say("prompt at once vs split", f"{diff} of {oa.numel()} outputs differ")
+    assert diff == 0
+    for x, y in zip(ka.read(0, 1), kb.read(0, 1)):
+        assert torch.equal(x, y)
     ka.close()
     kb.close()
 
