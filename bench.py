@@ -78,6 +78,11 @@ def parse_args(argv=None):
                          "embedding, per layer norm + in_proj + fused decode + out_proj, "
                          "final norm, lm_head, greedy pick")
     ap.add_argument("--vocab", type=int, default=248320)
+    ap.add_argument("--hybrid", action="store_true",
+                    help="with --exec: the 40-layer stack, an attention layer at every fourth "
+                         "position (3, 7, ..., 39) between the GDN layers")
+    ap.add_argument("--prompt-len", type=int, default=16,
+                    help="with --exec: prompt tokens per sequence before the decode steps")
     ap.add_argument("--attn", action="store_true",
                     help="time the attention layers' decode step on the paged KV cache "
                          "(gdn_kv_step + gdn_attn_forward) instead")
@@ -341,6 +346,7 @@ def exec_bench(args):
     gen = torch.Generator(device=dev).manual_seed(args.seed)
     bf = torch.bfloat16
     pool = gdn_amd.Pool(L, args.slots, HK, HV)
+    P = args.prompt_len
     gl, keep = [], []
     for l in range(L):
         inp = _rand_qlinear(QL_HIDDEN, QL_PARTS, gen, dev)
@@ -351,15 +357,34 @@ def exec_bench(args):
         norm_w = (1 + 0.1 * torch.randn(DV, generator=gen, device=dev)).to(bf)
         gl.append(gdn_amd.Layer(pool, l, inp, outp, A_log, dt_bias, conv_w, norm_w, 1e-6))
         keep += [inp, outp]
+    attn, kv, NA = [], None, 0
+    if args.hybrid:
+        # one attention layer after every three GDN layers (positions 3, 7, ...)
+        NA = L // 3
+        Hq, Hkv = ATT_HQ, ATT_HKV
+        nqkv = Hq * 2 * ATT_HD + 2 * Hkv * ATT_HD
+        grow = P + args.warmup + args.steps + 1
+        per_seq = -(-grow // ATT_PAGE)
+        kv = gdn_amd.KVCache(NA, args.slots, B * per_seq + 8, per_seq, Hq, Hkv,
+                             max_step_tokens=max(B, 4 * P, 64))
+        for i in range(NA):
+            qkv = _rand_qlinear(QL_HIDDEN, [nqkv], gen, dev)
+            o = _rand_qlinear(Hq * ATT_HD, [QL_HIDDEN], gen, dev)
+            qn = (1 + 0.1 * torch.randn(ATT_HD, generator=gen, device=dev)).to(bf)
+            kn = (1 + 0.1 * torch.randn(ATT_HD, generator=gen, device=dev)).to(bf)
+            attn.append((4 * i + 3, qkv, o, qn, kn))
+            keep += [qkv, o]
     in_norm = [(1 + 0.1 * torch.randn(QL_HIDDEN, generator=gen, device=dev)).to(bf)
-               for _ in range(L)]
+               for _ in range(L + NA)]
     fin = (1 + 0.1 * torch.randn(QL_HIDDEN, generator=gen, device=dev)).to(bf)
     embed = torch.randn((V, QL_HIDDEN), generator=gen, device=dev).to(bf)
     head = _rand_qlinear(QL_HIDDEN, [V], gen, dev)
-    ex = gdn_amd.Executor(pool, gl, in_norm, fin, embed, head, 1e-6, max_batch=B, max_prompt=64)
+    ex = gdn_amd.Executor(pool, gl, in_norm, fin, embed, head, 1e-6, max_batch=B,
+                          max_prompt=max(64, 4 * P), attn_layers=attn, kv=kv, rope_theta=ATT_THETA,
+                          rotary_dim=ATT_ROT)
     rng = torch.Generator().manual_seed(args.seed)
     ids = list(range(1, B + 1))
-    prompts = [torch.randint(0, V, (16,), generator=rng).tolist() for _ in ids]
+    prompts = [torch.randint(0, V, (P,), generator=rng).tolist() for _ in ids]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     cur = [ex.prefill(i, p) for i, p in zip(ids, prompts)]
@@ -389,7 +414,14 @@ def exec_bench(args):
     wbytes = L * (QL_N * QL_HIDDEN // 2 + 2 * QL_N * (QL_HIDDEN // 64) * 2
                   + QL_HIDDEN * HV * DV // 2 + 2 * QL_HIDDEN * (HV * DV // 64) * 2) \
         + V * QL_HIDDEN // 2 + 2 * V * (QL_HIDDEN // 64) * 2
-    step_bytes = B * L * STATE_BYTES + wbytes
+    if args.hybrid:
+        nqkv = ATT_HQ * 2 * ATT_HD + 2 * ATT_HKV * ATT_HD
+        wbytes += NA * (nqkv * QL_HIDDEN // 2 + 2 * nqkv * (QL_HIDDEN // 64) * 2
+                        + QL_HIDDEN * ATT_HQ * ATT_HD // 2
+                        + 2 * QL_HIDDEN * (ATT_HQ * ATT_HD // 64) * 2)
+    # cached keys read per step by the attention layers (mean context over the timed steps)
+    kv_bytes = NA * B * (P + args.warmup + args.steps / 2) * ATT_HKV * ATT_HD * 2 * 2
+    step_bytes = B * L * STATE_BYTES + wbytes + int(kv_bytes)
     gbs = step_bytes / (ms * 1e-3) / 1e9
     out = {
         "metric": "GDN decoder-stack decode tokens/s through the executor (B sequences, all layers)",
@@ -403,17 +435,21 @@ def exec_bench(args):
         "dtype": "bf16 activations, 4-bit affine weights, f32 state",
         "data": "synthetic",
         "config": {"workload": f"executor decode step: {L} GDN layers (in_proj, fused decode + "
-                               f"norm-gate, out_proj) + lm_head {QL_HIDDEN}->{V}, B={B}, "
-                               f"{args.slots}-slot pools",
-                   "layers": L, "batch": B, "slots": args.slots, "hidden": QL_HIDDEN,
-                   "vocab": V},
-        "prefill_ms_per_sequence": {"prompt_tokens": 16, "one_per_call": round(pre_one * 1e3, 3),
+                               f"norm-gate, out_proj)"
+                               + (f" + {NA} attention layers (q|k|v proj, paged-KV attention, "
+                                  f"o_proj) interleaved" if NA else "")
+                               + f" + lm_head {QL_HIDDEN}->{V}, B={B}, {args.slots}-slot pools, "
+                                 f"{P}-token prompts",
+                   "layers": L, "attention_layers": NA, "batch": B, "slots": args.slots,
+                   "hidden": QL_HIDDEN, "vocab": V, "prompt_tokens": P},
+        "prefill_ms_per_sequence": {"prompt_tokens": P, "one_per_call": round(pre_one * 1e3, 3),
                                     f"{g}_per_call": round(pre_batched * 1e3, 3)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
                      "algorithmic_bytes_per_step": step_bytes,
-                     "note": "whole step (state read+write of B sequences in every layer plus "
-                             "every weight byte once) over the host-measured step time"},
+                     "note": "whole step (state read+write of B sequences in every GDN layer, "
+                             "every weight byte once, every cached K/V byte once) over the "
+                             "host-measured step time"},
     }
     ex.close()
     for g in gl:
