@@ -251,9 +251,12 @@ __global__ __launch_bounds__(64, 2) void attn_block_kernel(
 
     auto compute = [&](int kb, const uint4(&kf)[8], uint2(&vf)[16]) {
       f32x4 S = {0.f, 0.f, 0.f, 0.f};
+      // Q^T is re-read from LDS for every block rather than held in registers:
+      // an empty asm with a memory clobber keeps the compiler from hoisting
+      // the reads (a volatile read would also drain the memory counters).
+      asm volatile("" ::: "memory");
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks)  // volatile: re-read per block, not held in registers
-        S = mfma32(kf[ks], *const_cast<const volatile u32x4*>(&qlds[ks][lane]), S);
+      for (int ks = 0; ks < 8; ++ks) S = mfma32(kf[ks], qlds[ks][lane], S);
       const int key0 = 16 * kb + 4 * g4;  // this lane's keys key0 .. key0 + 3
       float x[4];
 #pragma unroll
@@ -329,12 +332,15 @@ __global__ __launch_bounds__(64, 2) void attn_block_kernel(
     uint2 vA[16], vB[16];
     load(kb0, kA, vA);
     // kb0 and the chunk size are even, so a chunk ends inside the range only
-    // after the second block of a pair; the range's own end is flushed after
+    // after the second block of a pair; the range's own end is flushed after.
+    // Every pass issues its loads (an index past the range repeats the last
+    // block), so the vector-memory counter waits for the block being
+    // computed with the next one still in flight.
     for (int kb = kb0; kb < kb1; kb += 2) {
-      if (kb + 1 < kb1) load(kb + 1, kB, vB);
+      load(min(kb + 1, kb1 - 1), kB, vB);
       compute(kb, kA, vA);
       if (kb + 1 >= kb1) break;
-      if (kb + 2 < kb1) load(kb + 2, kA, vA);
+      load(min(kb + 2, kb1 - 1), kA, vA);
       compute(kb + 1, kB, vB);
       if ((kb + 2) % kChunkBlocks == 0 && kb + 2 < kb1) flush(kb + 1);
     }
