@@ -32,6 +32,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kStageK = 128;    // k per pipeline stage: two groups
 constexpr int kMaxGroups = 64;  // K <= 4096
+constexpr int kWideDecodeN = 131072;  // decode-sized calls at least this wide use 64 x 128 tiles
 
 __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
@@ -531,8 +532,8 @@ hipError_t launch_qlinear_pack(const QLinearPackArgs& a) {
 int qlinear_decode_slices(int K, int Npad) {
   // one work-group per 64 columns; layers with fewer than 128 such groups
   // (out_proj: 2048 columns), and every K above 2048, split K into 512-wide
-  // slices (K <= 4096: at most 8)
-  if (K <= 512 || (K <= 2048 && Npad / 64 >= 128)) return 1;
+  // slices (K <= 4096: at most 8); very wide layers take the tiled kernel
+  if (K <= 512 || (K <= 2048 && Npad / 64 >= 128) || Npad >= kWideDecodeN) return 1;
   return K / 512;
 }
 
@@ -546,7 +547,15 @@ int qlinear_decode_slices(int K, int Npad) {
 // with one wave per SIMD took 1.98 ms). Deeper x prefetch (two stages in
 // registers) pushed it to one wave per SIMD and 2.06 ms; an XCD-aware tile
 // order (each XCD's L2 holding its own weight columns) changed nothing.
+//
+// Very wide layers at decode sizes (lm_head, 248,320 columns) re-read all of
+// x per 64 columns in qlinear_decode_kernel, 4x the weight bytes through L2.
+// There a 64 x 128 tile with every wave holding all 64 rows and two column
+// fragments (one row of four waves) took 140 us at M = 64, K = 2048, against
+// 196 us for the decode kernel, 159 us for the 2 x 2 wave grid and 157 us for
+// four column fragments per wave (256 VGPRs, one wave per SIMD).
 hipError_t launch_qlinear(const QLinearArgs& a) {
+  if (a.M <= 64 && a.Npad >= kWideDecodeN) return launch_cfg<4, 2, 1, 4>(a);
   if (a.M <= 64) {
     const int ns = a.part ? qlinear_decode_slices(a.K, a.Npad) : 1;
     if (ns > 1 || a.K == 512 || a.K == 1024 || a.K == 2048) {

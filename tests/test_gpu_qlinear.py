@@ -111,6 +111,34 @@ def test_qlinear_extreme_values(gpu):
     layer.close()
 
 
+@pytest.mark.parametrize("M", [1, 37, 64])
+def test_qlinear_wide_decode_columns_sampled(gpu, M):
+    """Decode-sized call on a layer wide enough (131,088 columns) for the
+    64 x 128 tile route that lm_head takes; the oracle checks 1,024 sampled
+    columns (columns are independent: y[:, n] depends only on row n of the
+    weights), the first and last included, and the padding past N stays
+    unwritten."""
+    import torch
+    say("gdn_qlinear_forward", f"wide decode M={M} K=2048 N=131088 (sampled columns)")
+    rng = np.random.default_rng(503 + M)
+    N, K = 131072 + 16, QWEN_HIDDEN
+    w = rng.integers(0, 2**32, (N, K // 8), dtype=np.uint32)
+    s = O.f32_to_bf16((rng.random((N, K // 64)) * 0.004 + 0.001).astype(np.float32))
+    b = O.f32_to_bf16((rng.standard_normal((N, K // 64)) * 0.03).astype(np.float32))
+    x = O.f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    layer = _layer(K, [(w, s, b)])
+    y = torch.full((M, N + 8), -1, dtype=torch.int16, device=gpu)
+    layer.forward(dev(x), y)
+    torch.cuda.synchronize()
+    yh = host(y)
+    assert np.all(yh[:, N:] == 0xFFFF), "columns past N were written"
+    cols = np.sort(rng.choice(N, 1024, replace=False))
+    cols[0], cols[-1] = 0, N - 1
+    yr, ye, mag = O.qmatmul_w4(x, w[cols], s[cols], b[cols])
+    _check(yh[:, cols], ye, mag, yr, f"qlinear wide M={M} sampled columns")
+    layer.close()
+
+
 def test_qlinear_prefill_rows_sampled(gpu):
     """Prefill-sized call (16384 tokens) on the full merged layer; the oracle
     checks 96 sampled rows (rows are independent), the rest are checked for
