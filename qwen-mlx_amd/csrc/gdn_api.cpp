@@ -671,6 +671,16 @@ gdn_status gdn_qlinear_dims(const gdn_qlinear* q, int32_t* K, int32_t* N) {
 
 gdn_status gdn_qlinear_forward(const gdn_qlinear* q, const uint16_t* x, int64_t x_stride,
                                int32_t M, uint16_t* y, int64_t y_stride, void* stream) {
+  return gdn::qlinear_forward(q, x, x_stride, M, y, y_stride, stream, nullptr);
+}
+
+}  // extern "C"
+
+namespace gdn {
+
+gdn_status qlinear_forward(const gdn_qlinear* q, const uint16_t* x, int64_t x_stride, int32_t M,
+                           uint16_t* y, int64_t y_stride, void* stream, QPartial* defer) {
+  if (defer) *defer = QPartial{};
   if (!q) return fail(GDN_ERR_INVALID, "gdn_qlinear_forward: NULL layer");
   if (M < 0) return fail(GDN_ERR_INVALID, "gdn_qlinear_forward: M = %d < 0", M);
   if (M == 0) return GDN_OK;
@@ -698,13 +708,14 @@ gdn_status gdn_qlinear_forward(const gdn_qlinear* q, const uint16_t* x, int64_t 
   a.y = y;
   a.ys = y_stride;
   a.part = q->part;
+  a.defer = defer;
   a.stream = as_stream(stream);
   hipError_t e = gdn::launch_qlinear(a);
   if (e != hipSuccess) return hip_fail(e, "gdn_qlinear_forward launch");
   return GDN_OK;
 }
 
-}  // extern "C"
+}  // namespace gdn
 
 // ------------------------------------------------------------ gdn_layer --
 // One GatedDeltaNet layer end to end (GatedDeltaNet::forward_with_cache,
@@ -812,6 +823,15 @@ gdn_status gdn_pool_reserve(gdn_pool* pool, int32_t max_tokens, void* stream) {
 
 gdn_status gdn_layer_decode(gdn_layer* L, const int32_t* slot_ids, int32_t B, const uint16_t* x,
                             int64_t x_stride, uint16_t* out, int64_t out_stride, void* stream) {
+  return gdn::layer_decode(L, slot_ids, B, x, x_stride, out, out_stride, stream, nullptr);
+}
+
+}  // extern "C"
+
+gdn_status gdn::layer_decode(gdn_layer* L, const int32_t* slot_ids, int32_t B, const uint16_t* x,
+                             int64_t x_stride, uint16_t* out, int64_t out_stride, void* stream,
+                             QPartial* defer) {
+  if (defer) *defer = QPartial{};
   if (B == 0 && L) return GDN_OK;
   gdn_status st = layer_args(L, x, x_stride, out, out_stride, "gdn_layer_decode");
   if (st) return st;
@@ -833,8 +853,10 @@ gdn_status gdn_layer_decode(gdn_layer* L, const int32_t* slot_ids, int32_t B, co
                         L->proj_stride, L->A_log, L->dt_bias, L->conv_w, L->norm_w, L->norm_eps,
                         gated, nullptr, stream);
   if (st) return st;
-  return gdn_qlinear_forward(L->out_proj, gated, value, B, out, out_stride, stream);
+  return qlinear_forward(L->out_proj, gated, value, B, out, out_stride, stream, defer);
 }
+
+extern "C" {
 
 gdn_status gdn_layer_prefill(gdn_layer* L, const int32_t* slot_ids, const int32_t* cu_seqlens,
                              int32_t nseq, int32_t total_tokens, const uint16_t* x,

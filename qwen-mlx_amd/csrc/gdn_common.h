@@ -204,6 +204,16 @@ struct QLinearPackArgs {
   hipStream_t stream;
 };
 
+// f32 K-slice partials that a decode-sized qlinear call left for its consumer
+// to add: element (slice sl, row m, column n) at part[(sl * 64 + m) * Npad + n].
+// The sum over sl = 0, 1, ..., nslice - 1 in that order, rounded once to bf16,
+// is the call's output. nslice == 0: nothing pending (the call wrote y).
+struct QPartial {
+  const float* part = nullptr;
+  int nslice = 0;
+  int Npad = 0;
+};
+
 struct QLinearArgs {
   const uint16_t* x;  // [M, xs] bf16
   int64_t xs;
@@ -215,6 +225,8 @@ struct QLinearArgs {
   uint16_t* y;        // [M, ys] bf16
   int64_t ys;
   float* part;        // K-slice partials [slices][64][Npad] f32 (decode shapes), or null
+  QPartial* defer;    // non-null: a K-sliced call skips its slice sum and describes the
+                      // partials here instead of writing y (nslice = 0 when y was written)
   hipStream_t stream;
 };
 
@@ -270,8 +282,22 @@ gdn_status set_error(gdn_status code, const char* msg);
 // Executor model-body kernels (gdn_exec.hip).
 hipError_t launch_embed(const uint16_t* table, const int32_t* tok, int n, int vocab, int hidden,
                         uint16_t* h, hipStream_t s);
-hipError_t launch_add_norm(uint16_t* h, const uint16_t* d, int n, int hidden, const uint16_t* w,
-                           float eps, uint16_t* hn, hipStream_t s);
+// gdn_qlinear_forward and gdn_layer_decode with the option to leave the
+// projection's K-slice partials pending (defer non-null): a decode-sized
+// projection that splits K then skips its slice sum, writes nothing to y and
+// describes the partials in *defer for launch_add_norm to add; otherwise it
+// writes y and sets defer->nslice = 0. The partials sit in the projection's
+// own workspace until its next call.
+gdn_status qlinear_forward(const gdn_qlinear* q, const uint16_t* x, int64_t x_stride, int32_t M,
+                           uint16_t* y, int64_t y_stride, void* stream, QPartial* defer);
+gdn_status layer_decode(gdn_layer* L, const int32_t* slot_ids, int32_t B, const uint16_t* x,
+                        int64_t x_stride, uint16_t* out, int64_t out_stride, void* stream,
+                        QPartial* defer);
+
+// d: bf16 rows [n, hidden], or null; dp (taken over d when it has slices
+// pending): the f32 partials of a deferred projection with N == hidden.
+hipError_t launch_add_norm(uint16_t* h, const uint16_t* d, const QPartial* dp, int n, int hidden,
+                           const uint16_t* w, float eps, uint16_t* hn, hipStream_t s);
 hipError_t launch_gather_rows(const uint16_t* src, const int32_t* idx, int n, int hidden,
                               uint16_t* dst, hipStream_t s);
 // Greedy pick in two passes; pv / pi hold n * argmax_chunks(vocab) partials.

@@ -87,6 +87,8 @@ struct gdn_exec {
   uint16_t* h = nullptr;      // residual stream [rows, hidden]
   uint16_t* hn = nullptr;     // normed rows fed to a layer
   uint16_t* mix = nullptr;    // layer output rows
+  gdn::QPartial pend{};       // the last mixer's output as pending K-slice partials (in place
+                              // of mix rows when nslice > 0), added by the next residual seam
   uint16_t* logits = nullptr; // [max_batch, vocab]
   uint16_t* qkv = nullptr;    // attention q|gate, k, v rows [rows, nqkv]
   uint16_t* att = nullptr;    // gated attention rows [rows, Hq * 256]
@@ -151,9 +153,10 @@ gdn_status run_layers(gdn_exec* x, int n, bool prefill, int nseq = 0) {
   const int32_t* slots = prefill ? x->d_pre : x->d_dec;
   const int qw = 2 * x->Hq * 256, kw = x->Hkv * 256;  // q|gate and k widths of a qkv row
   for (size_t p = 0; p < x->stack.size(); ++p) {
-    HIP_TRY(gdn::launch_add_norm(x->h, p == 0 ? nullptr : x->mix, n, x->hidden, x->norm_w[p],
-                                 x->eps, x->hn, x->stream),
+    HIP_TRY(gdn::launch_add_norm(x->h, p == 0 ? nullptr : x->mix, p == 0 ? nullptr : &x->pend,
+                                 n, x->hidden, x->norm_w[p], x->eps, x->hn, x->stream),
             "residual add + norm");
+    x->pend = gdn::QPartial{};
     const int e = x->stack[p];
     if (e < 0) {
       const int ai = -e - 1;
@@ -162,13 +165,14 @@ gdn_status run_layers(gdn_exec* x, int n, bool prefill, int nseq = 0) {
       GDN_TRY(gdn_attn_forward(x->kv, ai, x->qkv, x->nqkv, x->qkv + qw, x->nqkv, x->qkv + qw + kw,
                                x->nqkv, a.q_norm_w, a.k_norm_w, x->eps, x->rope_theta,
                                x->rotary_dim, x->att, x->Hq * 256, x->stream));
-      GDN_TRY(gdn_qlinear_forward(a.o, x->att, x->Hq * 256, n, x->mix, x->hidden, x->stream));
+      GDN_TRY(gdn::qlinear_forward(a.o, x->att, x->Hq * 256, n, x->mix, x->hidden, x->stream,
+                                   &x->pend));
     } else if (prefill) {
       GDN_TRY(gdn_layer_prefill(x->layers[e], slots, x->d_pre + nseq, nseq, n, x->hn, x->hidden,
                                 x->mix, x->hidden, x->stream));
     } else {
-      GDN_TRY(gdn_layer_decode(x->layers[e], slots, n, x->hn, x->hidden, x->mix, x->hidden,
-                               x->stream));
+      GDN_TRY(gdn::layer_decode(x->layers[e], slots, n, x->hn, x->hidden, x->mix, x->hidden,
+                                x->stream, &x->pend));
     }
   }
   return GDN_OK;
@@ -180,8 +184,12 @@ gdn_status pick(gdn_exec* x, int r0, int n, int32_t* dst) {
   uint16_t* hr = x->h + (size_t)r0 * x->hidden;
   const uint16_t* mr = x->stack.empty() ? nullptr : x->mix + (size_t)r0 * x->hidden;
   uint16_t* nr = x->hn + (size_t)r0 * x->hidden;
-  HIP_TRY(gdn::launch_add_norm(hr, mr, n, x->hidden, x->final_norm_w, x->eps, nr, x->stream),
+  gdn::QPartial pp = x->pend;
+  if (pp.nslice > 0) pp.part += (size_t)r0 * pp.Npad;
+  HIP_TRY(gdn::launch_add_norm(hr, mr, mr ? &pp : nullptr, n, x->hidden, x->final_norm_w, x->eps,
+                               nr, x->stream),
           "final norm");
+  x->pend = gdn::QPartial{};
   GDN_TRY(gdn_qlinear_forward(x->head, nr, x->hidden, n, x->logits, x->vocab, x->stream));
   HIP_TRY(gdn::launch_argmax(x->logits, x->vocab, n, x->vocab, x->d_pv, x->d_pi, x->d_next,
                              x->stream),
@@ -431,9 +439,11 @@ gdn_status gdn_exec_prefill_batch(gdn_exec* x, int32_t nseq, const uint64_t* seq
           "embedding");
   GDN_TRY(run_layers(x, n, true, nseq));
   // final residual add + norm of every row, then each prompt's last row
-  HIP_TRY(gdn::launch_add_norm(x->h, x->stack.empty() ? nullptr : x->mix, n, x->hidden,
+  HIP_TRY(gdn::launch_add_norm(x->h, x->stack.empty() ? nullptr : x->mix,
+                               x->stack.empty() ? nullptr : &x->pend, n, x->hidden,
                                x->final_norm_w, x->eps, x->hn, x->stream),
           "final norm");
+  x->pend = gdn::QPartial{};
   HIP_TRY(gdn::launch_gather_rows(x->hn, d_last, nseq, x->hidden, x->mix, x->stream),
           "last rows");
   GDN_TRY(gdn_qlinear_forward(x->head, x->mix, x->hidden, nseq, x->logits, x->vocab, x->stream));

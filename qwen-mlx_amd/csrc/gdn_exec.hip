@@ -40,13 +40,18 @@ __global__ __launch_bounds__(kRowThreads) void embed_kernel(const uint16_t* __re
 
 // Residual add then rms-norm of one row (the decoder layer's
 // `x + mixer(input_layernorm(x))` seam, qwen3_5.rs:729-739):
-//   h = bf16(h + d)   (skipped when d is null)
+//   h = bf16(h + d)   (skipped when d and dp are null)
+// With dp, d is the bf16 rounding of the f32 sum of nslice partial rows
+// dp[(sl * 64 + row) * npad + c], added in slice order: the value the
+// projection's own slice-sum kernel would have stored, so the result is
+// bit-identical to the two-launch form.
 //   hn = bf16(w * bf16(h * rsqrt(mean(h^2) + eps)))
 // grid n, block 256; thread t owns the 8 elements from 8t + 2048j (16-byte
 // accesses; hidden a multiple of 8, at most 4096).
 __global__ __launch_bounds__(kRowThreads) void add_norm_kernel(uint16_t* __restrict__ h,
                                                                const uint16_t* __restrict__ d,
-                                                               int hidden,
+                                                               const float* __restrict__ dp,
+                                                               int nslice, int npad, int hidden,
                                                                const uint16_t* __restrict__ w,
                                                                float eps,
                                                                uint16_t* __restrict__ hn) {
@@ -61,9 +66,26 @@ __global__ __launch_bounds__(kRowThreads) void add_norm_kernel(uint16_t* __restr
     if (c < hidden) {
       uint4 hv = *reinterpret_cast<const uint4*>(h + row + c);
       const uint32_t* hw = reinterpret_cast<const uint32_t*>(&hv);
-      if (d != nullptr) {
-        const uint4 dv = *reinterpret_cast<const uint4*>(d + row + c);
-        const uint32_t* dw = reinterpret_cast<const uint32_t*>(&dv);
+      if (d != nullptr || dp != nullptr) {
+        uint32_t dw[4];
+        if (dp != nullptr) {
+          const float* src = dp + (size_t)blockIdx.x * npad + c;
+          v4f t0 = *reinterpret_cast<const v4f*>(src), t1 = *reinterpret_cast<const v4f*>(src + 4);
+          for (int sl = 1; sl < nslice; ++sl) {
+            const float* ps = src + (size_t)sl * 64 * npad;
+            t0 += *reinterpret_cast<const v4f*>(ps);
+            t1 += *reinterpret_cast<const v4f*>(ps + 4);
+          }
+          dw[0] = f2bf2(t0[0], t0[1]);
+          dw[1] = f2bf2(t0[2], t0[3]);
+          dw[2] = f2bf2(t1[0], t1[1]);
+          dw[3] = f2bf2(t1[2], t1[3]);
+        } else {
+          const uint4 dv = *reinterpret_cast<const uint4*>(d + row + c);
+          const uint32_t* dr = reinterpret_cast<const uint32_t*>(&dv);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) dw[e] = dr[e];
+        }
         uint32_t o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
@@ -192,11 +214,15 @@ hipError_t launch_embed(const uint16_t* table, const int32_t* tok, int n, int vo
   return hipGetLastError();
 }
 
-hipError_t launch_add_norm(uint16_t* h, const uint16_t* d, int n, int hidden, const uint16_t* w,
-                           float eps, uint16_t* hn, hipStream_t s) {
+hipError_t launch_add_norm(uint16_t* h, const uint16_t* d, const QPartial* dp, int n, int hidden,
+                           const uint16_t* w, float eps, uint16_t* hn, hipStream_t s) {
   if (n <= 0) return hipSuccess;
   if (hidden > kRowThreads * kMaxHiddenPerThread || hidden % 8) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(add_norm_kernel, dim3(n), dim3(kRowThreads), 0, s, h, d, hidden, w, eps, hn);
+  const bool part = dp != nullptr && dp->nslice > 0;
+  if (part && (n > 64 || dp->Npad < hidden || dp->Npad % 8)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(add_norm_kernel, dim3(n), dim3(kRowThreads), 0, s, h, part ? nullptr : d,
+                     part ? dp->part : nullptr, part ? dp->nslice : 0, part ? dp->Npad : 0,
+                     hidden, w, eps, hn);
   return hipGetLastError();
 }
 

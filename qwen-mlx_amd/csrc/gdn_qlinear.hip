@@ -555,6 +555,7 @@ int qlinear_decode_slices(int K, int Npad) {
 // 196 us for the decode kernel, 159 us for the 2 x 2 wave grid and 157 us for
 // four column fragments per wave (256 VGPRs, one wave per SIMD).
 hipError_t launch_qlinear(const QLinearArgs& a) {
+  if (a.defer) *a.defer = QPartial{};
   if (a.M <= 64 && a.Npad >= kWideDecodeN) return launch_cfg<4, 2, 1, 4>(a);
   if (a.M <= 64) {
     const int ns = a.part ? qlinear_decode_slices(a.K, a.Npad) : 1;
@@ -566,6 +567,10 @@ hipError_t launch_qlinear(const QLinearArgs& a) {
                            a.part, a.Npad);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
+        if (a.defer) {  // the consumer adds the slices
+          *a.defer = QPartial{a.part, ns, a.Npad};
+          return hipSuccess;
+        }
         const int64_t n4 = (int64_t)a.M * (a.Npad / 4);
         hipLaunchKernelGGL(qlinear_sum_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0,
                            a.stream, a.part, ns, a.M, a.N, a.Npad, a.y, a.ys);
