@@ -388,14 +388,21 @@ typedef struct gdn_exec_desc {
 
 /* Allocates the executor's buffers (activations for max(max_batch,
  * max_prompt) rows, logits for max_batch rows, pinned staging) and sizes the
- * pool's layer buffers with gdn_pool_reserve: later calls allocate nothing. */
+ * pool's layer buffers with gdn_pool_reserve: later decode steps allocate
+ * nothing. A prefill on a stack with attention layers may grow the KV cache's
+ * attention workspace (see gdn_kv_step). max_prompt must fit one slot's KV
+ * pages (max_pages_per_slot * 64 tokens). */
 gdn_status gdn_exec_create(const gdn_exec_desc* desc, void* stream, gdn_exec** out);
 /* Waits for the stream, frees the buffers and the slots still held. */
 gdn_status gdn_exec_destroy(gdn_exec* exec);
 
 /* ModelExecutor::prefill (executor.rs:23): admit seq_id (a free slot, or its
  * own slot again if it is known) with zeroed state, run the prompt through
- * every layer and return the first picked token. Synchronous. */
+ * every layer and return the first picked token. Synchronous. Checks that
+ * fail before admission change nothing; a failure after it retires every
+ * sequence of the call (slot and KV pages freed, id forgotten: a known
+ * sequence has given back its pages and its state is no longer usable), and
+ * the caller prefills them again. */
 gdn_status gdn_exec_prefill(gdn_exec* exec, uint64_t seq_id, const int32_t* prompt, int32_t len,
                             uint32_t* first_token);
 
@@ -498,7 +505,9 @@ gdn_status gdn_kv_free_pages(const gdn_kv* kv, int32_t* count);
  * list; the per-token metadata is copied to the device on `stream`. Fails
  * (changing nothing) when pages, max_pages_per_slot or max_step_tokens do not
  * suffice. A step with one token per sequence is a decode step, a prompt is
- * one sequence's ntok tokens. */
+ * one sequence's ntok tokens. gdn_kv_create sizes the attention workspace for
+ * every decode step; a step with prompts whose schedule needs more grows it
+ * here (waiting for `stream` first). */
 gdn_status gdn_kv_step(gdn_kv* kv, int32_t n, const int32_t* slots, const int32_t* ntok,
                        void* stream);
 

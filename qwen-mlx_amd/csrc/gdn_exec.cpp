@@ -257,6 +257,12 @@ gdn_status gdn_exec_create(const gdn_exec_desc* desc, void* stream, gdn_exec** o
                    pd.num_slots, rows, d.device);
     if (d.rotary_dim < 0 || d.rotary_dim > 256 || d.rotary_dim % 2 != 0 || !(d.rope_theta > 0.0f))
       return efail(GDN_ERR_INVALID, "gdn_exec_create: rotary_dim %d / rope_theta", d.rotary_dim);
+    // a prompt starts at position 0 of its slot's KV cache: the longest one
+    // must fit the pages one slot can hold
+    if ((int64_t)d.max_prompt > (int64_t)kd.max_pages_per_slot * 64)
+      return efail(GDN_ERR_INVALID,
+                   "gdn_exec_create: max_prompt %d > %lld tokens one slot's KV pages hold",
+                   d.max_prompt, (long long)kd.max_pages_per_slot * 64);
     Hq = kd.num_q_heads;
     Hkv = kd.num_kv_heads;
     nqkv = 2 * Hq * 256 + 2 * Hkv * 256;
@@ -367,11 +373,17 @@ gdn_status gdn_exec_prefill_batch(gdn_exec* x, int32_t nseq, const uint64_t* seq
   HIP_TRY(hipEventSynchronize(x->pre_copied), "gdn_exec_prefill");
   if (x->kv) {
     // the KV pages the prompts need against those free plus those the
-    // restarting (known) sequences give back: checked before anything changes
+    // restarting (known) sequences give back, and each prompt against one
+    // slot's page table: checked before anything changes
+    gdn_kv_desc kd{};
+    GDN_TRY(gdn_kv_describe(x->kv, &kd));
     int32_t free_pages = 0;
     GDN_TRY(gdn_kv_free_pages(x->kv, &free_pages));
     int64_t avail = free_pages, need = 0;
     for (int i = 0; i < nseq; ++i) {
+      if ((int64_t)lens[i] > (int64_t)kd.max_pages_per_slot * 64)
+        return efail(GDN_ERR_INVALID, "gdn_exec_prefill: prompt %d of %d tokens > %lld per slot",
+                     i, lens[i], (long long)kd.max_pages_per_slot * 64);
       need += (lens[i] + 63) / 64;
       auto it = x->slot_of.find(seq_ids[i]);
       if (it != x->slot_of.end()) {
@@ -405,17 +417,34 @@ gdn_status gdn_exec_prefill_batch(gdn_exec* x, int32_t nseq, const uint64_t* seq
     x->slot_of.emplace(seq_ids[i], slots[i]);
     fresh.push_back(i);
   }
+  // From here on a failure leaves the call's sequences without a usable
+  // state (a known sequence has given back its KV pages, and its GDN state may
+  // be zeroed or half updated): every sequence of the call is retired (slot and
+  // pages freed, id forgotten), and the caller prefills it again.
+  auto retire_call = [&](gdn_status st) {
+    for (int i = 0; i < nseq; ++i) {
+      auto it = x->slot_of.find(seq_ids[i]);
+      if (it == x->slot_of.end()) continue;
+      (void)gdn_slot_free(x->pool, it->second);
+      if (x->kv) (void)gdn_kv_release(x->kv, it->second);
+      x->slot_of.erase(it);
+    }
+    return st;
+  };
+#define GDN_TRY_RETIRE(expr)                  \
+  do {                                        \
+    gdn_status st_ = (expr);                  \
+    if (st_ != GDN_OK) return retire_call(st_); \
+  } while (0)
+#define HIP_TRY_RETIRE(expr, what)                            \
+  do {                                                        \
+    hipError_t e_ = (expr);                                   \
+    if (e_ != hipSuccess) return retire_call(hfail(e_, what)); \
+  } while (0)
   if (x->kv) {
     // every prompt starts at position 0 of its slot's KV cache
-    for (int i = 0; i < nseq; ++i) GDN_TRY(gdn_kv_release(x->kv, slots[i]));
-    gdn_status st = gdn_kv_step(x->kv, nseq, slots, lens, x->stream);
-    if (st != GDN_OK) {
-      for (int k : fresh) {
-        (void)gdn_slot_free(x->pool, slots[k]);
-        x->slot_of.erase(seq_ids[k]);
-      }
-      return st;
-    }
+    for (int i = 0; i < nseq; ++i) GDN_TRY_RETIRE(gdn_kv_release(x->kv, slots[i]));
+    GDN_TRY_RETIRE(gdn_kv_step(x->kv, nseq, slots, lens, x->stream));
   }
   int32_t* cu = x->p_pre + nseq;
   int32_t* last = cu + nseq + 1;
@@ -429,32 +458,36 @@ gdn_status gdn_exec_prefill_batch(gdn_exec* x, int32_t nseq, const uint64_t* seq
   const int32_t* d_cu = x->d_pre + nseq;
   const int32_t* d_last = d_cu + nseq + 1;
   const int32_t* d_toks = d_last + nseq;
-  HIP_TRY(hipMemcpyAsync(x->d_pre, x->p_pre, sizeof(int32_t) * (3 * (size_t)nseq + 1 + total),
-                         hipMemcpyHostToDevice, x->stream),
-          "prompt copy");
-  HIP_TRY(hipEventRecord(x->pre_copied, x->stream), "prompt copy event");
-  GDN_TRY(gdn_slots_zero(x->pool, GDN_ALL_LAYERS, x->d_pre, nseq, x->stream));
+  HIP_TRY_RETIRE(hipMemcpyAsync(x->d_pre, x->p_pre,
+                                sizeof(int32_t) * (3 * (size_t)nseq + 1 + total),
+                                hipMemcpyHostToDevice, x->stream),
+                 "prompt copy");
+  HIP_TRY_RETIRE(hipEventRecord(x->pre_copied, x->stream), "prompt copy event");
+  GDN_TRY_RETIRE(gdn_slots_zero(x->pool, GDN_ALL_LAYERS, x->d_pre, nseq, x->stream));
   const int n = (int)total;
-  HIP_TRY(gdn::launch_embed(x->embed, d_toks, n, x->vocab, x->hidden, x->h, x->stream),
-          "embedding");
-  GDN_TRY(run_layers(x, n, true, nseq));
+  HIP_TRY_RETIRE(gdn::launch_embed(x->embed, d_toks, n, x->vocab, x->hidden, x->h, x->stream),
+                 "embedding");
+  GDN_TRY_RETIRE(run_layers(x, n, true, nseq));
   // final residual add + norm of every row, then each prompt's last row
-  HIP_TRY(gdn::launch_add_norm(x->h, x->stack.empty() ? nullptr : x->mix,
-                               x->stack.empty() ? nullptr : &x->pend, n, x->hidden,
-                               x->final_norm_w, x->eps, x->hn, x->stream),
-          "final norm");
+  HIP_TRY_RETIRE(gdn::launch_add_norm(x->h, x->stack.empty() ? nullptr : x->mix,
+                                      x->stack.empty() ? nullptr : &x->pend, n, x->hidden,
+                                      x->final_norm_w, x->eps, x->hn, x->stream),
+                 "final norm");
   x->pend = gdn::QPartial{};
-  HIP_TRY(gdn::launch_gather_rows(x->hn, d_last, nseq, x->hidden, x->mix, x->stream),
-          "last rows");
-  GDN_TRY(gdn_qlinear_forward(x->head, x->mix, x->hidden, nseq, x->logits, x->vocab, x->stream));
-  HIP_TRY(gdn::launch_argmax(x->logits, x->vocab, nseq, x->vocab, x->d_pv, x->d_pi, x->d_next,
-                             x->stream),
-          "argmax");
-  HIP_TRY(hipMemcpyAsync(x->p_first, x->d_next, sizeof(int32_t) * nseq, hipMemcpyDeviceToHost,
-                         x->stream),
-          "token copy");
+  HIP_TRY_RETIRE(gdn::launch_gather_rows(x->hn, d_last, nseq, x->hidden, x->mix, x->stream),
+                 "last rows");
+  GDN_TRY_RETIRE(
+      gdn_qlinear_forward(x->head, x->mix, x->hidden, nseq, x->logits, x->vocab, x->stream));
+  HIP_TRY_RETIRE(gdn::launch_argmax(x->logits, x->vocab, nseq, x->vocab, x->d_pv, x->d_pi,
+                                    x->d_next, x->stream),
+                 "argmax");
+  HIP_TRY_RETIRE(hipMemcpyAsync(x->p_first, x->d_next, sizeof(int32_t) * nseq,
+                                hipMemcpyDeviceToHost, x->stream),
+                 "token copy");
   x->logits_rows = nseq;
-  HIP_TRY(hipStreamSynchronize(x->stream), "gdn_exec_prefill sync");
+  HIP_TRY_RETIRE(hipStreamSynchronize(x->stream), "gdn_exec_prefill sync");
+#undef GDN_TRY_RETIRE
+#undef HIP_TRY_RETIRE
   for (int i = 0; i < nseq; ++i) first_tokens[i] = (uint32_t)x->p_first[i];
   return GDN_OK;
 }

@@ -152,6 +152,25 @@ gdn_status gdn_kv_create(const gdn_kv_desc* desc, gdn_kv** out) {
     return kfail(GDN_ERR_OOM, "gdn_kv_create: %d layers x %d pages of %zu bytes", d.num_layers,
                  d.num_pages, page_bytes);
   }
+  // The attention workspace of any decode step (one token per sequence),
+  // sized once: n <= min(max_step_tokens, num_slots) sequences, each
+  // segment's keys cut into chunks of C blocks. Sequences hold distinct
+  // pages, so their blocks add up to at most 4 per page in the cache plus
+  // one partial block each: chunks <= Hkv (n + (4 num_pages + 2 n) / C + 2).
+  // A step with prompts (several tokens of one sequence, each group of them
+  // reading the shared prefix) can need more and then grows it.
+  {
+    const int64_t n = d.max_step_tokens < d.num_slots ? d.max_step_tokens : d.num_slots;
+    const int64_t chunks =
+        (int64_t)d.num_kv_heads * (n + (4 * (int64_t)d.num_pages + 2 * n) / gdn::attn_chunk_blocks() + 2);
+    const size_t ws = gdn::attn_workspace_bytes((int)n, d.num_q_heads, chunks);
+    if (hipMalloc(&kv->workspace, ws) != hipSuccess) {
+      (void)hipGetLastError();
+      kv_release_all(kv);
+      return kfail(GDN_ERR_OOM, "gdn_kv_create: attention workspace of %zu bytes", ws);
+    }
+    kv->ws_bytes = ws;
+  }
   kv->free_pages.resize(d.num_pages);
   for (int i = 0; i < d.num_pages; ++i) kv->free_pages[i] = d.num_pages - 1 - i;  // pop lowest first
   kv->len.assign(d.num_slots, 0);

@@ -243,3 +243,44 @@ def test_hybrid_descriptor_checks(hybrid):
     ex.close()
     for layer in layers:
         layer.close()
+
+
+def test_hybrid_failed_restart_changes_nothing(hybrid):
+    """A restart (prefill of a known sequence) that the KV cache cannot hold
+    fails before anything changes: the sequence keeps its slot, pages and
+    state, and decodes on exactly as in a twin run without the failed call.
+    An executor whose max_prompt exceeds one slot's KV pages is refused."""
+    import gdn_amd
+    say("gdn_exec hybrid", "failed restart, max_prompt vs pages per slot")
+    pool = gdn_amd.Pool(2, 4, HK, HV)
+    kv = gdn_amd.KVCache(2, 4, 16, 2, HQ, HKV, max_step_tokens=200)  # 128 tokens per slot
+    attn = [(p, a["qkv"], a["o"], a["qn"], a["kn"]) for p, a in zip(POS, hybrid.attn)]
+    with pytest.raises(gdn_amd.GdnError):
+        gdn_amd.Executor(pool, hybrid.gdn_layers(pool), [dev(w) for w in hybrid.in_norm],
+                         dev(hybrid.final_norm), dev(hybrid.embed), hybrid.head, EPS, 2, 200,
+                         attn_layers=attn, kv=kv, rope_theta=THETA, rotary_dim=ROT)
+    rng = np.random.default_rng(1260)
+    pa = [int(t) for t in rng.integers(0, VOCAB, 100)]   # 2 pages
+    pb = [int(t) for t in rng.integers(0, VOCAB, 150)]   # 3 pages
+    long_prompt = [int(t) for t in rng.integers(0, VOCAB, 160)]
+    runs = []
+    for fail in (False, True):
+        pool, kv, ex = hybrid.executor(4, max_batch=2, max_prompt=160, pages=5)
+        toks = [ex.prefill(1, pa), ex.prefill(2, pb)]
+        out = []
+        for _ in range(8):
+            toks = ex.decode_batch([1, 2], toks)
+            out.append(tuple(toks))
+        slot_a = ex.slot(1)
+        if fail:
+            # needs 3 pages; free 0 + the 2 sequence 1 gives back
+            with pytest.raises(gdn_amd.GdnError):
+                ex.prefill(1, long_prompt)
+            assert ex.slot(1) == slot_a and pool.slots_in_use() == 2 and kv.free_pages() == 0
+        for _ in range(8):
+            toks = ex.decode_batch([1, 2], toks)
+            out.append(tuple(toks))
+        assert pool.check() == 0
+        runs.append(out)
+        ex.close()
+    assert runs[0] == runs[1]
