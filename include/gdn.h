@@ -213,6 +213,22 @@ gdn_status gdn_prefill_varlen(gdn_pool* pool, int32_t layer, const int32_t* slot
                               const float* dt_bias, const uint16_t* conv_w,
                               uint16_t* y, void* stream);
 
+/* gdn_prefill_varlen for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops that forbid hipMalloc). No
+ * counterpart in the reference. Same arguments, kernels and results; the
+ * workspace is a fixed 16 MiB array per device held by the library until the
+ * process ends, instead of the pool's grown buffer. A call whose workspace
+ * (16,576 bytes per token at 16 key / 32 value heads: up to 1012 tokens)
+ * exceeds it fails with GDN_ERR_INVALID before any launch. Allocates nothing
+ * (hipMalloc, hipFree or otherwise). Every call on a device shares that
+ * array: calls that overlap on one device race, so order them on one stream. */
+gdn_status gdn_prefill_varlen_noalloc(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
+                                      const int32_t* cu_seqlens, int32_t nseq,
+                                      int32_t total_tokens, const uint16_t* mixed_qkv,
+                                      const uint16_t* ab, const float* A_log,
+                                      const float* dt_bias, const uint16_t* conv_w,
+                                      uint16_t* y, void* stream);
+
 /* gdn_prefill_varlen on merged projection rows with the RMSNormGated epilogue
  * fused into the chunk kernel's readout (qwen3_5.rs:660-665 after the S>1
  * path): out [total_tokens, Hv, Dv] = silu(z) * rms_norm(y, norm_w, norm_eps)

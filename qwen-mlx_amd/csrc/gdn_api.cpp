@@ -460,7 +460,8 @@ static gdn_status prefill_common(gdn_pool* pool, int32_t layer, const int32_t* s
                                  const uint16_t* qkv, int64_t xstride, const uint16_t* ab,
                                  int64_t ab_stride, const float* A_log, const float* dt_bias,
                                  const uint16_t* conv_w, uint16_t* y, const uint16_t* norm_w,
-                                 float norm_eps, uint16_t* out, void* stream, const char* who) {
+                                 float norm_eps, uint16_t* out, void* stream, const char* who,
+                                 bool noalloc = false) {
   gdn_status st = check_layer(pool, layer, false);
   if (st) return st;
   if (nseq < 0 || total_tokens < 0)
@@ -481,9 +482,25 @@ static gdn_status prefill_common(gdn_pool* pool, int32_t layer, const int32_t* s
     return fail(GDN_ERR_INVALID, "%s: token rows must be 16-byte aligned (pointer %% 16 == 0, "
                 "row stride %% 8 == 0)", who);
   DeviceGuard guard(pool->d.device);
-  st = ensure_workspace(pool, gdn::prefill_workspace_bytes(pool->R, pool->d.num_k_heads, total_tokens),
-                        stream, "prefill");
-  if (st) return st;
+  const size_t need = gdn::prefill_workspace_bytes(pool->R, pool->d.num_k_heads, total_tokens);
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  if (noalloc) {
+    ws_bytes = gdn::noalloc_scratch_bytes();
+    if (need > ws_bytes)
+      return fail(GDN_ERR_INVALID,
+                  "%s: %d tokens need %zu bytes of workspace; its fixed scratch holds %zu "
+                  "(%zu bytes per token at these head counts)",
+                  who, total_tokens, need, ws_bytes,
+                  gdn::prefill_workspace_bytes(pool->R, pool->d.num_k_heads, 1));
+    hipError_t e = gdn::noalloc_scratch(&ws);
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+  } else {
+    st = ensure_workspace(pool, need, stream, "prefill");
+    if (st) return st;
+    ws = pool->workspace;
+    ws_bytes = pool->workspace_bytes;
+  }
   gdn::PrefillArgs a{};
   a.R = pool->R;
   a.Hk = pool->d.num_k_heads;
@@ -506,8 +523,8 @@ static gdn_status prefill_common(gdn_pool* pool, int32_t layer, const int32_t* s
   a.norm_eps = norm_eps;
   a.out = out;
   a.status = pool->d_status;
-  a.workspace = pool->workspace;
-  a.workspace_bytes = pool->workspace_bytes;
+  a.workspace = ws;
+  a.workspace_bytes = ws_bytes;
   a.stream = as_stream(stream);
   hipError_t e = gdn::launch_prefill(a);
   if (e != hipSuccess) return hip_fail(e, who);
@@ -524,6 +541,19 @@ gdn_status gdn_prefill_varlen(gdn_pool* pool, int32_t layer, const int32_t* slot
   return prefill_common(pool, layer, slot_ids, cu_seqlens, nseq, total_tokens, mixed_qkv,
                         pool ? pool->D : 0, ab, pool ? 2 * pool->d.num_v_heads : 0, A_log, dt_bias,
                         conv_w, y, nullptr, 0.0f, nullptr, stream, "gdn_prefill_varlen");
+}
+
+gdn_status gdn_prefill_varlen_noalloc(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
+                                      const int32_t* cu_seqlens, int32_t nseq,
+                                      int32_t total_tokens, const uint16_t* mixed_qkv,
+                                      const uint16_t* ab, const float* A_log, const float* dt_bias,
+                                      const uint16_t* conv_w, uint16_t* y, void* stream) {
+  if (!y && total_tokens > 0 && nseq > 0)
+    return fail(GDN_ERR_INVALID, "gdn_prefill_varlen_noalloc: NULL token tensor");
+  return prefill_common(pool, layer, slot_ids, cu_seqlens, nseq, total_tokens, mixed_qkv,
+                        pool ? pool->D : 0, ab, pool ? 2 * pool->d.num_v_heads : 0, A_log, dt_bias,
+                        conv_w, y, nullptr, 0.0f, nullptr, stream, "gdn_prefill_varlen_noalloc",
+                        true);
 }
 
 gdn_status gdn_prefill_varlen_gated(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,

@@ -241,6 +241,9 @@ hipError_t launch_slots(const SlotArgs& a);
 hipError_t launch_validate(const int32_t* slot_ids, int n, int num_slots, uint32_t* status,
                            hipStream_t stream);
 size_t prefill_workspace_bytes(int R, int Hk, int total_tokens);
+// Fixed per-device workspace of gdn_prefill_varlen_noalloc (gdn_prefill.hip).
+size_t noalloc_scratch_bytes();
+hipError_t noalloc_scratch(void** out);
 hipError_t launch_prefill(const PrefillArgs& a);
 
 // Attention step on the paged KV cache (gdn_attn.hip).

@@ -11,6 +11,8 @@
 // Workspace layout (each region 256-byte aligned):
 //   qn [T,Hk,Dk] bf16 | kn [T,Hk,Dk] bf16 | vc [T,Hv,Dv] bf16 | beta [T,Hv] bf16 | lg [T,Hv] f32
 
+#include <mutex>
+
 #include "gdn_common.h"
 
 namespace gdn {
@@ -658,6 +660,37 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
 
 size_t prefill_workspace_bytes(int R, int Hk, int total_tokens) {
   return carve(nullptr, R, Hk, total_tokens, nullptr);
+}
+
+// ---------------------------------------------------- no-allocation scratch --
+// Workspace of gdn_prefill_varlen_noalloc: one fixed array per device, in
+// place of the pool's grown workspace. Every call on a device shares it and
+// finds the previous call's contents (the prefill writes every workspace byte
+// it reads, so nothing needs clearing); calls that overlap on one device race.
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+size_t noalloc_scratch_bytes() { return kNoAllocScratchBytes; }
+
+// The device address of `scratch` on the current device, looked up once per
+// device (the host-side name of the array is not a device address).
+hipError_t noalloc_scratch(void** out) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* ptrs[kMaxDevices] = {};
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    ptrs[dev] = p;
+  }
+  *out = ptrs[dev];
+  return hipSuccess;
 }
 
 template <int R>

@@ -51,6 +51,8 @@ SIGNATURES = {
                           _VP, _VP, _VP, ctypes.c_float, _VP, _VP, _VP], ctypes.c_int),
     "gdn_prefill_varlen": ([_VP, _I32, _VP, _VP, _I32, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _VP],
                            ctypes.c_int),
+    "gdn_prefill_varlen_noalloc": ([_VP, _I32, _VP, _VP, _I32, _I32, _VP, _VP, _VP, _VP, _VP, _VP,
+                                    _VP], ctypes.c_int),
     "gdn_prefill_varlen_gated": ([_VP, _I32, _VP, _VP, _I32, _I32, _VP, ctypes.c_int64, _VP,
                                   ctypes.c_int64, _VP, _VP, _VP, _VP, ctypes.c_float, _VP, _VP,
                                   _VP], ctypes.c_int),
@@ -311,6 +313,16 @@ class Pool:
                                            slot_ids.numel(), total_tokens, _ptr(mixed_qkv),
                                            _ptr(ab), _ptr(A_log), _ptr(dt_bias), _ptr(conv_w),
                                            _ptr(y), _stream(stream)))
+
+    def prefill_noalloc(self, layer, slot_ids, cu_seqlens, total_tokens, mixed_qkv, ab, A_log,
+                        dt_bias, conv_w, y, stream=None):
+        """prefill with the library's fixed per-device scratch as its workspace
+        (gdn_prefill_varlen_noalloc): no device allocation, bounded size."""
+        _check(self.lib.gdn_prefill_varlen_noalloc(self.handle, layer, _ptr(slot_ids),
+                                                   _ptr(cu_seqlens), slot_ids.numel(),
+                                                   total_tokens, _ptr(mixed_qkv), _ptr(ab),
+                                                   _ptr(A_log), _ptr(dt_bias), _ptr(conv_w),
+                                                   _ptr(y), _stream(stream)))
 
     def prefill_gated(self, layer, slot_ids, cu_seqlens, total_tokens, qkvz, ab, A_log, dt_bias,
                       conv_w, norm_w, norm_eps, out, y=None, stream=None):

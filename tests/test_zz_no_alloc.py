@@ -1,0 +1,68 @@
+"""GPU test of gdn_prefill_varlen_noalloc (the prefill with a fixed per-device
+scratch workspace) against gdn_prefill_varlen on twin pools: outputs and the
+slots' recurrent and conv states bit-identical, over two calls in a row, the
+second smaller; oversized calls are refused on the host."""
+import numpy as np
+import pytest
+
+from gdn_testlib import DK, DV, K, dev, gen_layer_params, gen_states, gen_tokens, host, say
+
+pytestmark = pytest.mark.gpu
+
+HK, HV = 16, 32
+
+
+def _ids(lst):
+    return dev(np.asarray(lst, np.int32))
+
+
+def _call(pool, noalloc, slots, lens, x, ab, p, gpu):
+    import torch
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    total = int(cu[-1])
+    y = torch.zeros((total, HV, DV), dtype=torch.int16, device=gpu)
+    fn = pool.prefill_noalloc if noalloc else pool.prefill
+    fn(0, _ids(slots), dev(cu), total, dev(x), dev(ab), dev(p["A_log"]), dev(p["dt_bias"]),
+       dev(p["conv_w"]), y)
+    s = torch.empty((len(slots), HV, DV, DK), dtype=torch.float32, device=gpu)
+    c = torch.empty((len(slots), K - 1, pool.D), dtype=torch.int16, device=gpu)
+    pool.read(0, _ids(slots), s, c)
+    torch.cuda.synchronize()
+    return host(y), host(s), host(c)
+
+
+def test_noalloc_prefill_matches_prefill(gpu):
+    import torch
+    import gdn_amd
+    rng = np.random.default_rng(1400)
+    p = gen_layer_params(rng, HK, HV)
+    pools = [gdn_amd.Pool(1, 12, HK, HV) for _ in range(2)]
+    slots = [9, 2, 5, 11]
+    st, cs = gen_states(rng, len(slots), HK, HV)
+    for pool in pools:
+        pool.write(0, _ids(slots), dev(st), dev(cs))
+    # two calls in a row on the same slots, the second smaller
+    for lens in ([70, 300, 5, 129], [33, 2, 64, 1]):
+        say("gdn_prefill_varlen_noalloc", f"lens={lens}")
+        x, ab = gen_tokens(rng, int(sum(lens)), HK, HV)
+        ya, sa, ca = _call(pools[0], False, slots, lens, x, ab, p, gpu)
+        yb, sb, cb = _call(pools[1], True, slots, lens, x, ab, p, gpu)
+        assert np.array_equal(ya, yb)
+        assert np.array_equal(sa, sb)
+        assert np.array_equal(ca, cb)
+    # a call beyond the fixed scratch fails before any launch, changing nothing
+    big = 1013
+    x, ab = gen_tokens(rng, big, HK, HV)
+    ybig = torch.zeros((big, HV, DV), dtype=torch.int16, device=gpu)
+    with pytest.raises(gdn_amd.GdnError, match="scratch"):
+        pools[1].prefill_noalloc(0, _ids([3]), dev(np.array([0, big], np.int32)), big, dev(x),
+                                 dev(ab), dev(p["A_log"]), dev(p["dt_bias"]), dev(p["conv_w"]),
+                                 ybig)
+    s = torch.empty((len(slots), HV, DV, DK), dtype=torch.float32, device=gpu)
+    c = torch.empty((len(slots), K - 1, pools[1].D), dtype=torch.int16, device=gpu)
+    pools[1].read(0, _ids(slots), s, c)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(s), sb) and np.array_equal(host(c), cb)
+    for pool in pools:
+        assert pool.check() == 0
+        pool.close()
