@@ -57,6 +57,11 @@ def parse_args(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (PMC byte-count calibration)")
+    ap.add_argument("--no-placement", action="store_true",
+                    help="skip the contiguous-slot timing of the same kernel")
+    ap.add_argument("--placement-steps", type=int, default=16)
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="skip the prefill sub-measurement of the default run")
     ap.add_argument("--prefill", action="store_true",
                     help="measure the chunked varlen prefill instead: 8 sequences x 16384 "
                          "tokens per layer over --layers layers")
@@ -143,18 +148,19 @@ PREFILL_FLOP_PER_TOKEN_HEAD_SEQ = 7 * DK * DK
 PEAK_BF16_TFLOPS = 2500.0
 
 
-def prefill_bench(args):
-    """Chunked varlen prefill: `prefill_seqs` sequences of `prefill_len`
-    tokens packed in one gdn_prefill_varlen call per layer, from zeroed slots,
-    inputs resident in HBM. Prints one JSON line."""
+def prefill_measure(L, n, P, seed=0, reps=1):
+    """Chunked varlen prefill: n sequences of P tokens packed in one
+    gdn_prefill_varlen call per layer, L layers, from zeroed slots, inputs
+    resident in HBM. Returns (wall seconds, GPU seconds per pass, status
+    flags); the GPU time comes from HIP events on the launch stream around
+    each pass of L calls (3 launches each: qkv, conv state, chunk kernel)."""
     import torch
 
     import gdn_amd
     dev = torch.device("cuda:0")
-    L, n, P = args.layers, args.prefill_seqs, args.prefill_len
     total = n * P
     pool = gdn_amd.Pool(L, n, HK, HV)
-    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    gen = torch.Generator(device=dev).manual_seed(seed)
     bf = torch.bfloat16
     conv_w = [(torch.randn((D, KW), generator=gen, device=dev) * 0.25).to(bf) for _ in range(L)]
     A_log = [torch.rand(HV, generator=gen, device=dev) * math.log(16.0) for _ in range(L)]
@@ -166,48 +172,73 @@ def prefill_bench(args):
     ids = torch.arange(n, dtype=torch.int32, device=dev)
     cu = torch.arange(n + 1, dtype=torch.int32, device=dev) * P
 
-    def run_layers():
+    def run_layers(events=None):
         pool.zero(-1, ids)
+        if events:
+            events[0].record()
         for l in range(L):
             pool.prefill(l, ids, cu, total, x[l % nsets], ab[l % nsets], A_log[l], dt_bias[l],
                          conv_w[l], y)
+        if events:
+            events[1].record()
 
     run_layers()  # warmup (also grows the workspace)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(reps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    e0.record()
-    run_layers()
-    e1.record()
+    for e in ev:
+        run_layers(e)
     torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    gpu_s = e0.elapsed_time(e1) * 1e-3
-    flops = PREFILL_FLOP_PER_TOKEN_HEAD * total * HV * L
-    tflops = flops / gpu_s / 1e12
+    elapsed = (time.perf_counter() - t0) / reps
+    gpu_s = sum(a.elapsed_time(b) for a, b in ev) * 1e-3 / reps
+    flags = pool.check()
+    pool.close()
+    del x, ab, y
+    torch.cuda.empty_cache()
+    return elapsed, gpu_s, flags
+
+
+def prefill_summary(L, n, P, elapsed, gpu_s):
+    total = n * P
+    tflops = PREFILL_FLOP_PER_TOKEN_HEAD * total * HV * L / gpu_s / 1e12
+    return {
+        "workload": f"{n} x {P}-token prefills packed per layer, {L} layers, chunk 64",
+        "tokens_per_s": round(total / elapsed, 1),
+        "ms_per_layer": round(gpu_s * 1e3 / L, 4),
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                     "flop_per_token_head": round(PREFILL_FLOP_PER_TOKEN_HEAD, 1),
+                     "achieved_min_count": round(tflops * PREFILL_FLOP_PER_TOKEN_HEAD_MIN
+                                                 / PREFILL_FLOP_PER_TOKEN_HEAD, 2),
+                     "flop_per_token_head_min": PREFILL_FLOP_PER_TOKEN_HEAD_MIN,
+                     "flop_per_token_head_sequential": PREFILL_FLOP_PER_TOKEN_HEAD_SEQ,
+                     "timing": "HIP events around each pass of L gdn_prefill_varlen calls "
+                               "(qkv, conv-state and chunk launches)"},
+    }
+
+
+def prefill_bench(args):
+    """The chunked prefill alone; prints one JSON line."""
+    L, n, P = args.layers, args.prefill_seqs, args.prefill_len
+    elapsed, gpu_s, flags = prefill_measure(L, n, P, args.seed, reps=2)
+    if flags:
+        print(f"pool status flags 0x{flags:x}", file=sys.stderr)
+        return 1
+    summ = prefill_summary(L, n, P, elapsed, gpu_s)
     out = {
         "metric": "GDN chunked prefill tokens/s (packed varlen, all layers)",
-        "value": round(total / elapsed, 1),
+        "value": summ["tokens_per_s"],
         "unit": "tokens/s",
         "n_gpus": 1,
         "ms_per_step": round(elapsed * 1e3, 3),
         "higher_is_better": True,
         "dtype": "bf16 MFMA products, f32 state",
         "data": "synthetic",
-        "config": {"workload": f"{n} x {P}-token prefills per layer, {L} layers, chunk 64",
-                   "layers": L, "sequences": n, "tokens_per_sequence": P},
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
-                     "flop_per_token_head": PREFILL_FLOP_PER_TOKEN_HEAD,
-                     "achieved_min_count": round(tflops * PREFILL_FLOP_PER_TOKEN_HEAD_MIN
-                                                 / PREFILL_FLOP_PER_TOKEN_HEAD, 2),
-                     "flop_per_token_head_min": PREFILL_FLOP_PER_TOKEN_HEAD_MIN,
-                     "flop_per_token_head_sequential": PREFILL_FLOP_PER_TOKEN_HEAD_SEQ,
-                     "note": "all prefill launches (conv, norm/gates, chunk recurrence)"},
+        "config": {"workload": summ["workload"], "layers": L, "sequences": n,
+                   "tokens_per_sequence": P},
+        "roofline": summ["roofline"],
     }
-    flags = pool.check()
-    if flags:
-        print(f"pool status flags 0x{flags:x}", file=sys.stderr)
-        return 1
     print(json.dumps(out), flush=True)
     return 0
 
@@ -728,24 +759,25 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(seconds: float):
+def cpu_baseline(seconds: float, layers: int = 30, batch: int = 64):
     """Oracle restatement of the reference step (stack copy, out-of-place
-    kernel, unstack as views) on the measured shape -- B=64, 30 layers --
-    timed on this host for a bounded number of steps."""
+    kernel, unstack as views) on the measured shape -- B=64, 30 layers -- or
+    another (layers, batch), timed on this host for a bounded number of
+    steps."""
     from oracle import oracle as O
-    Bc = 64
-    bs = O.BaselineStep(30, Bc, HK, HV, DK, DV, KW, seed=1)
+    Bc = batch
+    bs = O.BaselineStep(layers, Bc, HK, HV, DK, DV, KW, seed=1)
     bs.step()  # first touch of the output buffers
     n, t0 = 0, time.perf_counter()
     while True:
         bs.step()
         n += 1
         el = time.perf_counter() - t0
-        if (el >= seconds and n >= 3) or n >= 1000:
+        if (el >= seconds and n >= 3) or n >= 100000:
             break
     return {"value": round(Bc * n / el, 2), "unit": "tokens/s", "cores": O.num_threads(),
             "kind": "port",
-            "sample": f"B={Bc} sequences x 30 GDN layers x {n} decode steps ({el:.1f} s), "
+            "sample": f"B={Bc} sequences x {layers} GDN layers x {n} decode steps ({el:.1f} s), "
                       f"OpenMP over (b, hv), {O.num_threads()} threads of {os.cpu_count()} "
                       f"logical CPUs, {_cpu_model()}"}
 
@@ -806,6 +838,45 @@ def main(argv=None):
     if flags:
         print(f"pool status flags 0x{flags:x}", file=sys.stderr)
         return 1
+    # The same 64 sequences' kernel time when they sit in slots 0..63
+    # (contiguous), in the same run: the scattered placement above is the
+    # measured workload, this one shows what the placement costs.
+    placement = None
+    if not args.no_placement:
+        import torch as _t
+        w.d_ids.copy_(_t.arange(args.batch, dtype=_t.int32))
+        w.args.churn_every = 0
+        for _ in range(4):
+            w.step()
+        pev = [(_t.cuda.Event(enable_timing=True), _t.cuda.Event(enable_timing=True))
+               for _ in range(args.placement_steps)]
+        _t.cuda.synchronize()
+        for i in range(args.placement_steps):
+            w.step(pev[i])
+        _t.cuda.synchronize()
+        c_ms = sum(a.elapsed_time(b) for a, b in pev) / (args.placement_steps * args.layers)
+        c_gbs = launch_bytes / (c_ms * 1e-3) / 1e9
+        placement = {
+            "scattered_slots_kernel_avg_us": round(avg_ms * 1e3, 2),
+            "contiguous_slots_kernel_avg_us": round(c_ms * 1e3, 2),
+            "contiguous_slots_frac": round(c_gbs / PEAK_HBM_GBS, 4),
+            "note": "same 64 sequences and kernel, slots 0..63, no churn, "
+                    f"{args.placement_steps} steps",
+        }
+        if w.pool.check():
+            print("pool status flags after the placement run", file=sys.stderr)
+            return 1
+    prefill = None
+    if not args.no_prefill:
+        del w
+        import torch as _t
+        _t.cuda.empty_cache()
+        p_el, p_gpu, p_flags = prefill_measure(args.layers, args.prefill_seqs, args.prefill_len,
+                                               args.seed, reps=2)
+        if p_flags:
+            print(f"prefill pool status flags 0x{p_flags:x}", file=sys.stderr)
+            return 1
+        prefill = prefill_summary(args.layers, args.prefill_seqs, args.prefill_len, p_el, p_gpu)
     out = {
         "metric": METRIC,
         "value": round(tok_s, 1),
@@ -843,8 +914,14 @@ def main(argv=None):
         "state_traffic_gbs_whole_step": round(args.batch * args.layers * STATE_BYTES /
                                               (elapsed / args.steps) / 1e9, 1),
     }
+    if placement is not None:
+        out["placement"] = placement
+    if prefill is not None:
+        out["prefill"] = prefill
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        # the reference's CPU-runnable case: one layer, one sequence
+        out["cpu_baseline_1layer_b1"] = cpu_baseline(min(3.0, args.cpu_seconds), 1, 1)
     print(json.dumps(out), flush=True)
     return 0
 
