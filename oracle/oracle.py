@@ -7,6 +7,9 @@ does.
 bf16 tensors are numpy uint16 arrays holding the raw bit patterns. Every
 function returns new arrays and leaves its inputs untouched. The restated
 reference lines are cited in gdn_oracle.c next to each C function.
+StackForward (at the end) composes these pieces into the executor's decoder
+stack; its composition is pinned by a closed form (mixers with zero output
+weights leave lm_head(rms_norm(embed))) and by prefill / decode continuity.
 """
 from __future__ import annotations
 
@@ -408,3 +411,86 @@ def attention_step(q_full, k, v, q_norm_w, k_norm_w, eps: float, theta: float, r
             ob = bf16_to_f32(f64_to_bf16_array(o)).astype(np.float64)
             out[i, h] = f64_to_bf16_array(ob * sg[i, h])
     return out.reshape(S, Hq * hd), ck, cv
+
+
+class StackForward:
+    """The executor's decoder stack, composed from this module's pieces: the
+    Qwen3.5 decoder without its MLPs, one sequence at a time.
+
+      h = embed[tokens]                                   (qwen3_5.rs:835-855)
+      per layer: h = bf16(h + mixer(rms_norm(h, in_norm)))  (qwen3_5.rs:723-743,
+                                                           MLP half left out)
+      logits = lm_head(rms_norm(h, final_norm))             (qwen3_5.rs:861-874)
+
+    A GatedDeltaNet mixer (qwen3_5.rs:558-668): the merged 4-bit projections
+    (q|k|v, z, b, a; :572-586), the S=1 step (`decode`, :593-610) for one
+    token or the sequence form (`prefill`, :611-658) for several (the
+    reference picks by the call's token count), RMSNormGated (`norm_gate`,
+    :660-665) and out_proj (:668). An attention mixer (qwen3_5.rs:377-455):
+    the q|gate, k, v projection, `attention_step` with the sequence's growing
+    K/V (:419-424) and o_proj. Every 4-bit product is `qmatmul_w4` (exact,
+    rounded once to bf16).
+
+    layers: stack order; each a dict with "in_norm" and either
+      {"in_parts": [(w, s, b)] x 4 (q|k|v, z, b, a), "out": (w, s, b), "A_log",
+       "dt_bias", "conv_w", "norm_w"}  (GatedDeltaNet), or
+      {"qkv": (w, s, b), "o": (w, s, b), "qn", "kn"}  (attention).
+    Test infrastructure: host numpy arrays, float64 where not rounded."""
+
+    def __init__(self, layers, final_norm_w, embed, head, eps, Hk, Hv, Hq=16, Hkv=2,
+                 theta=1.0e7, rot_dim=64, Dk=128, Dv=128, K=4):
+        self.layers, self.final_norm_w, self.embed, self.head = layers, final_norm_w, embed, head
+        self.eps, self.Hk, self.Hv, self.Hq, self.Hkv = eps, Hk, Hv, Hq, Hkv
+        self.theta, self.rot_dim, self.Dk, self.Dv, self.K = theta, rot_dim, Dk, Dv, K
+        self.D = 2 * Hk * Dk + Hv * Dv
+        self.seqs = {}
+
+    def _fresh(self):
+        st = []
+        for L in self.layers:
+            if "in_parts" in L:
+                st.append([np.zeros((self.K - 1, self.D), np.uint16),
+                           np.zeros((self.Hv, self.Dv, self.Dk), np.float32)])
+            else:
+                st.append([np.zeros((self.Hkv, 0, 256), np.uint16),
+                           np.zeros((self.Hkv, 0, 256), np.uint16)])
+        return st
+
+    def forward(self, sid, tokens, fresh=False):
+        """Run `tokens` of sequence `sid` (a new sequence when fresh) and return
+        the last token's logits: (bf16 [vocab], exact float64 [vocab])."""
+        if fresh or sid not in self.seqs:
+            self.seqs[sid] = self._fresh()
+        st = self.seqs[sid]
+        toks = np.asarray(tokens, np.int64)
+        S = len(toks)
+        h = np.asarray(self.embed, np.uint16)[toks]
+        Hv, Dv, D = self.Hv, self.Dv, self.D
+        for L, ls in zip(self.layers, st):
+            hn = rms_norm_w(h, L["in_norm"], self.eps)
+            if "in_parts" in L:
+                proj = np.concatenate([qmatmul_w4(hn, *p)[0] for p in L["in_parts"]], axis=1)
+                mixed, z, ab = proj[:, :D], proj[:, D:D + Hv * Dv], proj[:, D + Hv * Dv:]
+                if S == 1:
+                    y, cs, ss = decode(ls[0][None], ls[1][None], mixed, ab, L["A_log"],
+                                       L["dt_bias"], L["conv_w"], self.Hk, Hv)
+                    ls[0], ls[1] = cs[0], ss[0]
+                else:
+                    y, ls[0], ls[1] = prefill(ls[0], ls[1], mixed, ab, L["A_log"], L["dt_bias"],
+                                              L["conv_w"], self.Hk, Hv)
+                g = norm_gate(y.reshape(S, Hv, Dv), z.reshape(S, Hv, Dv), L["norm_w"], self.eps)
+                d = qmatmul_w4(g.reshape(S, Hv * Dv), *L["out"])[0]
+            else:
+                qkv = qmatmul_w4(hn, *L["qkv"])[0]
+                nq, nk = self.Hq * 512, self.Hkv * 256
+                att, ls[0], ls[1] = attention_step(qkv[:, :nq], qkv[:, nq:nq + nk],
+                                                   qkv[:, nq + nk:nq + 2 * nk], L["qn"], L["kn"],
+                                                   self.eps, self.theta, self.rot_dim, ls[0],
+                                                   ls[1], self.Hq, self.Hkv)
+                d = qmatmul_w4(att, *L["o"])[0]
+            # residual add of two bf16 arrays: the exact sum rounded once
+            h = f64_to_bf16_array(bf16_to_f32(h).astype(np.float64) +
+                                  bf16_to_f32(d).astype(np.float64))
+        hn = rms_norm_w(h[-1:], self.final_norm_w, self.eps)
+        y, ye, _ = qmatmul_w4(hn, *self.head)
+        return y[0], ye[0]

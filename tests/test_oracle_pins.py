@@ -624,3 +624,68 @@ def test_attention_step_score_scale_and_softmax():
     gate = O.bf16_to_f32(q.reshape(1, 2, hd)[:, 1]).astype(np.float64)
     sg = O.bf16_to_f32(O.f64_to_bf16_array(1 / (1 + np.exp(-gate))))
     assert np.array_equal(out, O.f64_to_bf16_array(o * sg))
+
+
+def _tiny_stack(rng, zero_mixers=False, hidden=128, vocab=256, Hk=1, Hv=2, Hq=2, Hkv=1):
+    """A two-layer stack (GatedDeltaNet, attention) at tiny sizes for the
+    composition pins of O.StackForward."""
+    from gdn_testlib import quantize_w4
+
+    def q4(n, k, scale=0.05):
+        wf = rng.standard_normal((n, k)) * scale
+        return quantize_w4(np.zeros_like(wf) if zero_mixers else wf)
+
+    def bfw(n, s=0.1):
+        return O.f32_to_bf16((1 + s * rng.standard_normal(n)).astype(np.float32))
+
+    D = conv_dim(Hk, Hv)
+    p = gen_layer_params(rng, Hk, Hv)
+    gdn = dict(in_parts=[quantize_w4(rng.standard_normal((n, hidden)) * 0.05)
+                         for n in (D, Hv * DV, Hv, Hv)],
+               out=q4(hidden, Hv * DV), A_log=p["A_log"], dt_bias=p["dt_bias"],
+               conv_w=p["conv_w"], norm_w=bfw(DV), in_norm=bfw(hidden))
+    attn = dict(qkv=quantize_w4(rng.standard_normal((Hq * 512 + 2 * Hkv * 256, hidden)) * 0.05),
+                o=q4(hidden, Hq * 256), qn=bfw(256), kn=bfw(256), in_norm=bfw(hidden))
+    embed = O.f32_to_bf16(rng.standard_normal((vocab, hidden)).astype(np.float32))
+    head = quantize_w4(rng.standard_normal((vocab, hidden)) * 0.05)
+    return O.StackForward([gdn, attn], bfw(hidden), embed, head, 1e-6, Hk, Hv, Hq=Hq, Hkv=Hkv)
+
+
+def test_stack_forward_with_zero_mixers_is_head_of_embedding():
+    """Mixers whose output projections are zero add nothing to the residual
+    stream: the logits are lm_head(rms_norm(embed[token])) of the last token,
+    whatever the prompt before it."""
+    rng = np.random.default_rng(80)
+    st = _tiny_stack(rng, zero_mixers=True)
+    toks = [int(t) for t in rng.integers(0, 256, 9)]
+    y, ye = st.forward(1, toks, fresh=True)
+    hn = O.rms_norm_w(np.asarray(st.embed)[toks[-1:]], st.final_norm_w, st.eps)
+    y2, ye2, _ = O.qmatmul_w4(hn, *st.head)
+    assert np.array_equal(y, y2[0]) and np.array_equal(ye, ye2[0])
+    y3, _ = st.forward(1, toks[:1])   # one more token on the same sequence
+    hn = O.rms_norm_w(np.asarray(st.embed)[toks[:1]], st.final_norm_w, st.eps)
+    assert np.array_equal(y3, O.qmatmul_w4(hn, *st.head)[0][0])
+
+
+def test_stack_forward_prefill_then_decode_continues_the_sequence():
+    """A prompt of n tokens followed by one decode token leaves the same
+    logits as one pass over the n + 1 tokens, up to the S=1 conv's bf16
+    product rounding (the reference rounds each S=1 conv product, and not the
+    S>1 conv's): recurrent state, conv window, attention positions and the
+    growing K/V all carry over. A decode step that restarted the sequence, or
+    an attention step at position 0, fails it."""
+    rng = np.random.default_rng(81)
+    st = _tiny_stack(rng)
+    toks = [int(t) for t in rng.integers(0, 256, 21)]
+    st.forward(1, toks[:-1], fresh=True)
+    _, ye_a = st.forward(1, toks[-1:])
+    _, ye_b = st.forward(2, toks, fresh=True)
+    _, ye_c = st.forward(3, toks[-1:], fresh=True)   # the last token alone
+    scale = np.linalg.norm(ye_b)
+    assert np.linalg.norm(ye_a - ye_b) / scale < 1e-2
+    assert np.linalg.norm(ye_c - ye_b) / scale > 1e-1
+    # the states after both routes
+    ga, gb = st.seqs[1][0], st.seqs[2][0]
+    assert np.array_equal(ga[0], gb[0])   # conv window: the last 3 raw inputs
+    assert np.linalg.norm(ga[1] - gb[1]) / np.linalg.norm(gb[1]) < 1e-2
+    assert st.seqs[1][1][0].shape == st.seqs[2][1][0].shape == (1, 21, 256)
