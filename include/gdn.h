@@ -30,6 +30,13 @@
  *     gdn_pool_check() reads (synchronously) and clears.
  *   - Slot ids within one call must be distinct: two work-groups updating the
  *     same slot in one launch race. gdn_slots_validate() checks this on demand.
+ *     Debug switch: with the library built with -DGDN_DEBUG_SLOTS, or with the
+ *     environment variable GDN_DEBUG_SLOTS set to a value other than "0" (read
+ *     on every call), gdn_decode*, gdn_recurrent and gdn_prefill_varlen* copy
+ *     the slot list to the host, synchronize the stream and return
+ *     GDN_ERR_SLOTS for an id out of range or repeated, before any launch.
+ *     Off by default: it costs a copy and a host synchronization per call and
+ *     breaks HIP graph capture.
  *   - One pool is not reentrant: calls that touch the same slots must be
  *     ordered on one stream by the caller. gdn_prefill_varlen uses a device
  *     workspace held by the pool, so its calls on a pool must be ordered on

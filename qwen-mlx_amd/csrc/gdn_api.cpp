@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
+#include <cstdlib>
 #include <cstdio>
 #include <set>
 #include <string>
@@ -102,6 +103,42 @@ gdn_status check_layer(const gdn_pool* p, int32_t layer, bool allow_all) {
 }
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+// Debug check of a call's slot list (range and uniqueness) on the host before
+// any launch: on when the library is built with GDN_DEBUG_SLOTS defined or the
+// environment has GDN_DEBUG_SLOTS set to a value other than 0. It copies the
+// list to the host and waits for `stream`, so it is for debugging, not for
+// graph capture. Without it a repeated id races inside the kernels and an
+// out-of-range id only latches GDN_FLAG_BAD_SLOT.
+bool debug_slots_on() {
+#ifdef GDN_DEBUG_SLOTS
+  return true;
+#else
+  const char* e = getenv("GDN_DEBUG_SLOTS");
+  return e && e[0] && !(e[0] == '0' && e[1] == 0);
+#endif
+}
+
+gdn_status debug_check_slots(const gdn_pool* pool, const int32_t* slot_ids, int32_t n,
+                                    void* stream, const char* who) {
+  if (!debug_slots_on() || n <= 0) return GDN_OK;
+  std::vector<int32_t> ids(n);
+  hipError_t e = hipMemcpyAsync(ids.data(), slot_ids, sizeof(int32_t) * n,
+                                hipMemcpyDeviceToHost, as_stream(stream));
+  if (e == hipSuccess) e = hipStreamSynchronize(as_stream(stream));
+  if (e != hipSuccess) return hip_fail(e, "slot list check");
+  std::vector<uint8_t> seen(pool->d.num_slots, 0);
+  for (int32_t i = 0; i < n; ++i) {
+    const int32_t s = ids[i];
+    if (s < 0 || s >= pool->d.num_slots)
+      return fail(GDN_ERR_SLOTS, "%s: slot id %d at %d outside [0, %d)", who, s, i,
+                  pool->d.num_slots);
+    if (seen[s]) return fail(GDN_ERR_SLOTS, "%s: slot id %d appears twice", who, s);
+    seen[s] = 1;
+  }
+  return GDN_OK;
+}
+
 
 }  // namespace
 
@@ -326,6 +363,8 @@ gdn_status gdn_recurrent(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
   if (!slot_ids || !q || !k || !v || !g || !beta || !y)
     return fail(GDN_ERR_INVALID, "gdn_recurrent: NULL tensor pointer");
   DeviceGuard guard(pool->d.device);
+  st = debug_check_slots(pool, slot_ids, B, stream, "gdn_recurrent");
+  if (st) return st;
   gdn::RecurrentArgs a{};
   a.R = pool->R;
   a.Hk = pool->d.num_k_heads;
@@ -396,6 +435,8 @@ static gdn_status decode_common(gdn_pool* pool, int32_t layer, const int32_t* sl
   if (reinterpret_cast<uintptr_t>(conv_w) % 8 != 0)
     return fail(GDN_ERR_INVALID, "%s: conv_w must be 8-byte aligned", who);
   DeviceGuard guard(pool->d.device);
+  st = debug_check_slots(pool, slot_ids, B, stream, who);
+  if (st) return st;
   gdn::DecodeArgs a{};
   a.R = pool->R;
   a.Hk = pool->d.num_k_heads;
@@ -482,6 +523,8 @@ static gdn_status prefill_common(gdn_pool* pool, int32_t layer, const int32_t* s
     return fail(GDN_ERR_INVALID, "%s: token rows must be 16-byte aligned (pointer %% 16 == 0, "
                 "row stride %% 8 == 0)", who);
   DeviceGuard guard(pool->d.device);
+  st = debug_check_slots(pool, slot_ids, nseq, stream, who);
+  if (st) return st;
   const size_t need = gdn::prefill_workspace_bytes(pool->R, pool->d.num_k_heads, total_tokens);
   void* ws = nullptr;
   size_t ws_bytes = 0;
