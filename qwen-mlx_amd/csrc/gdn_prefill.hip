@@ -259,9 +259,8 @@ __global__ __launch_bounds__(256) void prefill_conv_state_kernel(
   }
 }
 
-// 3. Chunked (WY form) recurrence, one work-group of 512 threads (8 waves) per
-// (sequence, value head), walking the sequence's chunks of kC = 64 tokens. With G the cumulative log decay inside a chunk and S
-// ([Dv, Dk]) the state at the chunk start:
+// 3. Chunked (WY form) recurrence. With G the cumulative log decay inside a
+// chunk of kC = 64 tokens and S ([Dv, Dk]) the state at the chunk start:
 //   L_ij = beta_i (k_i.k_j) exp(G_i - G_j)   (j < i)
 //   P_ij = (q_i.k_j) exp(G_i - G_j)          (j <= i)
 //   R    = beta * (V - exp(G) * (K S^T))      per token row
@@ -270,106 +269,193 @@ __global__ __launch_bounds__(256) void prefill_conv_state_kernel(
 //   S^T <- exp(G_C) S^T + K^T (exp(G_C - G) * V')
 // which equals the token-by-token recurrence of metal_gdn.rs:37-62.
 //
-// Work split: waves 0-3 form K K^T (token row block w) and invert its
-// diagonal block, waves 4-7 form Q K^T; every other step runs wave-locally on
-// the wave's own 16 state rows (dv block w), so a chunk needs three
-// work-group barriers. The triangular solve works on V'
-// directly, 16-token blocks: V'_I = D_I (R_I - sum_{j<I} L_Ij V'_j) with
-// D_I = (I + L_II)^-1. A 16x16 MFMA accumulator holds row 4*(l/16) + r,
-// column l%16 of its tile in register r of lane l, which is the B-operand
-// layout of a 16-deep product: V' blocks and state tiles feed the next
-// products without data movement. k and q are bf16 (exact operands); f32
-// operands on the state path (S, L, D, R, V') are split into bf16 hi + lo
-// parts (~16 mantissa bits). A product with a split operand, X.Bh + X.Bl, is
-// one v_mfma_f32_16x16x32_bf16 whose 32-deep k axis holds, in each lane
-// group's 8 slots, 4 k of the hi part then the same 4 k of the lo part, with
-// the A fragment repeated (cat): the accumulator-layout registers are the B
-// operand as they are. The state lives in MFMA accumulators (S^T tiles)
-// across chunks. The next chunk's inputs are loaded into
-// registers while the current chunk computes. Padded rows of a
-// partial chunk have k = q = v = beta = 0 and log decay 0, so they change
+// Work split. The Dv rows of S evolve independently, so a head's 128 rows are
+// cut over 8/WV work-groups of WV waves, 16 rows per wave: a long prompt
+// spreads over Hv*8/WV groups instead of Hv. Each group forms the chunk's
+// state-independent matrices itself: wave 0 takes the four diagonal 16x16
+// blocks of L and inverts them, D_I = (I + L_II)^-1, while the other waves form
+// the off-diagonal blocks of L and the blocks of P. Every wave then works on
+// its own 16 state rows, held in MFMA accumulators across chunks. A chunk
+// needs three work-group barriers: inputs staged, matrices formed, chunk done.
+//
+// Operand layouts of v_mfma_f32_16x16x32_bf16 (lane l, q = l/16, c = l%16):
+// an A operand holds row c, k slots 8q..8q+7; a B operand column c, the same k
+// slots; the accumulator holds row 4q + r, column c in register r. Two 16-row
+// accumulator tiles side by side, cat(X, X'), form an operand whose k slots
+// 8q..8q+3 are rows 4q..4q+3 of X and 8q+4..8q+7 the same rows of X'; the
+// other operand reads its k values in that "pair order". Q and P rows are
+// stored in pair order so that such an operand is one 16-byte LDS read. K is
+// stored in natural dk order with its 8-byte segments XOR-swizzled per row:
+// the pair-order reads (two segments) and the transposing reads of the state
+// update (ds_read_b64_tr_b16, four rows of one column block) both spread over
+// the LDS banks.
+//
+// Precision: k and q are bf16, exact MFMA operands. f32 operands of the
+// products that feed the state (S in K S^T, -L, D, the solve's right-hand
+// sides, V') are split into bf16 hi + lo (~16 mantissa bits); the products
+// that only reach the bf16 outputs (Q S^T, P V') use hi alone. Padded rows of
+// a partial chunk have k = q = beta = 0, v = 0 and log decay 0, so they change
 // nothing.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 namespace {
 constexpr int kC = 64;
-constexpr int kLdK = kDk + 8;  // bf16 [64][128] rows (272 B)
-constexpr int kLdT = kC + 8;   // bf16 [*][64] rows (144 B)
-constexpr int kLdD = 24;       // bf16 [16][16] blocks (48 B rows)
+// Row strides. LDS serves the 16-byte operand reads below (lane (q, c): row
+// c, 16-byte column group q) without bank conflicts when the stride is 8 mod
+// 16 dwords (measured on gfx950 with SQ_LDS_BANK_CONFLICT).
+constexpr int kLdQ = kDk + 16;     // Q rows in pair order (288 B = 72 dwords)
+constexpr int kLdP = kC + 16;      // P rows in pair order (160 B = 40 dwords)
+constexpr int kLdN = 2 * kC + 16;  // -L rows: 16 groups of (4 hi, 4 lo) (288 B)
+constexpr int kLdD = 48;           // D_I rows: 4 groups of (4 hi, 4 lo) (96 B = 24 dwords)
+constexpr int kLdDB = 16 * kLdD + 32;  // D_I blocks: the 4 blocks start 16 banks apart
+constexpr int kLdL = 20;           // rows of the diagonal blocks of L, f32 (80 B)
+constexpr int kLdLB = 16 * kLdL + 8;
+constexpr int kKBlk = 16 * kDk + 64;   // K: 16-row blocks, 64 elements of padding between
 
-struct ChunkSmem {
-  uint16_t K[kC][kLdK];      // k, token-major
-  uint16_t KT[kDk][kLdT];    // k, dk-major
-  uint16_t Q[kC][kLdK];      // q, token-major
-  uint16_t V[kC][kLdK];      // v of the head, token-major
-  uint16_t P[kC][kLdT];      // masked, decayed q.k
-  uint16_t NLh[kC][kLdT];    // -L, bf16 hi part
-  uint16_t NLl[kC][kLdT];    // -L, bf16 lo part
-  float Ld[4][16][17];       // diagonal 16x16 blocks of L (f32)
-  uint16_t Dh[4][16][kLdD];  // D_I = (I + L_II)^-1, hi
-  uint16_t Dl[4][16][kLdD];  // lo
-  float beta[kC], G[kC], eG[kC], dec_end[kC];  // G: cumulative log2 decay
-  float ysq[kC][8];          // RMSNormGated: per token, each wave's sum of y^2
+struct __attribute__((aligned(16))) ChunkSmem {
+  uint16_t K[4 * kKBlk];       // k, natural dk order, segments swizzled (kseg)
+  uint16_t Q[kC][kLdQ];        // q, dk in pair order: 32b + 16h + 4m + u at 32b + 8m + 4h + u
+  uint16_t P[kC][kLdP];        // P, token columns in pair order; blocks above the diagonal stay 0
+  uint16_t NL[kC][kLdN];       // -L, hi/lo interleaved per 4 columns
+  uint16_t D[4 * kLdDB];       // D_I, rows of kLdD, hi/lo interleaved per 4 columns
+  float Ld[4 * kLdLB];         // diagonal blocks of L (f32), for the inversion
+  float beta[kC], G[kC], eG[kC], dec[kC];  // G: cumulative log2 decay
+  float ysq[kC][8];            // gated epilogue: per token, each wave's sum of y^2
 };
 
 __device__ __forceinline__ f32x4 mfma32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
-
-// Operand fragments whose k runs contiguous in memory; they serve as A
-// operands (rows = output rows) and as B operands (rows = output columns).
-//   frag32: lane l takes row r0 + l%16, k = k0 + 8*(l/16) .. +7
-//   frag16: lane l takes row r0 + l%16, k = k0 + 4*(l/16) .. +3
-// A 16x16 accumulator tile holds row 4*(l/16) + r, column l%16 in register r:
-// the frag16 layout of its transpose, i.e. a B operand with k = row.
-__device__ __forceinline__ bf16x8 frag32(const uint16_t* base, int ld, int r0, int k0, int lane) {
-  return *reinterpret_cast<const bf16x8*>(base + (r0 + (lane & 15)) * ld + k0 + (lane >> 4) * 8);
-}
-__device__ __forceinline__ s16x4 frag16(const uint16_t* base, int ld, int r0, int k0, int lane) {
-  return *reinterpret_cast<const s16x4*>(base + (r0 + (lane & 15)) * ld + k0 + (lane >> 4) * 4);
-}
-
-__device__ __forceinline__ short bfbits(float x) { return (short)f2bf(x); }
-
-// Two 4-element fragments as one 8-element MFMA operand. Every product of
-// the kernel is a v_mfma_f32_16x16x32_bf16, a lone 16-deep term padded with
-// zeros: accumulation chains that mixed it with v_mfma_f32_16x16x16_bf16
-// (the result of one feeding the accumulator of the other) gave wrong results
-// in testing, so no accumulator is ever shared between the two opcodes.
-typedef short s16x8 __attribute__((ext_vector_type(8)));
-constexpr s16x4 kZero4 = {0, 0, 0, 0};
 __device__ __forceinline__ bf16x8 cat(s16x4 a, s16x4 b) {
   return __builtin_bit_cast(bf16x8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
 }
+__device__ __forceinline__ s16x4 lds4(const uint16_t* p) {
+  return *static_cast<const s16x4*>(__builtin_assume_aligned(p, 8));
+}
+__device__ __forceinline__ bf16x8 lds8(const uint16_t* p) {
+  return *static_cast<const bf16x8*>(__builtin_assume_aligned(p, 16));
+}
+constexpr s16x4 kZero4 = {0, 0, 0, 0};
 
-// K^T is stored with its token column XOR-swizzled by 8 * ((dk >> 3) & 7):
-// the transposing 2-byte stores of one wave (16 dk rows 8 apart) then spread
-// over the LDS banks, and a 4-token group stays contiguous and 8-byte aligned.
-__device__ __forceinline__ int kt_col(int dk, int tok) { return tok ^ (((dk >> 3) & 7) << 3); }
-__device__ __forceinline__ s16x4 frag16_kt(const uint16_t (*KT)[kC + 8], int r0, int k0, int lane) {
-  const int row = r0 + (lane & 15);
-  return *reinterpret_cast<const s16x4*>(&KT[row][kt_col(row, k0 + (lane >> 4) * 4)]);
+// Element offset of the natural 4-dk segment s (dk 4s..4s+3) of K row `row`.
+// LDS has 64 banks of 4 bytes and serves an 8-byte access 32 lanes at a time.
+// Within a block of 16 rows the swizzle g(r) = (r & 7) << 2 | ((r >> 3) & 1)
+// << 1 (r = row % 16) puts the 32 segments of such a pass in 32 distinct bank
+// pairs for both access forms: a pair-order read (16 consecutive rows,
+// segments differing in bit 0; bits 1-4 of g run through 0..15) and a
+// transposing read (8 consecutive rows x 4 consecutive segments; bits 2-4 of g
+// run through 0..7). The 16-row blocks are kKBlk = 16*128 + 64 elements apart:
+// rows 16 apart are then 4224 bytes apart, a distance no ds_read2 form encodes,
+// so the compiler cannot fuse two rows' reads into one ds_read2st64_b64 whose
+// two addresses would share a bank (measured: 16 conflict cycles per pair).
+// For a fixed lane the offset is a lane constant XOR a compile-time constant
+// plus a compile-time block offset, so an operand read costs one VALU op.
+__device__ __forceinline__ int kseg(int row, int s) {
+  const int r = row & 15;
+  return (row >> 4) * kKBlk + r * kDk + 4 * (s ^ (((r & 7) << 2) | (((r >> 3) & 1) << 1)));
+}
+// K operand reads from per-lane constants: with kf = kseg(c, q), the pair-order
+// operand of row 16X + c, dk block b (32 values) reads segments 8b + q and
+// 8b + 4 + q at X*kKBlk + (kf ^ (32b + 16h)), h = 0, 1 (the XORed bits and the
+// row bits of kseg are disjoint).
+__device__ __forceinline__ bf16x8 kfrag(const uint16_t* K, int kf, int X, int b) {
+  return cat(lds4(K + X * kKBlk + (kf ^ (32 * b))), lds4(K + X * kKBlk + (kf ^ (32 * b + 16))));
+}
+// K^T operand rows for the state update: lane (q, c) receives
+// K[16 blk + 4q + u][16a + c], u = 0..3. ds_read_b64_tr_b16 hands lane j of a
+// 16-lane group element j of the 4 x 16 block whose row u the lanes 4u..4u+3
+// read, 4 elements each; lane 4u + s reads row 4q + u, segment 4a + s at
+// blk*kKBlk + (kt ^ 16a) with kt = kseg(4q + (i >> 2), i & 3), i = lane % 16.
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+__device__ __forceinline__ s16x4 ktr(const uint16_t* K, int kt, int blk, int a) {
+  lds_bf16x4* p = (lds_bf16x4*)(K + blk * kKBlk + (kt ^ (16 * a)));
+  return __builtin_bit_cast(s16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(p));
 }
 
-// f32 tile -> bf16 hi + lo (hi + lo carries ~16 mantissa bits of x)
+// f32 -> bf16 hi + lo (hi + lo carries ~16 mantissa bits)
 __device__ __forceinline__ void split4(const f32x4& x, s16x4& hi, s16x4& lo) {
+  const uint32_t h0 = f2bf2(x[0], x[1]), h1 = f2bf2(x[2], x[3]);
+  const uint32_t l0 = f2bf2(x[0] - bf_lo(h0), x[1] - bf_hi(h0));
+  const uint32_t l1 = f2bf2(x[2] - bf_lo(h1), x[3] - bf_hi(h1));
+  hi = __builtin_bit_cast(s16x4, (uint2){h0, h1});
+  lo = __builtin_bit_cast(s16x4, (uint2){l0, l1});
+}
+__device__ __forceinline__ s16x4 hi4(const f32x4& x) {
+  return __builtin_bit_cast(s16x4, (uint2){f2bf2(x[0], x[1]), f2bf2(x[2], x[3])});
+}
+
+// Tiles of the chunk's matrices, as accumulators holding row 4q + r, column c:
+// kk(I, J) = k_{16J+4q+r} . k_{16I+c} = (K K^T)[16I+c][16J+4q+r] and
+// kq(I, J) = (Q K^T)[16I+c][16J+4q+r]: lane c owns row 16I+c of L or P.
+__device__ __forceinline__ f32x4 tile_kk(const ChunkSmem& sm, int kf, int I, int J) {
+  f32x4 t = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const uint16_t h = f2bf(x[u]);
-    hi[u] = (short)h;
-    lo[u] = bfbits(x[u] - bf2f(h));
+  for (int b = 0; b < 4; ++b) t = mfma32(kfrag(sm.K, kf, J, b), kfrag(sm.K, kf, I, b), t);
+  return t;
+}
+__device__ __forceinline__ f32x4 tile_kq(const ChunkSmem& sm, int kf, int I, int J, int q, int c) {
+  f32x4 t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int b = 0; b < 4; ++b) t = mfma32(kfrag(sm.K, kf, J, b), lds8(&sm.Q[16 * I + c][32 * b + 8 * q]), t);
+  return t;
+}
+
+// L block (I, J), J <= I: an off-diagonal block as -L hi/lo into NL (row
+// 16I+c, columns 16J+4q..+3), a diagonal block into Ld in f32.
+__device__ __forceinline__ void put_l(ChunkSmem& sm, const f32x4& t, int I, int J, int q, int c) {
+  const int i = 16 * I + c;
+  const float Gi = sm.G[i], bi = sm.beta[i];
+  const f32x4 Gj = *reinterpret_cast<const f32x4*>(&sm.G[16 * J + 4 * q]);
+  f32x4 lv;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float v = bi * t[r] * __builtin_amdgcn_exp2f(fminf(Gi - Gj[r], 0.f));
+    lv[r] = (J < I || 4 * q + r < c) ? v : 0.f;
   }
+  if (J == I) {
+    *reinterpret_cast<f32x4*>(&sm.Ld[I * kLdLB + c * kLdL + 4 * q]) = lv;
+  } else {
+    s16x4 h, l;
+    split4(-lv, h, l);
+    *reinterpret_cast<bf16x8*>(&sm.NL[i][8 * (4 * J + q)]) = cat(h, l);
+  }
+}
+// P block (I, J), J <= I: row 16I+c, columns 16J+4q..+3 at their pair-order place.
+__device__ __forceinline__ void put_p(ChunkSmem& sm, const f32x4& t, int I, int J, int q, int c) {
+  const int i = 16 * I + c;
+  const float Gi = sm.G[i];
+  const f32x4 Gj = *reinterpret_cast<const f32x4*>(&sm.G[16 * J + 4 * q]);
+  f32x4 pv;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float v = t[r] * __builtin_amdgcn_exp2f(fminf(Gi - Gj[r], 0.f));
+    pv[r] = (J < I || 4 * q + r <= c) ? v : 0.f;
+  }
+  *static_cast<s16x4*>(__builtin_assume_aligned(&sm.P[i][32 * (J >> 1) + 8 * q + 4 * (J & 1)], 8)) = hi4(pv);
+}
+
+// The 16 blocks the waves other than wave 0 form: 6 off-diagonal blocks of L,
+// then the 10 blocks of P (I, J), J <= I.
+__device__ __forceinline__ void other_block(int t, int& I, int& J, bool& isl) {
+  constexpr int kI[16] = {1, 2, 2, 3, 3, 3, 0, 1, 1, 2, 2, 2, 3, 3, 3, 3};
+  constexpr int kJ[16] = {0, 0, 1, 0, 1, 2, 0, 0, 1, 0, 1, 2, 0, 1, 2, 3};
+  I = kI[t];
+  J = kJ[t];
+  isl = t < 6;
 }
 }  // namespace
 
 // With GATED the RMSNormGated epilogue (qwen3_5.rs:660-665) runs on the
 // chunk's outputs: out[t, hv, :] = silu(z) * rms_norm(y, norm_w, norm_eps)
 // over the Dv rows of the head, z read from the merged projection row
-// (z = zrow + t * xs, columns hv*Dv ..); y is also stored when non-null.
-template <int R, bool GATED>
-__global__ __launch_bounds__(512) void prefill_chunk_kernel(
+// (z = zrow + t * xs, columns hv*Dv ..); y is also stored when non-null. The
+// norm spans all 128 rows of a head, so the gated form runs with WV = 8.
+// grid (Hv * 8/WV, nseq), block 64*WV.
+template <int R, bool GATED, int WV>
+__global__ __launch_bounds__(64 * WV) void prefill_chunk_kernel(
     float* __restrict__ state, const int32_t* __restrict__ slot_ids,
     const int32_t* __restrict__ cu, int num_slots, int Hk, int T,
     const uint16_t* __restrict__ qn, const uint16_t* __restrict__ kn,
@@ -377,80 +463,105 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
     const uint16_t* __restrict__ betav, uint16_t* __restrict__ y,
     const uint16_t* __restrict__ zrow, int64_t xs, const uint16_t* __restrict__ norm_w,
     float norm_eps, uint16_t* __restrict__ out, uint32_t* __restrict__ status) {
-  constexpr int NT = 512;
+  static_assert(WV == 8 || WV == 4 || WV == 2, "8, 4 or 2 waves per group");
+  static_assert(!GATED || WV == 8, "the gated epilogue needs a head's 128 rows in one group");
+  constexpr int NT = 64 * WV, NS = 8 / WV;
+  constexpr int UK = kC * kDk / 8 / NT;  // 16-byte input units per thread and matrix
   __shared__ ChunkSmem sm;
-  const int hv = blockIdx.x, s = blockIdx.y;
+  const int hv = blockIdx.x / NS, s = blockIdx.y;
   const int Hv = Hk * R, hk = hv / R;
   const int tid = threadIdx.x, lane0 = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, scalar
+  const int dv0 = 16 * ((blockIdx.x % NS) * WV + w);       // this wave's first state row
   const int slot = slot_ids[s];
   if ((unsigned)slot >= (unsigned)num_slots) {
-    if (tid == 0 && hv == 0) flag_status(status, GDN_FLAG_BAD_SLOT);
+    if (tid == 0 && blockIdx.x == 0) flag_status(status, GDN_FLAG_BAD_SLOT);
     return;
   }
   const int st = min(max(cu[s], 0), T), en = min(max(cu[s + 1], st), T);
   if (en <= st) return;
-  // this lane's state row (accumulator column) and 4-row group
-  float* gstate = state + ((size_t)slot * Hv + hv) * kTileElems + (size_t)(16 * w + (lane0 & 15)) * kDk +
-                  4 * (lane0 >> 4);
-  // RMSNormGated: the norm weight of this lane's output row, and its z column
-  float nw = 0.f;
+  const int q0 = lane0 >> 4, c0l = lane0 & 15;
+  // this lane's state column (accumulator column c = state row dv0 + c)
+  float* gstate = state + ((size_t)slot * Hv + hv) * kTileElems + (size_t)(dv0 + c0l) * kDk + 4 * q0;
+  f32x4 acc[8];  // S^T tiles: dk rows 16a + 4q + r, state row dv0 + c
+#pragma unroll
+  for (int a = 0; a < 8; ++a) acc[a] = *reinterpret_cast<const f32x4*>(gstate + 16 * a);
+  // gated epilogue: norm weights of this lane's 4 output rows, and its z columns
+  f32x4 nw = {0.f, 0.f, 0.f, 0.f};
   const uint16_t* zcol = nullptr;
   if constexpr (GATED) {
-    nw = bf2f(norm_w[16 * w + (lane0 & 15)]);
-    zcol = zrow + (size_t)hv * kDv + 16 * w + (lane0 & 15);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) nw[r] = bf2f(norm_w[dv0 + 4 * q0 + r]);
+    zcol = zrow + (size_t)hv * kDv + dv0 + 4 * q0;
   }
+  // Blocks of P above the diagonal are never written: zero them once.
+  for (int e = tid; e < kC * kLdP / 4; e += NT) reinterpret_cast<uint2*>(&sm.P[0][0])[e] = make_uint2(0u, 0u);
 
-  // state accumulators: S^T tiles (dk block a, this wave's 16 state rows)
-  f32x4 acc[8];
-#pragma unroll
-  for (int a = 0; a < 8; ++a)
-    acc[a] = *reinterpret_cast<const f32x4*>(gstate + 16 * a);
-
-  // chunk inputs in registers (prefetched one chunk ahead)
-  uint4 kv[2], qv[2], vv[2];
+  // chunk inputs, prefetched one chunk ahead: k and q units, this lane's v
+  // values (tokens 16I + 4q + r, state row dv0 + c; out-of-chunk reads give 0)
+  uint4 kv[UK], qv[UK];
+  uint16_t vpre[16];
   float pb = 0.f, pl = 0.f;
-  auto load_inputs = [&](int c0) {
-    const int n = min(kC, en - c0);
+  const int voff = (4 * q0 * Hv * kDv + c0l) * 2;  // byte offset of this lane's first v value
+  auto load_inputs = [&](int c) {
+    const int n = min(kC, en - c);
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int e = tid + NT * u, i = e >> 4, c = (e & 15) * 8;
+    for (int u = 0; u < UK; ++u) {
+      // k unit: dk 8m..8m+7; q unit: pair-order group m = dk 32(m/4) + 4(m%4)
+      // .. +3 and the same 16 further on
+      const int e = tid + NT * u, i = e >> 4, m = e & 15;
       kv[u] = make_uint4(0u, 0u, 0u, 0u);
       qv[u] = kv[u];
-      vv[u] = kv[u];
       if (i < n) {
-        const size_t off = ((size_t)(c0 + i) * Hk + hk) * kDk + c;
-        kv[u] = *reinterpret_cast<const uint4*>(kn + off);
-        qv[u] = *reinterpret_cast<const uint4*>(qn + off);
-        vv[u] = *reinterpret_cast<const uint4*>(vc + ((size_t)(c0 + i) * Hv + hv) * kDv + c);
+        const size_t row = ((size_t)(c + i) * Hk + hk) * kDk;
+        kv[u] = *reinterpret_cast<const uint4*>(kn + row + 8 * m);
+        const int dq = 32 * (m >> 2) + 4 * (m & 3);
+        const uint2 q0 = *reinterpret_cast<const uint2*>(qn + row + dq);
+        const uint2 q1 = *reinterpret_cast<const uint2*>(qn + row + dq + 16);
+        qv[u] = make_uint4(q0.x, q0.y, q1.x, q1.y);
       }
     }
+    // v through a buffer resource whose size ends at the chunk's last token
+    const int base = hv * kDv + dv0;
+    const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(vc + (size_t)c * Hv * kDv + base), (short)0, (n * Hv * kDv - base) * 2, 0x00020000);
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        vpre[4 * I + r] = __builtin_amdgcn_raw_buffer_load_b16(vr, voff + (16 * I + r) * Hv * kDv * 2, 0, 0);
     pb = 0.f;
     pl = 0.f;
     if (w == 0 && lane0 < n) {
-      pb = bf2f(betav[(size_t)(c0 + lane0) * Hv + hv]);
-      pl = lgv[(size_t)(c0 + lane0) * Hv + hv];
+      pb = bf2f(betav[(size_t)(c + lane0) * Hv + hv]);
+      pl = lgv[(size_t)(c + lane0) * Hv + hv];
     }
   };
-  auto store_inputs = [&]() {
-    // Opaque to the compiler until here, so it cannot unpack the prefetched
-    // words (and wait for the loads) right after issuing them.
+
+  load_inputs(st);
+  for (int c0 = st; c0 < en; c0 += kC) {
+    const int n = min(kC, en - c0);
+    // Lane-derived values are recomputed in every chunk (a few VALU ops)
+    // instead of being held in registers across the loop.
+    int lane = lane0;
+    asm volatile("" : "+v"(lane));
+    const int q = lane >> 4, c = lane & 15;
+    const int kf = kseg(c, q), kt = kseg(4 * q + (c >> 2), c & 3);  // K operand lane constants
+    // (a) stage k (natural order, swizzled segments) and q (pair order); wave 0
+    // forms the decay prefix sums in log2 units
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int u = 0; u < UK; ++u)
       asm volatile("" : "+v"(kv[u].x), "+v"(kv[u].y), "+v"(kv[u].z), "+v"(kv[u].w),
-                   "+v"(qv[u].x), "+v"(qv[u].y), "+v"(qv[u].z), "+v"(qv[u].w),
-                   "+v"(vv[u].x), "+v"(vv[u].y), "+v"(vv[u].z), "+v"(vv[u].w));
+                   "+v"(qv[u].x), "+v"(qv[u].y), "+v"(qv[u].z), "+v"(qv[u].w));
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int e = tid + NT * u, i = e >> 4, c = (e & 15) * 8;
-      *reinterpret_cast<uint4*>(&sm.K[i][c]) = kv[u];
-      *reinterpret_cast<uint4*>(&sm.Q[i][c]) = qv[u];
-      *reinterpret_cast<uint4*>(&sm.V[i][c]) = vv[u];
-      const uint16_t* kb = reinterpret_cast<const uint16_t*>(&kv[u]);
-#pragma unroll
-      for (int x = 0; x < 8; ++x) sm.KT[c + x][kt_col(c + x, i)] = kb[x];
+    for (int u = 0; u < UK; ++u) {
+      // k: natural segments 2m, 2m + 1 stay adjacent and in order under the
+      // (even) swizzle, one 16-byte write; q: pair-order group m, one 16-byte write
+      const int e = tid + NT * u, i = e >> 4, m = e & 15;
+      *static_cast<uint4*>(__builtin_assume_aligned(&sm.K[kseg(i, 2 * m)], 16)) = kv[u];
+      *static_cast<uint4*>(__builtin_assume_aligned(&sm.Q[i][8 * m], 16)) = qv[u];
     }
-    if (w == 0) {  // inclusive prefix sum of the log decay, in log2 units
+    if (w == 0) {
       float gsum = pl * 1.4426950408889634f;
 #pragma unroll
       for (int off = 1; off < 64; off <<= 1) {
@@ -461,197 +572,183 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
       sm.beta[lane0] = pb;
       sm.G[lane0] = gsum;
       sm.eG[lane0] = __builtin_amdgcn_exp2f(gsum);
-      sm.dec_end[lane0] = __builtin_amdgcn_exp2f(gC - gsum);
+      sm.dec[lane0] = __builtin_amdgcn_exp2f(gC - gsum);
     }
-  };
-
-  load_inputs(st);
-  for (int c0 = st; c0 < en; c0 += kC) {
-    const int n = min(kC, en - c0);
-    // Lane-derived LDS addresses are recomputed in every chunk (a few VALU
-    // ops) instead of being held in registers across the loop.
-    int lane = lane0;
-    asm volatile("" : "+v"(lane));
-    const int lq = lane >> 4, lc = lane & 15;
-    const int drow = 16 * w + lc;
-    store_inputs();
+    uint16_t vcur[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) vcur[e] = vpre[e];
     __syncthreads();
     if (c0 + kC < en) load_inputs(c0 + kC);
 
-    // (b) waves 0-3: K K^T for token rows 16w.. -> -L (hi/lo) and its f32
-    // diagonal block; waves 4-7: Q K^T for token rows 16(7-w).. -> P. Column
-    // blocks above the row block are zero and skipped, so row block I has I+1
-    // blocks; waves w and w+4 share a SIMD, which thus gets (w+1) + (4-w) = 5.
-    {
-      const int I = w < 4 ? w : 7 - w;
-      const bool isq = w >= 4;
-      const uint16_t* A = isq ? &sm.Q[0][0] : &sm.K[0][0];
+    // (b) the chunk's matrices: wave 0 the diagonal blocks of L and their
+    // inverses, the other waves the remaining blocks of L and P
+    if (w == 0) {
 #pragma unroll
-      for (int J = 0; J < 4; ++J) {
-        if (J > I) continue;
-        f32x4 c = {0.f, 0.f, 0.f, 0.f};
+      for (int I = 0; I < 4; ++I) put_l(sm, tile_kk(sm, kf, I, I), I, I, q, c);
+      // this wave's own Ld writes, read back by other lanes of the wave
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      // lane (I = q, column j = c): column j of (I + L_II)^-1 by forward substitution
+      {
+        const float* Lb = &sm.Ld[q * kLdLB];
+        float t[16];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-          c = mfma32(frag32(A, kLdK, 16 * I, 32 * ks, lane),
-                     frag32(&sm.K[0][0], kLdK, 16 * J, 32 * ks, lane), c);
+        for (int i = 0; i < 16; ++i) {
+          asm volatile("" ::: "memory");  // bound live ranges: one row of L at a time
+          float a = i == c ? 1.f : 0.f;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int i = 16 * I + 4 * lq + r, j = 16 * J + lc;
-          const float d = __builtin_amdgcn_exp2f(fminf(sm.G[i] - sm.G[j], 0.f));
-          if (isq) {
-            sm.P[i][j] = f2bf(j <= i ? c[r] * d : 0.f);
-          } else {
-            const float lv = j < i ? sm.beta[i] * c[r] * d : 0.f;
-            const uint16_t nh = f2bf(-lv);
-            sm.NLh[i][j] = nh;
-            sm.NLl[i][j] = f2bf(-lv - bf2f(nh));
-            if (J == I) sm.Ld[I][4 * lq + r][lc] = lv;
-          }
+          for (int k = 0; k < i; ++k) a -= Lb[i * kLdL + k] * t[k];
+          t[i] = a;
+        }
+        uint16_t* Dp = &sm.D[q * kLdDB + 8 * (c >> 2) + (c & 3)];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const uint16_t h = f2bf(t[i]);
+          Dp[i * kLdD] = h;
+          Dp[i * kLdD + 4] = f2bf(t[i] - bf2f(h));
         }
       }
     }
-    // (c) waves 0-3: D_w = (I + L_ww)^-1 by forward substitution (lanes 0..15
-    // = columns)
-    if (w < 4 && lane < 16) {
-      const int j = lane;
-      float t[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        asm volatile("" ::: "memory");  // bound live ranges: one row of L at a time
-        float a = i == j ? 1.f : 0.f;
-#pragma unroll
-        for (int k = 0; k < i; ++k) a -= sm.Ld[w][i][k] * t[k];
-        t[i] = a;
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const uint16_t h = f2bf(t[i]);
-        sm.Dh[w][i][j] = h;
-        sm.Dl[w][i][j] = f2bf(t[i] - bf2f(h));
-      }
+    for (int t = 0; t < 16; ++t) {
+      constexpr int kOthers = WV > 1 ? WV - 1 : 1;
+      if (w != (WV > 1 ? 1 + t % kOthers : 0)) continue;
+      int I, J;
+      bool isl;
+      other_block(t, I, J, isl);
+      if (isl)
+        put_l(sm, tile_kk(sm, kf, I, J), I, J, q, c);
+      else
+        put_p(sm, tile_kq(sm, kf, I, J, q, c), I, J, q, c);
     }
-    // (d) Y_I = K_I S^T and Z_I = Q_I S^T for this wave's 16 state rows; the
-    // hi/lo split of the S^T accumulator tiles is the B operand
-    f32x4 yk[4], zq[4];
+    // (c) Y_I = K_I S^T (S hi and lo) and Zt_I = S Q_I^T (S hi) for this wave's
+    // 16 state rows; the pair (acc[2b], acc[2b+1]) is the operand of dk block b
+    f32x4 yk[4], zt[4];
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       yk[I] = f32x4{0.f, 0.f, 0.f, 0.f};
-      zq[I] = yk[I];
+      zt[I] = yk[I];
     }
 #pragma unroll
-    for (int a = 0; a < 8; ++a) {
+    for (int b = 0; b < 4; ++b) {
       asm volatile("" ::: "memory");  // bound live ranges: one dk block at a time
-      s16x4 sh, sl;
-      split4(acc[a], sh, sl);
-      const bf16x8 bs = cat(sh, sl);
+      s16x4 h0, l0, h1, l1;
+      split4(acc[2 * b], h0, l0);
+      split4(acc[2 * b + 1], h1, l1);
+      const bf16x8 sh = cat(h0, h1), sl = cat(l0, l1);
 #pragma unroll
       for (int I = 0; I < 4; ++I) {
-        const s16x4 ak = frag16(&sm.K[0][0], kLdK, 16 * I, 16 * a, lane);
-        const s16x4 aq = frag16(&sm.Q[0][0], kLdK, 16 * I, 16 * a, lane);
-        yk[I] = mfma32(cat(ak, ak), bs, yk[I]);
-        zq[I] = mfma32(cat(aq, aq), bs, zq[I]);
+        const bf16x8 ka = kfrag(sm.K, kf, I, b);
+        yk[I] = mfma32(ka, sh, yk[I]);
+        yk[I] = mfma32(ka, sl, yk[I]);
+        zt[I] = mfma32(sh, lds8(&sm.Q[16 * I + c][32 * b + 8 * q]), zt[I]);
       }
     }
     __syncthreads();
 
-    // (e, f) R_I, then V'_I = D_I (R_I - sum_{j<I} L_Ij V'_j)
-    s16x4 vph[4], vpl[4];
+    // (d) R_I = beta (V - exp(G) Y_I), then V'_I = D_I (R_I - sum_{j<I} L_Ij V'_j)
+    f32x4 vf[4];        // V' (f32), tokens 16I + 4q + r, state row dv0 + c
+    bf16x8 vpd[4];      // cat(V'h, V'h)
+    bf16x8 vplz[4];     // cat(V'l, 0)
+    s16x4 vph[4];
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
+      const f32x4 bt = *reinterpret_cast<const f32x4*>(&sm.beta[16 * I + 4 * q]);
+      const f32x4 eg = *reinterpret_cast<const f32x4*>(&sm.eG[16 * I + 4 * q]);
       f32x4 x;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 16 * I + 4 * lq + r;
-        x[r] = sm.beta[i] * (bf2f(sm.V[i][drow]) - sm.eG[i] * yk[I][r]);
-      }
+      for (int r = 0; r < 4; ++r) x[r] = bt[r] * (bf2f(vcur[4 * I + r]) - eg[r] * yk[I][r]);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         if (j >= I) continue;
-        const s16x4 lh = frag16(&sm.NLh[0][0], kLdT, 16 * I, 16 * j, lane);
-        const s16x4 ll = frag16(&sm.NLl[0][0], kLdT, 16 * I, 16 * j, lane);
-        x = mfma32(cat(lh, ll), cat(vph[j], vph[j]), x);  // lh.vph + ll.vph
-        x = mfma32(cat(lh, kZero4), cat(vpl[j], vpl[j]), x);  // lh.vpl
+        const bf16x8 nl = lds8(&sm.NL[16 * I + c][8 * (4 * j + q)]);  // -L hi | lo
+        x = mfma32(nl, vpd[j], x);   // (NLh + NLl) V'h
+        x = mfma32(nl, vplz[j], x);  // NLh V'l
       }
       s16x4 xh, xl;
       split4(x, xh, xl);
-      const s16x4 dh = frag16(&sm.Dh[I][0][0], kLdD, 0, 0, lane);
-      const s16x4 dl = frag16(&sm.Dl[I][0][0], kLdD, 0, 0, lane);
+      const bf16x8 d = lds8(&sm.D[I * kLdDB + c * kLdD + 8 * q]);  // D hi | lo
       f32x4 v = {0.f, 0.f, 0.f, 0.f};
-      v = mfma32(cat(dh, dl), cat(xh, xh), v);      // dh.xh + dl.xh
-      v = mfma32(cat(dh, kZero4), cat(xl, xl), v);  // dh.xl
-      split4(v, vph[I], vpl[I]);
+      v = mfma32(d, cat(xh, xh), v);     // (Dh + Dl) xh
+      v = mfma32(d, cat(xl, kZero4), v); // Dh xl
+      vf[I] = v;
+      s16x4 vl;
+      split4(v, vph[I], vl);
+      vpd[I] = cat(vph[I], vph[I]);
+      vplz[I] = cat(vl, kZero4);
     }
-    // (g) O_I = exp(G) * Z_I + sum_{j<=I} P_Ij V'_j
-    float yo[4][4];      // GATED: y of tokens 16I + 4lq + r, row drow (bf16 values)
-    uint16_t zv[4][4];   // GATED: z of the same outputs
-    if constexpr (GATED) {  // issued first, consumed after the y^2 sums
-#pragma unroll
-      for (int I = 0; I < 4; ++I)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          zv[I][r] = zcol[(size_t)min(c0 + 16 * I + 4 * lq + r, en - 1) * xs];
-    }
+    // (e) O^T_I = exp(G) Zt_I + V'^T P^T: rows dv0 + 4q + r, token 16I + c
+    f32x4 yo[4];
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
-      f32x4 o;
+      f32x4 o = zt[I] * sm.eG[16 * I + c];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) o[r] = zq[I][r] * sm.eG[16 * I + 4 * lq + r];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (j > I) continue;
-        const s16x4 ph = frag16(&sm.P[0][0], kLdT, 16 * I, 16 * j, lane);
-        o = mfma32(cat(ph, ph), cat(vph[j], vpl[j]), o);
+      for (int p = 0; p < 2; ++p) {
+        if (2 * p > I) continue;
+        o = mfma32(cat(vph[2 * p], vph[2 * p + 1]), lds8(&sm.P[16 * I + c][32 * p + 8 * q]), o);
       }
+      yo[I] = o;
+      const int i = 16 * I + c;
+      if (y != nullptr && i < n)
+        *reinterpret_cast<uint2*>(y + ((size_t)(c0 + i) * Hv + hv) * kDv + dv0 + 4 * q) =
+            make_uint2(f2bf2(o[0], o[1]), f2bf2(o[2], o[3]));
+    }
+    uint2 zv[4];
+    if constexpr (GATED) {  // z of the outputs, and each wave's sums of y^2 per token
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 16 * I + 4 * lq + r;
-        if constexpr (GATED) {
-          yo[I][r] = rbf(o[r]);
-          // sum of y^2 over this wave's 16 rows (the 16 lanes of the DPP row)
-          const float ss = sum16(yo[I][r] * yo[I][r]);
-          if (lc == 0) sm.ysq[i][w] = ss;
-        }
-        if (y != nullptr && i < n) y[((size_t)(c0 + i) * Hv + hv) * kDv + drow] = f2bf(o[r]);
+      for (int I = 0; I < 4; ++I) {
+        zv[I] = *reinterpret_cast<const uint2*>(zcol + (size_t)min(c0 + 16 * I + c, en - 1) * xs);
+        f32x4 yb;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) yb[r] = rbf(yo[I][r]);
+        yo[I] = yb;
+        float ss = (yb[0] * yb[0] + yb[1] * yb[1]) + (yb[2] * yb[2] + yb[3] * yb[3]);
+        ss += __shfl_xor(ss, 16, 64);
+        ss += __shfl_xor(ss, 32, 64);
+        if (q == 0) sm.ysq[16 * I + c][w] = ss;
       }
     }
-    if constexpr (GATED) {  // RMSNormGated over the Dv = 128 rows of each token
-      __syncthreads();
+    // (f) S^T <- exp(G_C) S^T + K^T (exp(G_C - G) V'), V' hi and lo
+    bf16x8 vth[2], vtl[2];
 #pragma unroll
-      for (int I = 0; I < 4; ++I)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int i = 16 * I + 4 * lq + r;
-          const f32x4 p0 = *reinterpret_cast<const f32x4*>(&sm.ysq[i][0]);
-          const f32x4 p1 = *reinterpret_cast<const f32x4*>(&sm.ysq[i][4]);
-          const float tot = ((p0[0] + p0[1]) + (p0[2] + p0[3])) + ((p1[0] + p1[1]) + (p1[2] + p1[3]));
-          const float rn = 1.0f / sqrtf(tot / (float)kDv + norm_eps);
-          const float normed = rbf(nw * rbf(yo[I][r] * rn));
-          if (i < n)
-            out[((size_t)(c0 + i) * Hv + hv) * kDv + drow] = f2bf(silu_bf16(bf2f(zv[I][r])) * normed);
-        }
+    for (int p = 0; p < 2; ++p) {
+      s16x4 h0, l0, h1, l1;
+      const f32x4 d0 = *reinterpret_cast<const f32x4*>(&sm.dec[32 * p + 4 * q]);
+      const f32x4 d1 = *reinterpret_cast<const f32x4*>(&sm.dec[32 * p + 16 + 4 * q]);
+      split4(vf[2 * p] * d0, h0, l0);
+      split4(vf[2 * p + 1] * d1, h1, l1);
+      vth[p] = cat(h0, h1);
+      vtl[p] = cat(l0, l1);
     }
-    // (h) S^T <- exp(G_C) S^T + K^T (exp(G_C - G) * V')
     const float eC = sm.eG[kC - 1];
 #pragma unroll
-    for (int a = 0; a < 8; ++a) acc[a] *= eC;
+    for (int a = 0; a < 8; ++a) {
+      acc[a] *= eC;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      asm volatile("" ::: "memory");  // bound live ranges: one token block at a time
-      f32x4 vt;
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        vt[r] = (bf2f((uint16_t)vph[j][r]) + bf2f((uint16_t)vpl[j][r])) *
-                sm.dec_end[16 * j + 4 * lq + r];
-      s16x4 th, tl;
-      split4(vt, th, tl);
-      const bf16x8 bt = cat(th, tl);
-#pragma unroll
-      for (int a = 0; a < 8; ++a) {
-        const s16x4 kt = frag16_kt(sm.KT, 16 * a, 16 * j, lane);
-        acc[a] = mfma32(cat(kt, kt), bt, acc[a]);
+      for (int p = 0; p < 2; ++p) {
+        const bf16x8 ka = cat(ktr(sm.K, kt, 2 * p, a), ktr(sm.K, kt, 2 * p + 1, a));
+        acc[a] = mfma32(ka, vth[p], acc[a]);
+        acc[a] = mfma32(ka, vtl[p], acc[a]);
       }
     }
     __syncthreads();
+    if constexpr (GATED) {  // RMSNormGated over the 128 rows of each token
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        const int i = 16 * I + c;
+        const f32x4 p0 = *reinterpret_cast<const f32x4*>(&sm.ysq[i][0]);
+        const f32x4 p1 = *reinterpret_cast<const f32x4*>(&sm.ysq[i][4]);
+        const float tot = ((p0[0] + p0[1]) + (p0[2] + p0[3])) + ((p1[0] + p1[1]) + (p1[2] + p1[3]));
+        const float rn = 1.0f / sqrtf(tot / (float)kDv + norm_eps);
+        const float z4[4] = {bf_lo(zv[I].x), bf_hi(zv[I].x), bf_lo(zv[I].y), bf_hi(zv[I].y)};
+        f32x4 ov;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ov[r] = silu_bf16(z4[r]) * rbf(nw[r] * rbf(yo[I][r] * rn));
+        if (i < n)
+          *reinterpret_cast<uint2*>(out + ((size_t)(c0 + i) * Hv + hv) * kDv + dv0 + 4 * q) =
+              make_uint2(f2bf2(ov[0], ov[1]), f2bf2(ov[2], ov[3]));
+      }
+    }
   }
 #pragma unroll
   for (int a = 0; a < 8; ++a)
@@ -713,13 +810,26 @@ static hipError_t launch_prefill_r(const PrefillArgs& a) {
                      a.total_tokens, a.mixed, a.xstride, a.status);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  // Work-groups per head: one 8-wave group while the heads of the batch fill
+  // the machine, else the state rows split over 2 or 4 groups per head.
+  const int units = Hv * a.nseq;
   if (a.out)
-    hipLaunchKernelGGL((prefill_chunk_kernel<R, true>), dim3(Hv, a.nseq), dim3(512), 0,
+    hipLaunchKernelGGL((prefill_chunk_kernel<R, true, 8>), dim3(Hv, a.nseq), dim3(512), 0,
                        a.stream, a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk,
                        a.total_tokens, ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, a.y, a.mixed + D,
                        a.xstride, a.norm_w, a.norm_eps, a.out, a.status);
+  else if (units >= 192)
+    hipLaunchKernelGGL((prefill_chunk_kernel<R, false, 8>), dim3(Hv, a.nseq), dim3(512), 0,
+                       a.stream, a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk,
+                       a.total_tokens, ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, a.y, nullptr,
+                       a.xstride, nullptr, 0.0f, nullptr, a.status);
+  else if (units >= 96)
+    hipLaunchKernelGGL((prefill_chunk_kernel<R, false, 4>), dim3(Hv * 2, a.nseq), dim3(256), 0,
+                       a.stream, a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk,
+                       a.total_tokens, ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, a.y, nullptr,
+                       a.xstride, nullptr, 0.0f, nullptr, a.status);
   else
-    hipLaunchKernelGGL((prefill_chunk_kernel<R, false>), dim3(Hv, a.nseq), dim3(512), 0,
+    hipLaunchKernelGGL((prefill_chunk_kernel<R, false, 2>), dim3(Hv * 4, a.nseq), dim3(128), 0,
                        a.stream, a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk,
                        a.total_tokens, ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, a.y, nullptr,
                        a.xstride, nullptr, 0.0f, nullptr, a.status);
