@@ -272,10 +272,10 @@ __global__ __launch_bounds__(256) void prefill_conv_state_kernel(
 // Work split. The Dv rows of S evolve independently, so a head's 128 rows are
 // cut over 8/WV work-groups of WV waves, 16 rows per wave: a long prompt
 // spreads over Hv*8/WV groups instead of Hv. Each group forms the chunk's
-// state-independent matrices itself: wave 0 takes the four diagonal 16x16
-// blocks of L and inverts them, D_I = (I + L_II)^-1, while the other waves form
-// the off-diagonal blocks of L and the blocks of P. Every wave then works on
-// its own 16 state rows, held in MFMA accumulators across chunks. A chunk
+// state-independent matrices itself: each of four waves takes one diagonal
+// 16x16 block of L and inverts it, D_I = (I + L_II)^-1, while the other waves
+// form the off-diagonal blocks of L and the blocks of P. Every wave then works
+// on its own 16 state rows, held in MFMA accumulators across chunks. A chunk
 // needs three work-group barriers: inputs staged, matrices formed, chunk done.
 //
 // Operand layouts of v_mfma_f32_16x16x32_bf16 (lane l, q = l/16, c = l%16):
@@ -321,11 +321,16 @@ struct __attribute__((aligned(16))) ChunkSmem {
   uint16_t P[kC][kLdP];        // P, token columns in pair order; blocks above the diagonal stay 0
   uint16_t NL[kC][kLdN];       // -L, hi/lo interleaved per 4 columns
   uint16_t D[4 * kLdDB];       // D_I, rows of kLdD, hi/lo interleaved per 4 columns
-  float Ld[4 * kLdLB];         // diagonal blocks of L (f32), for the inversion
+  float Ld[4 * kLdLB];         // diagonal blocks of L (f32): row i, column 4m + p at 4p + m
   float beta[kC], G[kC], eG[kC], dec[kC];  // G: cumulative log2 decay
   float ysq[kC][8];            // gated epilogue: per token, each wave's sum of y^2
 };
 
+// DPP move of a float (lanes without a source read 0)
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
 __device__ __forceinline__ f32x4 mfma32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
@@ -416,7 +421,10 @@ __device__ __forceinline__ void put_l(ChunkSmem& sm, const f32x4& t, int I, int 
     lv[r] = (J < I || 4 * q + r < c) ? v : 0.f;
   }
   if (J == I) {
-    *reinterpret_cast<f32x4*>(&sm.Ld[I * kLdLB + c * kLdL + 4 * q]) = lv;
+    // row c of the block, column 4q + r at place 4r + q (the inversion's lane
+    // p reads columns p, p+4, p+8, p+12 as one 16-byte group)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sm.Ld[I * kLdLB + c * kLdL + 4 * r + q] = lv[r];
   } else {
     s16x4 h, l;
     split4(-lv, h, l);
@@ -437,7 +445,7 @@ __device__ __forceinline__ void put_p(ChunkSmem& sm, const f32x4& t, int I, int 
   *static_cast<s16x4*>(__builtin_assume_aligned(&sm.P[i][32 * (J >> 1) + 8 * q + 4 * (J & 1)], 8)) = hi4(pv);
 }
 
-// The 16 blocks the waves other than wave 0 form: 6 off-diagonal blocks of L,
+// The 16 blocks besides the diagonal blocks of L: 6 off-diagonal blocks of L,
 // then the 10 blocks of P (I, J), J <= I.
 __device__ __forceinline__ void other_block(int t, int& I, int& J, bool& isl) {
   constexpr int kI[16] = {1, 2, 2, 3, 3, 3, 0, 1, 1, 2, 2, 2, 3, 3, 3, 3};
@@ -562,13 +570,17 @@ __global__ __launch_bounds__(64 * WV) void prefill_chunk_kernel(
       *static_cast<uint4*>(__builtin_assume_aligned(&sm.Q[i][8 * m], 16)) = qv[u];
     }
     if (w == 0) {
+      // inclusive prefix sum over the 64 lanes on DPP: shifts within each
+      // 16-lane row, then row 0's and row 2's totals into rows 1 and 3
+      // (row_bcast:15), then the first half's total into rows 2 and 3 (row_bcast:31)
       float gsum = pl * 1.4426950408889634f;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const float t = __shfl_up(gsum, off, 64);
-        if (lane0 >= off) gsum += t;
-      }
-      const float gC = __shfl(gsum, 63, 64);
+      gsum += dpp_f<0x111, 0xF>(gsum);  // row_shr:1
+      gsum += dpp_f<0x112, 0xF>(gsum);  // row_shr:2
+      gsum += dpp_f<0x114, 0xF>(gsum);  // row_shr:4
+      gsum += dpp_f<0x118, 0xF>(gsum);  // row_shr:8
+      gsum += dpp_f<0x142, 0xA>(gsum);  // row_bcast:15
+      gsum += dpp_f<0x143, 0xC>(gsum);  // row_bcast:31
+      const float gC = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gsum), 63));
       sm.beta[lane0] = pb;
       sm.G[lane0] = gsum;
       sm.eG[lane0] = __builtin_amdgcn_exp2f(gsum);
@@ -580,39 +592,48 @@ __global__ __launch_bounds__(64 * WV) void prefill_chunk_kernel(
     __syncthreads();
     if (c0 + kC < en) load_inputs(c0 + kC);
 
-    // (b) the chunk's matrices: wave 0 the diagonal blocks of L and their
-    // inverses, the other waves the remaining blocks of L and P
-    if (w == 0) {
+    // (b) the chunk's matrices. Diagonal block I of L goes to wave I % WV,
+    // which forms it and inverts it, D_I = (I + L_II)^-1, by forward
+    // substitution with four lanes per column: lane (j = l/4, p = l%4) sums
+    // the terms k = p (mod 4) of each row and two DPP adds close the sum over
+    // its quad, so a row costs a handful of dependent VALU ops. The
+    // off-diagonal blocks of L and the blocks of P go to waves 4-7 (to every
+    // wave with fewer than 8).
 #pragma unroll
-      for (int I = 0; I < 4; ++I) put_l(sm, tile_kk(sm, kf, I, I), I, I, q, c);
+    for (int I = 0; I < 4; ++I) {
+      if (w != I % WV) continue;
+      put_l(sm, tile_kk(sm, kf, I, I), I, I, q, c);
       // this wave's own Ld writes, read back by other lanes of the wave
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
       __builtin_amdgcn_wave_barrier();
-      // lane (I = q, column j = c): column j of (I + L_II)^-1 by forward substitution
-      {
-        const float* Lb = &sm.Ld[q * kLdLB];
-        float t[16];
+      const int j = lane0 >> 2, pp = lane0 & 3;
+      const float* Lb = &sm.Ld[I * kLdLB + 4 * pp];
+      float tv[4] = {pp == 0 && j == 0 ? 1.f : 0.f, 0.f, 0.f, 0.f};  // t_{4m+p} of column j
+      f32x4 row = *reinterpret_cast<const f32x4*>(&Lb[kLdL]);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          asm volatile("" ::: "memory");  // bound live ranges: one row of L at a time
-          float a = i == c ? 1.f : 0.f;
+      for (int i = 1; i < 16; ++i) {
+        const f32x4 cur = row;
+        if (i + 1 < 16) row = *reinterpret_cast<const f32x4*>(&Lb[(i + 1) * kLdL]);
+        float part = 0.f;
 #pragma unroll
-          for (int k = 0; k < i; ++k) a -= Lb[i * kLdL + k] * t[k];
-          t[i] = a;
-        }
-        uint16_t* Dp = &sm.D[q * kLdDB + 8 * (c >> 2) + (c & 3)];
+        for (int m = 0; m <= (i - 1) >> 2; ++m) part += cur[m] * tv[m];
+        part += dpp_f<0xB1, 0xF>(part);  // quad_perm xor 1
+        part += dpp_f<0x4E, 0xF>(part);  // quad_perm xor 2
+        const float ti = (i == j ? 1.f : 0.f) - part;
+        if (pp == (i & 3)) tv[i >> 2] = ti;
+      }
+      // rows 4m + p of column j, hi and lo
+      uint16_t* Dp = &sm.D[I * kLdDB + 8 * (j >> 2) + (j & 3)];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const uint16_t h = f2bf(t[i]);
-          Dp[i * kLdD] = h;
-          Dp[i * kLdD + 4] = f2bf(t[i] - bf2f(h));
-        }
+      for (int m = 0; m < 4; ++m) {
+        const uint16_t h = f2bf(tv[m]);
+        Dp[(4 * m + pp) * kLdD] = h;
+        Dp[(4 * m + pp) * kLdD + 4] = f2bf(tv[m] - bf2f(h));
       }
     }
 #pragma unroll
     for (int t = 0; t < 16; ++t) {
-      constexpr int kOthers = WV > 1 ? WV - 1 : 1;
-      if (w != (WV > 1 ? 1 + t % kOthers : 0)) continue;
+      if (w != (WV == 8 ? 4 + t % 4 : t % WV)) continue;
       int I, J;
       bool isl;
       other_block(t, I, J, isl);
