@@ -461,7 +461,7 @@ __device__ __forceinline__ void other_block(int t, int& I, int& J, bool& isl) {
 // over the Dv rows of the head, z read from the merged projection row
 // (z = zrow + t * xs, columns hv*Dv ..); y is also stored when non-null. The
 // norm spans all 128 rows of a head, so the gated form runs with WV = 8.
-// grid (Hv * 8/WV, nseq), block 64*WV.
+// 1D grid of Hv * 8/WV * nseq groups, block 64*WV.
 template <int R, bool GATED, int WV>
 __global__ __launch_bounds__(64 * WV) void prefill_chunk_kernel(
     float* __restrict__ state, const int32_t* __restrict__ slot_ids,
@@ -473,14 +473,32 @@ __global__ __launch_bounds__(64 * WV) void prefill_chunk_kernel(
     float norm_eps, uint16_t* __restrict__ out, uint32_t* __restrict__ status) {
   static_assert(WV == 8 || WV == 4 || WV == 2, "8, 4 or 2 waves per group");
   static_assert(!GATED || WV == 8, "the gated epilogue needs a head's 128 rows in one group");
-  constexpr int NT = 64 * WV, NS = 8 / WV;
+  constexpr int NT = 64 * WV, NS = 8 / WV, GK = R * NS;
   constexpr int UK = kC * kDk / 8 / NT;  // 16-byte input units per thread and matrix
   __shared__ ChunkSmem sm;
-  const int hv = blockIdx.x / NS, s = blockIdx.y;
-  const int Hv = Hk * R, hk = hv / R;
+  const int Hv = Hk * R;
+  // 1D grid of Hv * NS * nseq groups. Work-groups are dealt to the 8 XCDs
+  // round-robin; the GK = R * NS groups that read one key head's k and q (its
+  // value heads, all row blocks) are numbered 8 apart, so they run on one XCD
+  // and fetch those rows from HBM once.
+  int hv, ns, s;
+  {
+    const int L = blockIdx.x;
+    if ((int)gridDim.x % (8 * GK) == 0) {
+      const int m = L >> 3, g = (L & 7) + 8 * (m / GK), r = m % GK;
+      s = g / Hk;
+      hv = (g % Hk) * R + r / NS;
+      ns = r % NS;
+    } else {
+      ns = L % NS;
+      hv = (L / NS) % Hv;
+      s = L / (NS * Hv);
+    }
+  }
+  const int hk = hv / R;
   const int tid = threadIdx.x, lane0 = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, scalar
-  const int dv0 = 16 * ((blockIdx.x % NS) * WV + w);       // this wave's first state row
+  const int dv0 = 16 * (ns * WV + w);                      // this wave's first state row
   const int slot = slot_ids[s];
   if ((unsigned)slot >= (unsigned)num_slots) {
     if (tid == 0 && blockIdx.x == 0) flag_status(status, GDN_FLAG_BAD_SLOT);
@@ -597,8 +615,8 @@ __global__ __launch_bounds__(64 * WV) void prefill_chunk_kernel(
     // substitution with four lanes per column: lane (j = l/4, p = l%4) sums
     // the terms k = p (mod 4) of each row and two DPP adds close the sum over
     // its quad, so a row costs a handful of dependent VALU ops. The
-    // off-diagonal blocks of L and the blocks of P go to waves 4-7 (to every
-    // wave with fewer than 8).
+    // off-diagonal blocks of L and the blocks of P go mostly to waves 4-7 (to
+    // every wave with fewer than 8).
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       if (w != I % WV) continue;
@@ -633,7 +651,10 @@ __global__ __launch_bounds__(64 * WV) void prefill_chunk_kernel(
     }
 #pragma unroll
     for (int t = 0; t < 16; ++t) {
-      if (w != (WV == 8 ? 4 + t % 4 : t % WV)) continue;
+      // with 8 waves: three blocks each to waves 4-7 and one P block each to
+      // the inverting waves 0-3, which balances the two halves (measured)
+      constexpr int kOwn8[16] = {4, 5, 6, 7, 4, 5, 0, 1, 2, 3, 6, 7, 4, 5, 6, 7};
+      if (w != (WV == 8 ? kOwn8[t] : t % WV)) continue;
       int I, J;
       bool isl;
       other_block(t, I, J, isl);
@@ -831,26 +852,27 @@ static hipError_t launch_prefill_r(const PrefillArgs& a) {
                      a.total_tokens, a.mixed, a.xstride, a.status);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  // Work-groups per head: one 8-wave group while the heads of the batch fill
-  // the machine, else the state rows split over 2 or 4 groups per head.
+  // Waves per work-group: 8 (one group per head) while the batch's heads fill
+  // the machine, else the state rows split over 2 or 4 groups per head so
+  // that a few long prompts still spread over the CUs.
   const int units = Hv * a.nseq;
   if (a.out)
-    hipLaunchKernelGGL((prefill_chunk_kernel<R, true, 8>), dim3(Hv, a.nseq), dim3(512), 0,
+    hipLaunchKernelGGL((prefill_chunk_kernel<R, true, 8>), dim3(units), dim3(512), 0,
                        a.stream, a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk,
                        a.total_tokens, ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, a.y, a.mixed + D,
                        a.xstride, a.norm_w, a.norm_eps, a.out, a.status);
   else if (units >= 192)
-    hipLaunchKernelGGL((prefill_chunk_kernel<R, false, 8>), dim3(Hv, a.nseq), dim3(512), 0,
+    hipLaunchKernelGGL((prefill_chunk_kernel<R, false, 8>), dim3(units), dim3(512), 0,
                        a.stream, a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk,
                        a.total_tokens, ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, a.y, nullptr,
                        a.xstride, nullptr, 0.0f, nullptr, a.status);
   else if (units >= 96)
-    hipLaunchKernelGGL((prefill_chunk_kernel<R, false, 4>), dim3(Hv * 2, a.nseq), dim3(256), 0,
+    hipLaunchKernelGGL((prefill_chunk_kernel<R, false, 4>), dim3(units * 2), dim3(256), 0,
                        a.stream, a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk,
                        a.total_tokens, ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, a.y, nullptr,
                        a.xstride, nullptr, 0.0f, nullptr, a.status);
   else
-    hipLaunchKernelGGL((prefill_chunk_kernel<R, false, 2>), dim3(Hv * 4, a.nseq), dim3(128), 0,
+    hipLaunchKernelGGL((prefill_chunk_kernel<R, false, 2>), dim3(units * 4), dim3(128), 0,
                        a.stream, a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk,
                        a.total_tokens, ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, a.y, nullptr,
                        a.xstride, nullptr, 0.0f, nullptr, a.status);
