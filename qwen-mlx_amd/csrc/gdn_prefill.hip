@@ -269,14 +269,14 @@ __global__ __launch_bounds__(256) void prefill_conv_state_kernel(
 //   S^T <- exp(G_C) S^T + K^T (exp(G_C - G) * V')
 // which equals the token-by-token recurrence of metal_gdn.rs:37-62.
 //
-// Work split. The Dv rows of S evolve independently, so a head's 128 rows are
-// cut over 8/WV work-groups of WV waves, 16 rows per wave: a long prompt
-// spreads over Hv*8/WV groups instead of Hv. Each group forms the chunk's
-// state-independent matrices itself: each of four waves takes one diagonal
-// 16x16 block of L and inverts it, D_I = (I + L_II)^-1, while the other waves
-// form the off-diagonal blocks of L and the blocks of P. Every wave then works
-// on its own 16 state rows, held in MFMA accumulators across chunks. A chunk
-// needs three work-group barriers: inputs staged, matrices formed, chunk done.
+// Work split. One work-group of 8 waves per (sequence, value head), each wave
+// owning 16 of the 128 state rows (the rows of S evolve independently). The
+// group forms the chunk's state-independent matrices itself: each of four
+// waves takes one diagonal 16x16 block of L and inverts it, D_I = (I +
+// L_II)^-1, while the waves share the off-diagonal blocks of L and the blocks
+// of P. Every wave then works on its own 16 state rows, held in MFMA
+// accumulators across chunks. A chunk needs three work-group barriers: inputs
+// staged, matrices formed, chunk done.
 //
 // Operand layouts of v_mfma_f32_16x16x32_bf16 (lane l, q = l/16, c = l%16):
 // an A operand holds row c, k slots 8q..8q+7; a B operand column c, the same k
@@ -323,6 +323,7 @@ struct __attribute__((aligned(16))) ChunkSmem {
   uint16_t D[4 * kLdDB];       // D_I, rows of kLdD, hi/lo interleaved per 4 columns
   float Ld[4 * kLdLB];         // diagonal blocks of L (f32): row i, column 4m + p at 4p + m
   float beta[kC], G[kC], eG[kC], dec[kC];  // G: cumulative log2 decay
+  uint16_t Y[kC][kDv + 8];     // the chunk's outputs y (bf16), written out as whole rows
   float ysq[kC][8];            // gated epilogue: per token, each wave's sum of y^2
 };
 
@@ -459,11 +460,20 @@ __device__ __forceinline__ void other_block(int t, int& I, int& J, bool& isl) {
 // With GATED the RMSNormGated epilogue (qwen3_5.rs:660-665) runs on the
 // chunk's outputs: out[t, hv, :] = silu(z) * rms_norm(y, norm_w, norm_eps)
 // over the Dv rows of the head, z read from the merged projection row
-// (z = zrow + t * xs, columns hv*Dv ..); y is also stored when non-null. The
-// norm spans all 128 rows of a head, so the gated form runs with WV = 8.
-// 1D grid of Hv * 8/WV * nseq groups, block 64*WV.
-template <int R, bool GATED, int WV>
-__global__ __launch_bounds__(64 * WV) void prefill_chunk_kernel(
+// (z = zrow + t * xs, columns hv*Dv ..); y is also stored when non-null.
+//
+// One work-group of 8 waves per (sequence, value head): the chunks of a
+// sequence are a serial chain, so the time per chunk of one group sets the
+// kernel time; splitting a head's rows over more, smaller groups lengthens it
+// (measured for one 16,384-token prompt: 1.49 ms with 32 groups of 8 waves,
+// 1.79 ms with 64 of 4, 2.26 ms with 128 of 2). The chunk's outputs go
+// through LDS and leave as whole 256-byte rows.
+//
+// 1D grid of Hv * nseq groups. Work-groups are dealt to the 8 XCDs
+// round-robin; the R groups that read one key head's k and q are numbered 8
+// apart, so they run on one XCD and fetch those rows from HBM once.
+template <int R, bool GATED>
+__global__ __launch_bounds__(512) void prefill_chunk_kernel(
     float* __restrict__ state, const int32_t* __restrict__ slot_ids,
     const int32_t* __restrict__ cu, int num_slots, int Hk, int T,
     const uint16_t* __restrict__ qn, const uint16_t* __restrict__ kn,
@@ -471,34 +481,26 @@ __global__ __launch_bounds__(64 * WV) void prefill_chunk_kernel(
     const uint16_t* __restrict__ betav, uint16_t* __restrict__ y,
     const uint16_t* __restrict__ zrow, int64_t xs, const uint16_t* __restrict__ norm_w,
     float norm_eps, uint16_t* __restrict__ out, uint32_t* __restrict__ status) {
-  static_assert(WV == 8 || WV == 4 || WV == 2, "8, 4 or 2 waves per group");
-  static_assert(!GATED || WV == 8, "the gated epilogue needs a head's 128 rows in one group");
-  constexpr int NT = 64 * WV, NS = 8 / WV, GK = R * NS;
+  constexpr int NT = 512;
   constexpr int UK = kC * kDk / 8 / NT;  // 16-byte input units per thread and matrix
   __shared__ ChunkSmem sm;
   const int Hv = Hk * R;
-  // 1D grid of Hv * NS * nseq groups. Work-groups are dealt to the 8 XCDs
-  // round-robin; the GK = R * NS groups that read one key head's k and q (its
-  // value heads, all row blocks) are numbered 8 apart, so they run on one XCD
-  // and fetch those rows from HBM once.
-  int hv, ns, s;
+  int hv, s;
   {
     const int L = blockIdx.x;
-    if ((int)gridDim.x % (8 * GK) == 0) {
-      const int m = L >> 3, g = (L & 7) + 8 * (m / GK), r = m % GK;
+    if ((int)gridDim.x % (8 * R) == 0) {
+      const int m = L >> 3, g = (L & 7) + 8 * (m / R);
       s = g / Hk;
-      hv = (g % Hk) * R + r / NS;
-      ns = r % NS;
+      hv = (g % Hk) * R + m % R;
     } else {
-      ns = L % NS;
-      hv = (L / NS) % Hv;
-      s = L / (NS * Hv);
+      hv = L % Hv;
+      s = L / Hv;
     }
   }
   const int hk = hv / R;
   const int tid = threadIdx.x, lane0 = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, scalar
-  const int dv0 = 16 * (ns * WV + w);                      // this wave's first state row
+  const int dv0 = 16 * w;                                  // this wave's first state row
   const int slot = slot_ids[s];
   if ((unsigned)slot >= (unsigned)num_slots) {
     if (tid == 0 && blockIdx.x == 0) flag_status(status, GDN_FLAG_BAD_SLOT);
@@ -512,14 +514,9 @@ __global__ __launch_bounds__(64 * WV) void prefill_chunk_kernel(
   f32x4 acc[8];  // S^T tiles: dk rows 16a + 4q + r, state row dv0 + c
 #pragma unroll
   for (int a = 0; a < 8; ++a) acc[a] = *reinterpret_cast<const f32x4*>(gstate + 16 * a);
-  // gated epilogue: norm weights of this lane's 4 output rows, and its z columns
-  f32x4 nw = {0.f, 0.f, 0.f, 0.f};
-  const uint16_t* zcol = nullptr;
-  if constexpr (GATED) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) nw[r] = bf2f(norm_w[dv0 + 4 * q0 + r]);
-    zcol = zrow + (size_t)hv * kDv + dv0 + 4 * q0;
-  }
+  // write-out layout: thread (tokens tid/16 and 32 + tid/16, 8 output rows
+  // from 8 * (tid % 16)); 16 lanes cover one token's 256-byte row
+  const int oi = tid >> 4, od = 8 * (tid & 15);
   // Blocks of P above the diagonal are never written: zero them once.
   for (int e = tid; e < kC * kLdP / 4; e += NT) reinterpret_cast<uint2*>(&sm.P[0][0])[e] = make_uint2(0u, 0u);
 
@@ -542,9 +539,9 @@ __global__ __launch_bounds__(64 * WV) void prefill_chunk_kernel(
         const size_t row = ((size_t)(c + i) * Hk + hk) * kDk;
         kv[u] = *reinterpret_cast<const uint4*>(kn + row + 8 * m);
         const int dq = 32 * (m >> 2) + 4 * (m & 3);
-        const uint2 q0 = *reinterpret_cast<const uint2*>(qn + row + dq);
-        const uint2 q1 = *reinterpret_cast<const uint2*>(qn + row + dq + 16);
-        qv[u] = make_uint4(q0.x, q0.y, q1.x, q1.y);
+        const uint2 qa = *reinterpret_cast<const uint2*>(qn + row + dq);
+        const uint2 qb = *reinterpret_cast<const uint2*>(qn + row + dq + 16);
+        qv[u] = make_uint4(qa.x, qa.y, qb.x, qb.y);
       }
     }
     // v through a buffer resource whose size ends at the chunk's last token
@@ -563,7 +560,6 @@ __global__ __launch_bounds__(64 * WV) void prefill_chunk_kernel(
       pl = lgv[(size_t)(c + lane0) * Hv + hv];
     }
   };
-
   load_inputs(st);
   for (int c0 = st; c0 < en; c0 += kC) {
     const int n = min(kC, en - c0);
@@ -610,16 +606,16 @@ __global__ __launch_bounds__(64 * WV) void prefill_chunk_kernel(
     __syncthreads();
     if (c0 + kC < en) load_inputs(c0 + kC);
 
-    // (b) the chunk's matrices. Diagonal block I of L goes to wave I % WV,
-    // which forms it and inverts it, D_I = (I + L_II)^-1, by forward
-    // substitution with four lanes per column: lane (j = l/4, p = l%4) sums
-    // the terms k = p (mod 4) of each row and two DPP adds close the sum over
-    // its quad, so a row costs a handful of dependent VALU ops. The
-    // off-diagonal blocks of L and the blocks of P go mostly to waves 4-7 (to
-    // every wave with fewer than 8).
+    // (b) the chunk's matrices. Diagonal block I of L goes to wave I, which
+    // forms it and inverts it, D_I = (I + L_II)^-1, by forward substitution
+    // with four lanes per column: lane (j = l/4, p = l%4) sums the terms
+    // k = p (mod 4) of each row and two DPP adds close the sum over its quad,
+    // so a row costs a handful of dependent VALU ops. Of the other 16 blocks,
+    // waves 4-7 take three each and waves 0-3 one each, which balances the two
+    // halves (measured).
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
-      if (w != I % WV) continue;
+      if (w != I) continue;
       put_l(sm, tile_kk(sm, kf, I, I), I, I, q, c);
       // this wave's own Ld writes, read back by other lanes of the wave
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -651,10 +647,8 @@ __global__ __launch_bounds__(64 * WV) void prefill_chunk_kernel(
     }
 #pragma unroll
     for (int t = 0; t < 16; ++t) {
-      // with 8 waves: three blocks each to waves 4-7 and one P block each to
-      // the inverting waves 0-3, which balances the two halves (measured)
-      constexpr int kOwn8[16] = {4, 5, 6, 7, 4, 5, 0, 1, 2, 3, 6, 7, 4, 5, 6, 7};
-      if (w != (WV == 8 ? kOwn8[t] : t % WV)) continue;
+      constexpr int kOwn[16] = {4, 5, 6, 7, 4, 5, 0, 1, 2, 3, 6, 7, 4, 5, 6, 7};
+      if (w != kOwn[t]) continue;
       int I, J;
       bool isl;
       other_block(t, I, J, isl);
@@ -720,7 +714,7 @@ __global__ __launch_bounds__(64 * WV) void prefill_chunk_kernel(
       vplz[I] = cat(vl, kZero4);
     }
     // (e) O^T_I = exp(G) Zt_I + V'^T P^T: rows dv0 + 4q + r, token 16I + c
-    f32x4 yo[4];
+    // y (bf16) into the LDS rows; with GATED each wave's sum of y^2 per token
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       f32x4 o = zt[I] * sm.eG[16 * I + c];
@@ -729,22 +723,11 @@ __global__ __launch_bounds__(64 * WV) void prefill_chunk_kernel(
         if (2 * p > I) continue;
         o = mfma32(cat(vph[2 * p], vph[2 * p + 1]), lds8(&sm.P[16 * I + c][32 * p + 8 * q]), o);
       }
-      yo[I] = o;
-      const int i = 16 * I + c;
-      if (y != nullptr && i < n)
-        *reinterpret_cast<uint2*>(y + ((size_t)(c0 + i) * Hv + hv) * kDv + dv0 + 4 * q) =
-            make_uint2(f2bf2(o[0], o[1]), f2bf2(o[2], o[3]));
-    }
-    uint2 zv[4];
-    if constexpr (GATED) {  // z of the outputs, and each wave's sums of y^2 per token
-#pragma unroll
-      for (int I = 0; I < 4; ++I) {
-        zv[I] = *reinterpret_cast<const uint2*>(zcol + (size_t)min(c0 + 16 * I + c, en - 1) * xs);
-        f32x4 yb;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) yb[r] = rbf(yo[I][r]);
-        yo[I] = yb;
-        float ss = (yb[0] * yb[0] + yb[1] * yb[1]) + (yb[2] * yb[2] + yb[3] * yb[3]);
+      const uint2 yb = make_uint2(f2bf2(o[0], o[1]), f2bf2(o[2], o[3]));
+      *reinterpret_cast<uint2*>(&sm.Y[16 * I + c][dv0 + 4 * q]) = yb;
+      if constexpr (GATED) {
+        const float y0 = bf_lo(yb.x), y1 = bf_hi(yb.x), y2 = bf_lo(yb.y), y3 = bf_hi(yb.y);
+        float ss = (y0 * y0 + y1 * y1) + (y2 * y2 + y3 * y3);
         ss += __shfl_xor(ss, 16, 64);
         ss += __shfl_xor(ss, 32, 64);
         if (q == 0) sm.ysq[16 * I + c][w] = ss;
@@ -774,21 +757,34 @@ __global__ __launch_bounds__(64 * WV) void prefill_chunk_kernel(
       }
     }
     __syncthreads();
-    if constexpr (GATED) {  // RMSNormGated over the 128 rows of each token
+    // (g) write-out: thread (tokens oi and oi + 32, rows od..od+7) stores 16
+    // bytes of y per token; GATED: out = silu(z) * bf16(w * bf16(y * rn)), rn
+    // from the 8 waves' sums of y^2
 #pragma unroll
-      for (int I = 0; I < 4; ++I) {
-        const int i = 16 * I + c;
+    for (int h = 0; h < 2; ++h) {
+      const int i = oi + 32 * h;
+      if (i >= n) continue;
+      const uint4 yv = *reinterpret_cast<const uint4*>(&sm.Y[i][od]);
+      const size_t row = ((size_t)(c0 + i) * Hv + hv) * kDv + od;
+      if (y != nullptr) *reinterpret_cast<uint4*>(y + row) = yv;
+      if constexpr (GATED) {
         const f32x4 p0 = *reinterpret_cast<const f32x4*>(&sm.ysq[i][0]);
         const f32x4 p1 = *reinterpret_cast<const f32x4*>(&sm.ysq[i][4]);
         const float tot = ((p0[0] + p0[1]) + (p0[2] + p0[3])) + ((p1[0] + p1[1]) + (p1[2] + p1[3]));
         const float rn = 1.0f / sqrtf(tot / (float)kDv + norm_eps);
-        const float z4[4] = {bf_lo(zv[I].x), bf_hi(zv[I].x), bf_lo(zv[I].y), bf_hi(zv[I].y)};
-        f32x4 ov;
+        const uint4 zv = *reinterpret_cast<const uint4*>(zrow + (size_t)(c0 + i) * xs + (size_t)hv * kDv + od);
+        const uint4 nv = *reinterpret_cast<const uint4*>(norm_w + od);  // the rows' norm weights
+        const uint32_t yw[4] = {yv.x, yv.y, yv.z, yv.w};
+        const uint32_t zw[4] = {zv.x, zv.y, zv.z, zv.w};
+        const uint32_t ww[4] = {nv.x, nv.y, nv.z, nv.w};
+        uint32_t ow[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) ov[r] = silu_bf16(z4[r]) * rbf(nw[r] * rbf(yo[I][r] * rn));
-        if (i < n)
-          *reinterpret_cast<uint2*>(out + ((size_t)(c0 + i) * Hv + hv) * kDv + dv0 + 4 * q) =
-              make_uint2(f2bf2(ov[0], ov[1]), f2bf2(ov[2], ov[3]));
+        for (int e = 0; e < 4; ++e) {
+          const float o0 = silu_bf16(bf_lo(zw[e])) * rbf(bf_lo(ww[e]) * rbf(bf_lo(yw[e]) * rn));
+          const float o1 = silu_bf16(bf_hi(zw[e])) * rbf(bf_hi(ww[e]) * rbf(bf_hi(yw[e]) * rn));
+          ow[e] = f2bf2(o0, o1);
+        }
+        *reinterpret_cast<uint4*>(out + row) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
       }
     }
   }
@@ -852,30 +848,17 @@ static hipError_t launch_prefill_r(const PrefillArgs& a) {
                      a.total_tokens, a.mixed, a.xstride, a.status);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  // Waves per work-group: 8 (one group per head) while the batch's heads fill
-  // the machine, else the state rows split over 2 or 4 groups per head so
-  // that a few long prompts still spread over the CUs.
   const int units = Hv * a.nseq;
   if (a.out)
-    hipLaunchKernelGGL((prefill_chunk_kernel<R, true, 8>), dim3(units), dim3(512), 0,
-                       a.stream, a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk,
-                       a.total_tokens, ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, a.y, a.mixed + D,
-                       a.xstride, a.norm_w, a.norm_eps, a.out, a.status);
-  else if (units >= 192)
-    hipLaunchKernelGGL((prefill_chunk_kernel<R, false, 8>), dim3(units), dim3(512), 0,
-                       a.stream, a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk,
-                       a.total_tokens, ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, a.y, nullptr,
-                       a.xstride, nullptr, 0.0f, nullptr, a.status);
-  else if (units >= 96)
-    hipLaunchKernelGGL((prefill_chunk_kernel<R, false, 4>), dim3(units * 2), dim3(256), 0,
-                       a.stream, a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk,
-                       a.total_tokens, ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, a.y, nullptr,
-                       a.xstride, nullptr, 0.0f, nullptr, a.status);
+    hipLaunchKernelGGL((prefill_chunk_kernel<R, true>), dim3(units), dim3(512), 0, a.stream,
+                       a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk, a.total_tokens,
+                       ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, a.y, a.mixed + D, a.xstride,
+                       a.norm_w, a.norm_eps, a.out, a.status);
   else
-    hipLaunchKernelGGL((prefill_chunk_kernel<R, false, 2>), dim3(units * 4), dim3(128), 0,
-                       a.stream, a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk,
-                       a.total_tokens, ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, a.y, nullptr,
-                       a.xstride, nullptr, 0.0f, nullptr, a.status);
+    hipLaunchKernelGGL((prefill_chunk_kernel<R, false>), dim3(units), dim3(512), 0, a.stream,
+                       a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk, a.total_tokens,
+                       ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, a.y, nullptr, a.xstride, nullptr,
+                       0.0f, nullptr, a.status);
   return hipGetLastError();
 }
 
