@@ -450,7 +450,14 @@ gdn_status gdn_exec_decode_batch(gdn_exec* exec, const uint64_t* seq_ids, const 
 /* ModelExecutor::submit_batch / collect_batch (executor.rs:31-42): queue the
  * step and return at once; collect waits for it. One batch in flight at a
  * time (a second submit before collect fails). A prefill between the two is
- * allowed (it waits for the batch). */
+ * allowed (it waits for the batch).
+ * A decode step replays HIP graphs: the first step at a batch size B
+ * captures the step's launches (on a private stream) as one graph per span
+ * between attention calls, which run eagerly because their launch shape
+ * follows the step's KV plan; later steps at B launch the graphs on the
+ * executor's stream. Results are bit-identical to launching kernel by kernel,
+ * which the environment variable GDN_EXEC_GRAPHS=0 (read at gdn_exec_create)
+ * selects. A batch size whose capture fails runs eagerly. */
 gdn_status gdn_exec_submit_batch(gdn_exec* exec, const uint64_t* seq_ids, const uint32_t* tokens,
                                  int32_t B);
 gdn_status gdn_exec_collect_batch(gdn_exec* exec, uint32_t* next_tokens, int32_t B);

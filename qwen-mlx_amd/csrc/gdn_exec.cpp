@@ -18,6 +18,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
+#include <cstdlib>
 #include <cstdio>
 #include <string>
 #include <unordered_map>
@@ -105,6 +106,16 @@ struct gdn_exec {
   bool inflight = false;
   int32_t inflight_B = 0;
   int32_t logits_rows = 0;
+  // Decode steps replay HIP graphs, one per batch size: the step's launches
+  // between attention calls captured once as segments (an attention call's
+  // launch shape follows the step's KV plan, so it runs eagerly between them).
+  bool use_graphs = true;
+  hipStream_t cap = nullptr;  // private stream the segments are captured on
+  struct StepGraphs {
+    std::vector<hipGraphExec_t> seg;
+    bool failed = false;  // capture refused (e.g. a debug check syncing): run eagerly
+  };
+  std::unordered_map<int32_t, StepGraphs> graphs;
 };
 
 namespace {
@@ -112,6 +123,10 @@ namespace {
 void exec_release(gdn_exec* x) {
   if (!x) return;
   if (x->stream) (void)hipStreamSynchronize(x->stream);
+  else (void)hipDeviceSynchronize();
+  for (auto& kv : x->graphs)
+    for (hipGraphExec_t g : kv.second.seg) (void)hipGraphExecDestroy(g);
+  if (x->cap) (void)hipStreamDestroy(x->cap);
   for (void* p : {(void*)x->d_dec, (void*)x->d_pre, (void*)x->d_next, (void*)x->h, (void*)x->hn,
                   (void*)x->mix, (void*)x->logits, (void*)x->d_pv, (void*)x->d_pi, (void*)x->qkv,
                   (void*)x->att})
@@ -178,27 +193,103 @@ gdn_status run_layers(gdn_exec* x, int n, bool prefill, int nseq = 0) {
   return GDN_OK;
 }
 
-// lm_head + argmax of n rows starting at row r0 of h (after the last
-// layer's residual add), picked tokens into d_next and the pinned `dst`.
-gdn_status pick(gdn_exec* x, int r0, int n, int32_t* dst) {
-  uint16_t* hr = x->h + (size_t)r0 * x->hidden;
-  const uint16_t* mr = x->stack.empty() ? nullptr : x->mix + (size_t)r0 * x->hidden;
-  uint16_t* nr = x->hn + (size_t)r0 * x->hidden;
+// One attention layer's gdn_attn_forward on rows already projected into qkv.
+gdn_status attn_call(gdn_exec* x, int ai) {
+  const gdn_exec::Attn& a = x->attn[ai];
+  const int qw = 2 * x->Hq * 256, kw = x->Hkv * 256;
+  return gdn_attn_forward(x->kv, ai, x->qkv, x->nqkv, x->qkv + qw, x->nqkv, x->qkv + qw + kw,
+                          x->nqkv, a.q_norm_w, a.k_norm_w, x->eps, x->rope_theta, x->rotary_dim,
+                          x->att, x->Hq * 256, x->stream);
+}
+
+// Segment k of a decode step over B rows (segments end at each attention
+// call): segment 0 starts with the embedding, every segment but the last ends
+// with an attention layer's q|k|v projection, the next one starts with its
+// output projection, and the last ends with lm_head and the greedy pick into
+// d_next. The segments and the attention calls between them, in order, are
+// the step.
+gdn_status decode_seg(gdn_exec* x, int B, int k) {
+  int seg = 0;
+  if (k == 0)
+    HIP_TRY(gdn::launch_embed(x->embed, x->d_dec + x->max_batch, B, x->vocab, x->hidden, x->h,
+                              x->stream),
+            "embedding");
+  for (size_t p = 0; p < x->stack.size(); ++p) {
+    const int e = x->stack[p];
+    if (seg == k) {
+      HIP_TRY(gdn::launch_add_norm(x->h, p == 0 ? nullptr : x->mix, p == 0 ? nullptr : &x->pend,
+                                   B, x->hidden, x->norm_w[p], x->eps, x->hn, x->stream),
+              "residual add + norm");
+      x->pend = gdn::QPartial{};
+      if (e >= 0) {
+        GDN_TRY(gdn::layer_decode(x->layers[e], x->d_dec, B, x->hn, x->hidden, x->mix, x->hidden,
+                                  x->stream, &x->pend));
+      } else {
+        GDN_TRY(gdn_qlinear_forward(x->attn[-e - 1].qkv, x->hn, x->hidden, B, x->qkv, x->nqkv,
+                                    x->stream));
+      }
+    }
+    if (e < 0) {
+      ++seg;
+      if (seg == k)
+        GDN_TRY(gdn::qlinear_forward(x->attn[-e - 1].o, x->att, x->Hq * 256, B, x->mix, x->hidden,
+                                     x->stream, &x->pend));
+    }
+  }
+  if (seg != k) return GDN_OK;
   gdn::QPartial pp = x->pend;
-  if (pp.nslice > 0) pp.part += (size_t)r0 * pp.Npad;
-  HIP_TRY(gdn::launch_add_norm(hr, mr, mr ? &pp : nullptr, n, x->hidden, x->final_norm_w, x->eps,
-                               nr, x->stream),
+  HIP_TRY(gdn::launch_add_norm(x->h, x->stack.empty() ? nullptr : x->mix,
+                               x->stack.empty() ? nullptr : &pp, B, x->hidden, x->final_norm_w,
+                               x->eps, x->hn, x->stream),
           "final norm");
   x->pend = gdn::QPartial{};
-  GDN_TRY(gdn_qlinear_forward(x->head, nr, x->hidden, n, x->logits, x->vocab, x->stream));
-  HIP_TRY(gdn::launch_argmax(x->logits, x->vocab, n, x->vocab, x->d_pv, x->d_pi, x->d_next,
+  GDN_TRY(gdn_qlinear_forward(x->head, x->hn, x->hidden, B, x->logits, x->vocab, x->stream));
+  HIP_TRY(gdn::launch_argmax(x->logits, x->vocab, B, x->vocab, x->d_pv, x->d_pi, x->d_next,
                              x->stream),
           "argmax");
-  HIP_TRY(hipMemcpyAsync(dst, x->d_next, sizeof(int32_t) * n, hipMemcpyDeviceToHost, x->stream),
-          "token copy");
-  x->logits_rows = n;
   return GDN_OK;
 }
+
+// Captures the B-row decode step's segments into graphs (once per B). A
+// capture that fails leaves the batch size on the eager path.
+gdn_exec::StepGraphs& step_graphs(gdn_exec* x, int B) {
+  gdn_exec::StepGraphs& sg = x->graphs[B];
+  if (!sg.seg.empty() || sg.failed) return sg;
+  const int nseg = (int)x->attn.size() + 1;
+  if (!x->cap && hipStreamCreateWithFlags(&x->cap, hipStreamNonBlocking) != hipSuccess) {
+    (void)hipGetLastError();
+    sg.failed = true;
+    return sg;
+  }
+  hipStream_t saved = x->stream;
+  x->stream = x->cap;
+  const gdn::QPartial pend0 = x->pend;
+  for (int k = 0; k < nseg && !sg.failed; ++k) {
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    if (hipStreamBeginCapture(x->cap, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+      sg.failed = true;
+      break;
+    }
+    const gdn_status st = decode_seg(x, B, k);
+    const hipError_t e = hipStreamEndCapture(x->cap, &g);
+    if (st != GDN_OK || e != hipSuccess || !g ||
+        hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess)
+      sg.failed = true;
+    else
+      sg.seg.push_back(ge);
+    if (g) (void)hipGraphDestroy(g);
+  }
+  x->stream = saved;
+  x->pend = pend0;
+  if (sg.failed) {
+    (void)hipGetLastError();
+    for (hipGraphExec_t ge : sg.seg) (void)hipGraphExecDestroy(ge);
+    sg.seg.clear();
+  }
+  return sg;
+}
+
 
 }  // namespace
 
@@ -304,6 +395,10 @@ gdn_status gdn_exec_create(const gdn_exec_desc* desc, void* stream, gdn_exec** o
   x->rows = rows;
   x->device = d.device;
   x->stream = static_cast<hipStream_t>(stream);
+  {
+    const char* g = getenv("GDN_EXEC_GRAPHS");
+    x->use_graphs = !(g && g[0] == '0' && g[1] == 0);
+  }
   const size_t act = (size_t)x->rows * hidden * sizeof(uint16_t);
   bool ok = hipMalloc(&x->d_dec, sizeof(int32_t) * 2 * d.max_batch) == hipSuccess &&
             hipMalloc(&x->d_pre, sizeof(int32_t) * pre_words(d.max_batch, d.max_prompt)) == hipSuccess &&
@@ -528,11 +623,20 @@ gdn_status gdn_exec_submit_batch(gdn_exec* x, const uint64_t* seq_ids, const uin
   HIP_TRY(hipMemcpyAsync(x->d_dec, x->p_dec, sizeof(int32_t) * 2 * x->max_batch,
                          hipMemcpyHostToDevice, x->stream),
           "batch copy");
-  HIP_TRY(gdn::launch_embed(x->embed, x->d_dec + x->max_batch, B, x->vocab, x->hidden, x->h,
-                            x->stream),
-          "embedding");
-  GDN_TRY(run_layers(x, B, false));
-  GDN_TRY(pick(x, 0, B, x->p_next));
+  const int nseg = (int)x->attn.size() + 1;
+  gdn_exec::StepGraphs* sg = x->use_graphs ? &step_graphs(x, B) : nullptr;
+  const bool replay = sg && !sg->seg.empty();
+  for (int k = 0; k < nseg; ++k) {
+    if (replay)
+      HIP_TRY(hipGraphLaunch(sg->seg[k], x->stream), "decode step graph");
+    else
+      GDN_TRY(decode_seg(x, B, k));
+    if (k + 1 < nseg) GDN_TRY(attn_call(x, k));
+  }
+  HIP_TRY(hipMemcpyAsync(x->p_next, x->d_next, sizeof(int32_t) * B, hipMemcpyDeviceToHost,
+                         x->stream),
+          "token copy");
+  x->logits_rows = B;
   HIP_TRY(hipEventRecord(x->done, x->stream), "gdn_exec_submit_batch event");
   x->inflight = true;
   x->inflight_B = B;

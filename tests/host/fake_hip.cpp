@@ -55,6 +55,26 @@ hipError_t hipGetDeviceCount(int* count) {
   return hipSuccess;
 }
 hipError_t hipStreamSynchronize(hipStream_t) { return hipSuccess; }
+hipError_t hipStreamCreateWithFlags(hipStream_t* stream, unsigned) {
+  *stream = reinterpret_cast<hipStream_t>(new char[8]);
+  return hipSuccess;
+}
+hipError_t hipStreamDestroy(hipStream_t stream) {
+  delete[] reinterpret_cast<char*>(stream);
+  return hipSuccess;
+}
+// No stream capture here: the executor's decode steps take their eager path.
+hipError_t hipStreamBeginCapture(hipStream_t, hipStreamCaptureMode) { return hipErrorNotSupported; }
+hipError_t hipStreamEndCapture(hipStream_t, hipGraph_t* graph) {
+  *graph = nullptr;
+  return hipErrorNotSupported;
+}
+hipError_t hipGraphInstantiate(hipGraphExec_t*, hipGraph_t, hipGraphNode_t*, char*, size_t) {
+  return hipErrorNotSupported;
+}
+hipError_t hipGraphDestroy(hipGraph_t) { return hipSuccess; }
+hipError_t hipGraphExecDestroy(hipGraphExec_t) { return hipSuccess; }
+hipError_t hipGraphLaunch(hipGraphExec_t, hipStream_t) { return hipErrorNotSupported; }
 hipError_t hipDeviceSynchronize(void) { return hipSuccess; }
 hipError_t hipGetLastError(void) { return hipSuccess; }
 const char* hipGetErrorString(hipError_t) { return "host stand-in"; }
