@@ -315,7 +315,7 @@ def qlinear_bench(args):
         roof = {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None,
                 "flop_per_launch": flops}
-    roof.update({"kernel": "qlinear_decode_kernel<2, 8>" if M <= 64 else "qlinear_kernel<2, 4, 2, 2>",
+    roof.update({"kernel": "qlinear_decode_kernel<8, 2>" if M <= 64 else "qlinear_kernel<2, 4, 2, 2>",
                  "kernel_avg_us": round(avg_ms * 1e3, 2),
                  "kernel_timing": "HIP events around each step's back-to-back launches / launches"})
     out = {

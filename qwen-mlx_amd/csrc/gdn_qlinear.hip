@@ -289,205 +289,251 @@ __global__ __launch_bounds__(256) void qlinear_kernel(
   }
 }
 
-// Decode shapes (M <= 64): one 64-row tile, 64 columns per work-group, the K
-// axis split over KS groups of four waves (wave w: column fragment w % 4, K
-// part w / 4) that add their sums through LDS at the end. A launch of a few
-// hundred work-groups with one column fragment per wave is latency-bound, so
-// the S stages of a K part are unrolled and every load is issued early in
-// stage order: x of the first three stages, then the wave's whole weight and
-// scale slice and its correction operands, then x three stages ahead of use.
-// Vector-memory counters drain in issue order, so each stage waits only for
-// its own weights and x, never for the loads queued behind them.
+// s_waitcnt vmcnt(n) (gfx9 encoding; expcnt and lgkmcnt left at their maximum)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Decode shapes (M <= 64). A work-group owns 64 columns (four 16-wide
+// fragments) and the K slice of NW * SPW stages starting at stage
+// NW * SPW * blockIdx.y; wave w takes SPW stages of it and computes partial
+// sums of all 64 x 64 outputs of its stages. The NW partial tiles are added
+// through LDS at the end in wave order, each wave finishing 16 / NW of the
+// sixteen 16 x 16 tiles (correction and store).
 //
-// A work-group covers the K slice [kof, kof + 128 KS S) of a K-wide layer,
-// kof = 128 KS S * blockIdx.y. With one slice (gridDim.y == 1) it writes bf16
-// y; with several (layers too narrow in N to fill the chip) it writes its f32
-// partial sums, correction of its own groups included, to
-// part[blockIdx.y][m][n] (row stride Npad), and qlinear_sum_kernel adds the
-// slices in order and rounds once.
-template <int KS, int S>
-__global__ __launch_bounds__(256 * KS) void qlinear_decode_kernel(
+// Roles: x is the MFMA A operand and the weights the B operand, so a lane
+// holds D[m][n] for four rows m = 16u + 4c + i and one column n = r16 of the
+// fragment, and the per-group scale it applies is a single number.
+//
+// x goes through LDS: every work-group reads all of x, and a load of 16 rows x
+// 64 B (the MFMA operand layout) ran at less than half the rate of whole
+// 128-B rows through a CU's vector memory path, so each wave copies its own
+// x slice, one group (64 rows x 64 k) at a time, with loads of 8 rows x 128 B
+// straight into LDS (no VGPRs), the 16-B chunks of a row XOR-swizzled by
+// (row / 2) % 8 so that the operand reads (ds_read_b128 of 16 rows) are
+// conflict-free. Two buffers per wave: group q + 2 is loaded while q + 1 is
+// in flight and q is used. Only the wave itself reads its buffers, so the
+// hand-off is a vmcnt wait, no barrier; the buffers are two separate arrays
+// so the compiler can tell loads into one from reads of the other.
+//
+// X_g (the group sums of x) comes from MFMAs of x against 0/1 row selectors
+// (the A operand, ones in rows 4u..4u+3 for the 16-row block u), chained so
+// the four blocks land in different output rows and lane (r16, c) ends with
+// X_g[16c + r16] in one register, stored to LDS after the loop (an LDS store
+// in the loop would make the compiler wait for every LDS copy in flight).
+//
+// With one slice (gridDim.y == 1) the kernel writes bf16 y; with several it
+// writes its f32 partial sums, correction of its own groups included, to
+// part[blockIdx.y][m][n] (row stride Npad), and qlinear_sum_kernel (or the
+// consumer of a deferred call) adds the slices in order and rounds once.
+template <int NW, int SPW>
+__global__ __launch_bounds__(64 * NW) void qlinear_decode_kernel(
     const uint16_t* __restrict__ x, int64_t xs, int M, int K, const u32x4* __restrict__ wp,
     const uint16_t* __restrict__ sp, const uint16_t* __restrict__ bias,
     const uint16_t* __restrict__ nsc, int N, uint16_t* __restrict__ y, int64_t ys,
     float* __restrict__ part, int Npad) {
-  static_assert(S >= 2 && S % 2 == 0, "S stages per K part, alternating x buffers");
-  constexpr int MT = 64, XROW = kStageK * 2, SJ = MT / 16;
-  constexpr int G = 2 * KS * S;  // groups of the work-group's K slice
-  __shared__ __align__(16) uint8_t xl[KS][2][MT * XROW];
-  __shared__ float sx[G * MT];  // X_g[m] at sx[g*MT + m], g local to the slice
+  constexpr int G = 2 * NW * SPW;  // groups of the slice
+  constexpr int NG = 2 * SPW;      // groups of a wave
+  constexpr int GJ = (G + 31) / 32;
+  constexpr int TPW = 16 / NW;     // tiles each wave finishes
+  constexpr int XR = 32 * GJ + 8;  // bf16 per row of the split X_g arrays (16 B pad)
+  static_assert(NW == 4 || NW == 8, "16 tiles over the waves");
+  // Per wave two x buffers of one group each (64 rows x 128 B, chunk-swizzled);
+  // after the loop the wave's partial tiles (tiles 0-7 in xb0, 8-15 in xb1).
+  __shared__ __align__(16) uint8_t xb0[NW][8192];
+  __shared__ __align__(16) uint8_t xb1[NW][8192];
+  __shared__ __align__(16) float sx[G * 64];          // X_g[m] at sx[g * 64 + m]
+  __shared__ __align__(16) uint16_t xsp[3][64 * XR];  // X_g = hi + mid + lo, [m][g] bf16
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int ks = wave >> 2, wn = wave & 3;
-  const int Ptot = K >> 7, Gtot = K >> 6;
-  const int pbase = blockIdx.y * (KS * S);  // first stage of the slice in the layer
-  const int p0 = ks * S;                    // first stage of the wave's K part in the slice
-  const int f = blockIdx.x * 4 + wn;  // the wave's column fragment
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, c4 = lane >> 4;
+  const int P = K >> 7, Gtot = K >> 6;
+  const int pslice = blockIdx.y * (NW * SPW);
+  const int p0 = pslice + w * SPW;  // first stage of the wave
+  const int fb = blockIdx.x * 4;    // first fragment of the work-group
 
-  // x staging: thread -> rows srow + 16j, chunk sch, of this K part
-  const int lt = tid & 255, srow = lt >> 4, sch = lt & 15;
-  const int sdst = srow * XROW + ((sch ^ srow) << 4);
-  const uint16_t* xsrc[SJ];
+  const u32x4* wsrc = wp + ((int64_t)fb * P + p0) * 64 + lane;
+  // scales of column r16 of each fragment, groups 2p and 2p+1 (one dword)
+  const uint32_t* ssrc = reinterpret_cast<const uint32_t*>(sp) + ((int64_t)fb * P + p0) * 16 + r16;
+  // x rows M..63 read as zeros: the buffer ends with row M-1
+  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)x, (short)0, (int)(((int64_t)(M - 1) * xs + K) * 2), 0x00020000);
+  // group q of the wave into buffer bq: load i covers rows 8i..8i+7, lane L
+  // row 8i + L/8 and chunk (L % 8) ^ ((row / 2) % 8), stored at byte 16 L
+  const int drow = lane >> 3;
+  auto copy_x = [&](int q, int bq) {
+    uint8_t* const sb = bq ? xb1[w] : xb0[w];
 #pragma unroll
-  for (int j = 0; j < SJ; ++j)
-    xsrc[j] = x + (int64_t)min(srow + 16 * j, M - 1) * xs + sch * 8 + (pbase + p0) * kStageK;
-  constexpr int XD = S < 3 ? S : 3;  // x stages in flight
-  u32x4 R[XD][SJ];
-#pragma unroll
-  for (int q = 0; q < XD; ++q) {
-#pragma unroll
-    for (int j = 0; j < SJ; ++j) R[q][j] = *reinterpret_cast<const u32x4*>(xsrc[j] + q * kStageK);
-    __builtin_amdgcn_sched_barrier(0);  // keep the issue order (the counters drain in it)
-  }
+    for (int i = 0; i < 8; ++i) {
+      const int r = 8 * i + drow;
+      const int c = (lane & 7) ^ ((4 * i + (drow >> 1)) & 7);
+      const int voff = (int)((r * xs + 128 * p0 + 64 * q + 8 * c) * 2);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          xrs, (void __attribute__((address_space(3)))*)(sb + i * 1024), 16, voff, 0, 0, 0);
+    }
+  };
+  // chunk c (8 k) of row r in buffer bq
+  auto x_chunk = [&](int bq, int r, int c) -> u32x4 {
+    const uint8_t* const sb = bq ? xb1[w] : xb0[w];
+    return *reinterpret_cast<const u32x4*>(sb + 128 * r + 16 * (c ^ ((r >> 1) & 7)));
+  };
 
-  // Weights, scales and the correction operands are read once: nontemporal,
-  // so the stream does not evict x, which every work-group re-reads, from L2.
-  const u32x4* wsrc = wp + ((int64_t)f * Ptot + pbase + p0) * 64 + lane;
-  const u32x4* ssrc = reinterpret_cast<const u32x4*>(sp) + ((int64_t)f * Ptot + pbase + p0) * 4 + c4;
-  u32x4 wr[S], sr[S];
+  // Issue order (the vmcnt waits below count it): x of groups 0 and 1, then
+  // every weight and scale of the wave, then the correction operands.
+  u32x4 wr[SPW][4];
+  uint32_t sr[SPW][4];
+  copy_x(0, 0);
+  if (NG > 1) copy_x(1, 1);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int p = 0; p < S; ++p) {
-    wr[p] = __builtin_nontemporal_load(wsrc + p * 64);
-    sr[p] = __builtin_nontemporal_load(ssrc + p * 4);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  constexpr int GJ = (G + 31) / 32;  // 32-group blocks of the correction
+  for (int s = 0; s < SPW; ++s)
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      // weights and scales are read once: nontemporal
+      wr[s][f] = __builtin_nontemporal_load(wsrc + (int64_t)f * P * 64 + s * 64);
+      sr[s][f] = __builtin_nontemporal_load(ssrc + (int64_t)f * P * 16 + s * 16);
+    }
+  // correction operands of the fragment this wave finishes (groups beyond the slice: zero)
+  const int fo = (w * TPW) >> 2;
   u32x4 Ab[GJ], As[GJ];
 #pragma unroll
   for (int j = 0; j < GJ; ++j) {
-    Ab[j] = As[j] = (u32x4){0u, 0u, 0u, 0u};
-    if (32 * j + 8 * c4 < G) {  // G is a multiple of 8: whole 8-group words
-      const int64_t o = ((int64_t)f * 16 + r16) * Gtot + 2 * pbase + 32 * j + 8 * c4;
-      Ab[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bias + o));
-      As[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(nsc + o));
-    }
+    const bool gin = 32 * j + 8 * c4 < G;
+    const int64_t o = ((int64_t)(fb + fo) * 16 + r16) * Gtot + 2 * pslice + (gin ? 32 * j + 8 * c4 : 0);
+    Ab[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bias + o));
+    As[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(nsc + o));
+    if (!gin) Ab[j] = As[j] = (u32x4){0u, 0u, 0u, 0u};
   }
   __builtin_amdgcn_sched_barrier(0);
 
+  // T[f][u]: D[m][n] for m = 16u + 4c4 + i, n = 16(fb+f) + r16
+  f32x4 T[4][4];
 #pragma unroll
-  for (int j = 0; j < SJ; ++j) *reinterpret_cast<u32x4*>(&xl[ks][0][sdst + 16 * j * XROW]) = R[0][j];
-  lds_barrier();
-
-  f32x4 T[4];
+  for (int f = 0; f < 4; ++f)
 #pragma unroll
-  for (int u = 0; u < 4; ++u) T[u] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < 4; ++u) T[f][u] = (f32x4){0.f, 0.f, 0.f, 0.f};
   const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   uint32_t nib = 0x000F000Fu;
   asm volatile("" : "+v"(nib));
+  // sel1[u]: the A operand with ones in rows 4u..4u+3 (lane r16 supplies row r16)
+  u32x4 sel1[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) sel1[u] = (r16 >> 2) == u ? ones : (u32x4){0u, 0u, 0u, 0u};
+  float xgv[NG];
+  constexpr int WS = 8 * SPW + 2 * GJ;  // weight, scale and correction loads
 
 #pragma unroll
-  for (int p = 0; p < S; ++p) {
-    const int b = p & 1;
-    if (p + XD < S) {  // x of stage p+XD into the registers stage p's x came in
+  for (int q = 0; q < NG; ++q) {
+    const int b = q & 1, s = q >> 1, gl = q & 1;
+    // x of group q in LDS: the vector-memory ops issued after its copy may be pending
+    if (q == 0) wait_vm<(NG > 1 ? 8 : 0) + WS>();
+    else if (q == 1) wait_vm<WS + (NG > 2 ? 8 : 0)>();
+    else if (q + 1 < NG) wait_vm<8>();
+    else wait_vm<0>();
+    u32x4 X[2][4];
 #pragma unroll
-      for (int i = 0; i < SJ; ++i)
-        R[p % XD][i] = *reinterpret_cast<const u32x4*>(xsrc[i] + (p + XD) * kStageK);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    const uint8_t* xb = xl[ks][b];
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int gl = 0; gl < 2; ++gl) {
-      u32x4 X[4][2];
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int ch = 8 * gl + 4 * h + c4;
-          X[u][h] = *reinterpret_cast<const u32x4*>(&xb[(u * 16 + r16) * XROW + ((ch ^ r16) << 4)]);
-        }
-      {  // X_g of row fragment wn
-        const int row = wn * 16 + r16;
-        const u32x4 s0 = *reinterpret_cast<const u32x4*>(&xb[row * XROW + (((8 * gl + c4) ^ r16) << 4)]);
-        const u32x4 s1 = *reinterpret_cast<const u32x4*>(&xb[row * XROW + (((8 * gl + 4 + c4) ^ r16) << 4)]);
-        f32x4 a = mfma(ones, s0, zero);
-        a = mfma(ones, s1, a);
-        if (c4 == 0) sx[(2 * (p0 + p) + gl) * MT + row] = a[0];
-      }
-      const u32x4 A0 = unpack_w(wr[p][2 * gl], nib), A1 = unpack_w(wr[p][2 * gl + 1], nib);
-      float sc[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sc[r] = gl ? bf_hi(sr[p][r]) : bf_lo(sr[p][r]);
+      for (int u = 0; u < 4; ++u) X[j][u] = x_chunk(b, 16 * u + r16, 4 * j + c4);
+    {  // D[n][m] += X_g[16u + m] for n in 4u..4u+3: lane (r16, c4) gets X_g[16 c4 + r16]
+      f32x4 xg = zero;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        f32x4 a = mfma(A0, X[u][0], zero);
-        a = mfma(A1, X[u][1], a);
+        xg = mfma(sel1[u], X[0][u], xg);
+        xg = mfma(sel1[u], X[1][u], xg);
+      }
+      xgv[q] = xg[0];
+    }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) T[u][r] = fmaf(sc[r], a[r], T[u][r]);
+    for (int f = 0; f < 4; ++f) {
+      const u32x4 A0 = unpack_w(wr[s][f][2 * gl], nib), A1 = unpack_w(wr[s][f][2 * gl + 1], nib);
+      const float sc = gl ? bf_hi(sr[s][f]) : bf_lo(sr[s][f]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        f32x4 a = mfma(X[0][u], A0, zero);
+        a = mfma(X[1][u], A1, a);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) T[f][u][i] = fmaf(sc, a[i], T[f][u][i]);
       }
     }
-    if (p + 1 < S) {  // x of stage p+1 into the other buffer (last read in stage p-1)
-#pragma unroll
-      for (int i = 0; i < SJ; ++i)
-        *reinterpret_cast<u32x4*>(&xl[ks][b ^ 1][sdst + 16 * i * XROW]) = R[(p + 1) % XD][i];
+    if (q + 2 < NG) {  // buffer b is free once its reads have returned
+      wait_lgkm0();
+      copy_x(q + 2, b);
     }
-    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
   }
 
-  if (KS > 1) {  // K parts 1.. hand their sums to part 0 through the (now idle) x buffers
-    f32x4* red = reinterpret_cast<f32x4*>(&xl[0][0][0]);
-    if (ks > 0) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) red[(((ks - 1) * 4 + wn) * 4 + u) * 64 + lane] = T[u];
+  for (int q = 0; q < NG; ++q) sx[(2 * w * SPW + q) * 64 + 16 * c4 + r16] = xgv[q];
+  // partial tiles into the wave's own buffers (all its copies have landed and been read)
+#pragma unroll
+  for (int f = 0; f < 4; ++f)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = 4 * f + u;
+      reinterpret_cast<f32x4*>(t < 8 ? xb0[w] : xb1[w])[(t & 7) * 64 + lane] = T[f][u];
     }
-    lds_barrier();
-    if (ks > 0) return;
-    for (int k2 = 1; k2 < KS; ++k2)
-#pragma unroll
-      for (int u = 0; u < 4; ++u) T[u] += red[(((k2 - 1) * 4 + wn) * 4 + u) * 64 + lane];
-  }
+  lds_barrier();
 
-  // sum_g (b_g - 128 s_g) X_g with X_g = hi + mid + lo
+  // X_g split once per work-group: thread -> row m, four groups
+  for (int idx = tid; idx < 64 * 8 * GJ; idx += 64 * NW) {
+    const int m = idx & 63, g0 = 4 * (idx >> 6);
+    uint32_t h2[2], m2[2], l2[2];
 #pragma unroll
-  for (int jb = 0; jb < GJ; ++jb) {
-    const int j = 32 * jb;
-    const bool gin = j + 8 * c4 < G;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int row = u * 16 + r16;
-      u32x4 hi, mid, lo;
-#pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        float v0 = 0.f, v1 = 0.f;
-        if (gin) {
-          v0 = sx[(j + 8 * c4 + e) * MT + row];
-          v1 = sx[(j + 8 * c4 + e + 1) * MT + row];
-        }
-        const uint32_t h = f2bf2(v0, v1);
-        const float q0 = v0 - bf_lo(h), q1 = v1 - bf_hi(h);
-        const uint32_t md = f2bf2(q0, q1);
-        hi[e >> 1] = h;
-        mid[e >> 1] = md;
-        lo[e >> 1] = f2bf2(q0 - bf_lo(md), q1 - bf_hi(md));
-      }
-      f32x4 t = T[u];
-      t = mfma(Ab[jb], hi, t);
-      t = mfma(Ab[jb], mid, t);
-      t = mfma(Ab[jb], lo, t);
-      t = mfma(As[jb], hi, t);
-      t = mfma(As[jb], mid, t);
-      t = mfma(As[jb], lo, t);
-      T[u] = t;
+    for (int e = 0; e < 4; e += 2) {
+      const float v0 = g0 + e < G ? sx[(g0 + e) * 64 + m] : 0.f;
+      const float v1 = g0 + e + 1 < G ? sx[(g0 + e + 1) * 64 + m] : 0.f;
+      const uint32_t h = f2bf2(v0, v1);
+      const float q0 = v0 - bf_lo(h), q1 = v1 - bf_hi(h);
+      const uint32_t md = f2bf2(q0, q1);
+      h2[e >> 1] = h;
+      m2[e >> 1] = md;
+      l2[e >> 1] = f2bf2(q0 - bf_lo(md), q1 - bf_hi(md));
     }
+    *reinterpret_cast<u32x2*>(&xsp[0][m * XR + g0]) = (u32x2){h2[0], h2[1]};
+    *reinterpret_cast<u32x2*>(&xsp[1][m * XR + g0]) = (u32x2){m2[0], m2[1]};
+    *reinterpret_cast<u32x2*>(&xsp[2][m * XR + g0]) = (u32x2){l2[0], l2[1]};
   }
+  lds_barrier();
 
-  const int n = f * 16 + 4 * c4;
-  if (part != nullptr) {  // f32 partial of this K slice (all Npad columns)
+  const int n = (fb + fo) * 16 + r16;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int m = u * 16 + r16;
-      if (m < M)
-        *reinterpret_cast<f32x4*>(part + ((int64_t)blockIdx.y * MT + m) * Npad + n) = T[u];
+  for (int i = 0; i < TPW; ++i) {
+    const int t = w * TPW + i, u = t & 3;
+    f32x4 acc = reinterpret_cast<const f32x4*>(t < 8 ? xb0[0] : xb1[0])[(t & 7) * 64 + lane];
+#pragma unroll
+    for (int v = 1; v < NW; ++v)
+      acc += reinterpret_cast<const f32x4*>(t < 8 ? xb0[v] : xb1[v])[(t & 7) * 64 + lane];
+    // sum_g (b_g - 128 s_g) X_g, X_g of rows 16u + r16 as the A operand
+#pragma unroll
+    for (int jb = 0; jb < GJ; ++jb) {
+      const int o = (16 * u + r16) * XR + 32 * jb + 8 * c4;
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(&xsp[0][o]);
+      const u32x4 mid = *reinterpret_cast<const u32x4*>(&xsp[1][o]);
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(&xsp[2][o]);
+      acc = mfma(hi, Ab[jb], acc);
+      acc = mfma(mid, Ab[jb], acc);
+      acc = mfma(lo, Ab[jb], acc);
+      acc = mfma(hi, As[jb], acc);
+      acc = mfma(mid, As[jb], acc);
+      acc = mfma(lo, As[jb], acc);
     }
-  } else if (n < N) {
+    const int m0 = 16 * u + 4 * c4;
+    if (part != nullptr) {
+      float* pr = part + ((int64_t)blockIdx.y * 64 + m0) * Npad + n;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int m = u * 16 + r16;
-      if (m < M)
-        *reinterpret_cast<u32x2*>(y + (int64_t)m * ys + n) =
-            (u32x2){f2bf2(T[u][0], T[u][1]), f2bf2(T[u][2], T[u][3])};
+      for (int e = 0; e < 4; ++e)
+        if (m0 + e < M) pr[(int64_t)e * Npad] = acc[e];
+    } else if (n < N) {
+      uint16_t* yr = y + (int64_t)m0 * ys + n;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (m0 + e < M) yr[(int64_t)e * ys] = f2bf(acc[e]);
     }
   }
 }
@@ -531,14 +577,14 @@ hipError_t launch_qlinear_pack(const QLinearPackArgs& a) {
 
 int qlinear_decode_slices(int K, int Npad) {
   // one work-group per 64 columns; layers with fewer than 128 such groups
-  // (out_proj: 2048 columns), and every K above 2048, split K into 512-wide
-  // slices (K <= 4096: at most 8); very wide layers take the tiled kernel
+  // (out_proj: 2048 columns), and every K above 2048, split K into slices of
+  // 1024 (K a multiple of 1024) or 512; very wide layers take the tiled kernel
   if (K <= 512 || (K <= 2048 && Npad / 64 >= 128) || Npad >= kWideDecodeN) return 1;
-  return K / 512;
+  return K % 1024 == 0 ? K / 1024 : K / 512;
 }
 
 // Tile choice: up to 64 rows (batched decode) qlinear_decode_kernel, whole K
-// (K <= 2048) or K slices of 512 (narrow layers, and every K above 2048 --
+// (K = 512, 1024, 2048) or K slices (narrow layers, and every K above 2048 --
 // those always get a workspace); otherwise 64 x 128 tiles (prefill). Of the
 // tilings swept at 16384 x 2048 -> 12352 (four waves each, 16-wide fragments
 // per wave m x n: 4x4, 2x4, 4x2, 2x2, 2x4 in one row of waves, 1x4, 2x2 in
@@ -548,8 +594,14 @@ int qlinear_decode_slices(int K, int Npad) {
 // registers) pushed it to one wave per SIMD and 2.06 ms; an XCD-aware tile
 // order (each XCD's L2 holding its own weight columns) changed nothing.
 //
+// Decode kernel shapes (64 x 12352 x 2048 and 64 x 2048 x 4096, 30 distinct
+// layers): eight waves of two stages for K = 2048 (four waves of four stages,
+// one wave per SIMD, were 20% slower), and for the narrow layer four slices
+// of 1024 on eight waves (eight slices of 512 on four waves: 8% slower, and
+// twice the partials).
+//
 // Very wide layers at decode sizes (lm_head, 248,320 columns) re-read all of
-// x per 64 columns in qlinear_decode_kernel, 4x the weight bytes through L2.
+// x per 64 columns in the decode kernel, 4x the weight bytes through L2.
 // There a 64 x 128 tile with every wave holding all 64 rows and two column
 // fragments (one row of four waves) took 140 us at M = 64, K = 2048, against
 // 196 us for the decode kernel, 159 us for the 2 x 2 wave grid and 157 us for
@@ -559,29 +611,25 @@ hipError_t launch_qlinear(const QLinearArgs& a) {
   if (a.M <= 64 && a.Npad >= kWideDecodeN) return launch_cfg<4, 2, 1, 4>(a);
   if (a.M <= 64) {
     const int ns = a.part ? qlinear_decode_slices(a.K, a.Npad) : 1;
-    if (ns > 1 || a.K == 512 || a.K == 1024 || a.K == 2048) {
+    const int ksl = a.K / ns;  // K of a slice
+    if (ksl == 512 || ksl == 1024 || ksl == 2048) {
       const u32x4* wp = reinterpret_cast<const u32x4*>(a.wp);
-      if (ns > 1) {  // 512-wide slices: two K parts of two stages
-        hipLaunchKernelGGL((qlinear_decode_kernel<2, 2>), dim3(a.Npad / 64, ns), dim3(512), 0,
-                           a.stream, a.x, a.xs, a.M, a.K, wp, a.sp, a.bias, a.nsc, a.N, a.y, a.ys,
-                           a.part, a.Npad);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        if (a.defer) {  // the consumer adds the slices
-          *a.defer = QPartial{a.part, ns, a.Npad};
-          return hipSuccess;
-        }
-        const int64_t n4 = (int64_t)a.M * (a.Npad / 4);
-        hipLaunchKernelGGL(qlinear_sum_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0,
-                           a.stream, a.part, ns, a.M, a.N, a.Npad, a.y, a.ys);
-        return hipGetLastError();
+      auto kern = ksl == 2048   ? qlinear_decode_kernel<8, 2>
+                  : ksl == 1024 ? qlinear_decode_kernel<8, 1>
+                                : qlinear_decode_kernel<4, 1>;
+      const int threads = ksl == 512 ? 256 : 512;
+      hipLaunchKernelGGL(kern, dim3(a.Npad / 64, ns), dim3(threads), 0, a.stream, a.x, a.xs, a.M,
+                         a.K, wp, a.sp, a.bias, a.nsc, a.N, a.y, a.ys, ns > 1 ? a.part : nullptr,
+                         a.Npad);
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess || ns == 1) return e;
+      if (a.defer) {  // the consumer adds the slices
+        *a.defer = QPartial{a.part, ns, a.Npad};
+        return hipSuccess;
       }
-      // two K parts of S = K/256 stages each
-      auto kern = a.K == 2048   ? qlinear_decode_kernel<2, 8>
-                  : a.K == 1024 ? qlinear_decode_kernel<2, 4>
-                                : qlinear_decode_kernel<2, 2>;
-      hipLaunchKernelGGL(kern, dim3(a.Npad / 64), dim3(512), 0, a.stream, a.x, a.xs, a.M, a.K, wp,
-                         a.sp, a.bias, a.nsc, a.N, a.y, a.ys, nullptr, a.Npad);
+      const int64_t n4 = (int64_t)a.M * (a.Npad / 4);
+      hipLaunchKernelGGL(qlinear_sum_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0,
+                         a.stream, a.part, ns, a.M, a.N, a.Npad, a.y, a.ys);
       return hipGetLastError();
     }
   }
