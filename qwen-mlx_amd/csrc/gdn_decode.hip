@@ -354,14 +354,23 @@ __global__ __launch_bounds__(256 * R) void decode_kernel(
 
 // ------------------------------------------------------------ launchers --
 
+// Occupancy of the fused decode at R = 2: one 512-thread group per CU. The
+// launch reserves 80 KB of LDS per group (unused; the CU has 160 KB), so a
+// second group cannot start beside the first. With 256 groups resident
+// instead of 512, half as many slots stream at once; measured on 30 layers x
+// B = 64 scattered slots: 50.2-50.9 us per launch against 50.8-51.8 us with
+// two groups per CU (the same results bit for bit).
+constexpr size_t kDecodeOccupancyLds = 80 * 1024;
+
 template <int R>
 static hipError_t launch_decode_r(const DecodeArgs& a) {
+  const size_t lds = R == 2 ? kDecodeOccupancyLds : 0;
   if (a.out)
-    hipLaunchKernelGGL((decode_kernel<R, true>), dim3(a.Hk, a.B), dim3(256 * R), 0, a.stream,
+    hipLaunchKernelGGL((decode_kernel<R, true>), dim3(a.Hk, a.B), dim3(256 * R), lds, a.stream,
                        a.state, a.conv, a.slot_ids, a.num_slots, a.Hk, a.mixed, a.xstride, a.ab, a.ab_stride,
                        a.A_log, a.dt_bias, a.conv_w, a.y, a.norm_w, a.norm_eps, a.out, a.status);
   else
-    hipLaunchKernelGGL((decode_kernel<R, false>), dim3(a.Hk, a.B), dim3(256 * R), 0, a.stream,
+    hipLaunchKernelGGL((decode_kernel<R, false>), dim3(a.Hk, a.B), dim3(256 * R), lds, a.stream,
                        a.state, a.conv, a.slot_ids, a.num_slots, a.Hk, a.mixed, a.xstride, a.ab, a.ab_stride,
                        a.A_log, a.dt_bias, a.conv_w, a.y, a.norm_w, a.norm_eps, a.out, a.status);
   return hipGetLastError();
