@@ -12,6 +12,7 @@
 //   qn [T,Hk,Dk] bf16 | kn [T,Hk,Dk] bf16 | vc [T,Hv,Dv] bf16 | beta [T,Hv] bf16 | lg [T,Hv] f32
 
 #include <mutex>
+#include <type_traits>
 
 #include "gdn_common.h"
 
@@ -64,6 +65,7 @@ __device__ __forceinline__ int seq_of(const int32_t* __restrict__ cu, int nseq, 
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // The sigmoid of the conv activations on the hardware exp2 and reciprocal
 // (v_exp_f32, v_rcp_f32; ~2 ulp instead of the ~1 ulp of expf and an IEEE
@@ -303,9 +305,19 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 namespace {
 constexpr int kC = 64;
-// Row strides. LDS serves the 16-byte operand reads below (lane (q, c): row
-// c, 16-byte column group q) without bank conflicts when the stride is 8 mod
-// 16 dwords (measured on gfx950 with SQ_LDS_BANK_CONFLICT).
+// LDS on gfx950 (measured with SQ_LDS_BANK_CONFLICT on single access
+// patterns): reads are served 256 bytes per cycle from 64 banks of 4 bytes,
+// a pass being 64 lanes of a 4-byte read, 32 lanes of an 8-byte read, and
+// lanes 0-7 with 16-23 (or 8-15 with 24-31) of a 16-byte read; writes are
+// served 128 bytes per cycle from 32 banks, a pass being 32 lanes of a 4-byte
+// write, 16 of an 8-byte and 8 of a 16-byte write. Lanes of one pass that hit
+// one bank at different addresses serialize.
+//
+// Row strides: the 16-byte operand reads below (lane (q, c): row c, 16-byte
+// column group q) are conflict-free when the stride is 8 mod 16 dwords. The
+// writes of L and P blocks (lane c: row c) then meet rows c and c + 4 (mod 8)
+// in one bank group; their 16-byte column groups are XORed with bit 2 of the
+// row (gsw), which the reads undo.
 constexpr int kLdQ = kDk + 16;     // Q rows in pair order (288 B = 72 dwords)
 constexpr int kLdP = kC + 16;      // P rows in pair order (160 B = 40 dwords)
 constexpr int kLdN = 2 * kC + 16;  // -L rows: 16 groups of (4 hi, 4 lo) (288 B)
@@ -315,6 +327,14 @@ constexpr int kLdL = 20;           // rows of the diagonal blocks of L, f32 (80 
 constexpr int kLdLB = 16 * kLdL + 8;
 constexpr int kKBlk = 16 * kDk + 64;   // K: 16-row blocks, 64 elements of padding between
 
+// 16-byte column group g of row `row` of NL or P is stored at group g ^ gsw(row).
+__device__ __forceinline__ int gsw(int row) { return (row >> 2) & 1; }
+// Input unit e (0..1023) of q: chunk row qrow(e), 16-byte unit qunit(e) of
+// the row (lanes 0-7 units 0-7 of an even row, lanes 8-15 the same of the
+// next row, lanes 16-31 units 8-15 of the two rows).
+__device__ __forceinline__ int qrow(int e) { return 2 * (e >> 5) + ((e >> 3) & 1); }
+__device__ __forceinline__ int qunit(int e) { return (e & 7) + 8 * ((e >> 4) & 1); }
+
 struct __attribute__((aligned(16))) ChunkSmem {
   uint16_t K[4 * kKBlk];       // k, natural dk order, segments swizzled (kseg)
   uint16_t Q[kC][kLdQ];        // q, dk in pair order: 32b + 16h + 4m + u at 32b + 8m + 4h + u
@@ -323,7 +343,11 @@ struct __attribute__((aligned(16))) ChunkSmem {
   uint16_t D[4 * kLdDB];       // D_I, rows of kLdD, hi/lo interleaved per 4 columns
   float Ld[4 * kLdLB];         // diagonal blocks of L (f32): row i, column 4m + p at 4p + m
   float beta[kC], G[kC], eG[kC], dec[kC];  // G: cumulative log2 decay
-  uint16_t Y[kC][kDv + 8];     // the chunk's outputs y (bf16), written out as whole rows
+  uint16_t V[kC][kLdQ];        // v rows (row stride 288 B: the transposing reads of 8
+                               // consecutive rows x 32 bytes hit distinct banks)
+  uint16_t Y[kC][kDv + 4];     // the chunk's outputs y (bf16), written out as whole rows; the
+                               // 66-dword stride puts the 16 rows of an 8-byte write pass and
+                               // the 2 rows of an 8-byte read pass in distinct banks
   float ysq[kC][8];            // gated epilogue: per token, each wave's sum of y^2
 };
 
@@ -381,6 +405,14 @@ __device__ __forceinline__ s16x4 ktr(const uint16_t* K, int kt, int blk, int a) 
   return __builtin_bit_cast(s16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(p));
 }
 
+// v operand of the solve, a transposing read like ktr: lane (q, c) passes
+// row 16I + 4q + (c >> 2) and column dv0 + 4(c & 3) and receives
+// V[16I + 4q + u][dv0 + c], u = 0..3.
+__device__ __forceinline__ s16x4 vtr(const ChunkSmem& sm, int row, int col) {
+  lds_bf16x4* p = (lds_bf16x4*)&sm.V[row][col];
+  return __builtin_bit_cast(s16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(p));
+}
+
 // f32 -> bf16 hi + lo (hi + lo carries ~16 mantissa bits)
 __device__ __forceinline__ void split4(const f32x4& x, s16x4& hi, s16x4& lo) {
   const uint32_t h0 = f2bf2(x[0], x[1]), h1 = f2bf2(x[2], x[3]);
@@ -391,22 +423,6 @@ __device__ __forceinline__ void split4(const f32x4& x, s16x4& hi, s16x4& lo) {
 }
 __device__ __forceinline__ s16x4 hi4(const f32x4& x) {
   return __builtin_bit_cast(s16x4, (uint2){f2bf2(x[0], x[1]), f2bf2(x[2], x[3])});
-}
-
-// Tiles of the chunk's matrices, as accumulators holding row 4q + r, column c:
-// kk(I, J) = k_{16J+4q+r} . k_{16I+c} = (K K^T)[16I+c][16J+4q+r] and
-// kq(I, J) = (Q K^T)[16I+c][16J+4q+r]: lane c owns row 16I+c of L or P.
-__device__ __forceinline__ f32x4 tile_kk(const ChunkSmem& sm, int kf, int I, int J) {
-  f32x4 t = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int b = 0; b < 4; ++b) t = mfma32(kfrag(sm.K, kf, J, b), kfrag(sm.K, kf, I, b), t);
-  return t;
-}
-__device__ __forceinline__ f32x4 tile_kq(const ChunkSmem& sm, int kf, int I, int J, int q, int c) {
-  f32x4 t = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int b = 0; b < 4; ++b) t = mfma32(kfrag(sm.K, kf, J, b), lds8(&sm.Q[16 * I + c][32 * b + 8 * q]), t);
-  return t;
 }
 
 // L block (I, J), J <= I: an off-diagonal block as -L hi/lo into NL (row
@@ -429,7 +445,7 @@ __device__ __forceinline__ void put_l(ChunkSmem& sm, const f32x4& t, int I, int 
   } else {
     s16x4 h, l;
     split4(-lv, h, l);
-    *reinterpret_cast<bf16x8*>(&sm.NL[i][8 * (4 * J + q)]) = cat(h, l);
+    *reinterpret_cast<bf16x8*>(&sm.NL[i][32 * J + 8 * (q ^ gsw(c))]) = cat(h, l);
   }
 }
 // P block (I, J), J <= I: row 16I+c, columns 16J+4q..+3 at their pair-order place.
@@ -443,17 +459,72 @@ __device__ __forceinline__ void put_p(ChunkSmem& sm, const f32x4& t, int I, int 
     const float v = t[r] * __builtin_amdgcn_exp2f(fminf(Gi - Gj[r], 0.f));
     pv[r] = (J < I || 4 * q + r <= c) ? v : 0.f;
   }
-  *static_cast<s16x4*>(__builtin_assume_aligned(&sm.P[i][32 * (J >> 1) + 8 * q + 4 * (J & 1)], 8)) = hi4(pv);
+  *static_cast<s16x4*>(__builtin_assume_aligned(&sm.P[i][32 * (J >> 1) + 8 * (q ^ gsw(c)) + 4 * (J & 1)], 8)) =
+      hi4(pv);
 }
 
-// The 16 blocks besides the diagonal blocks of L: 6 off-diagonal blocks of L,
-// then the 10 blocks of P (I, J), J <= I.
-__device__ __forceinline__ void other_block(int t, int& I, int& J, bool& isl) {
-  constexpr int kI[16] = {1, 2, 2, 3, 3, 3, 0, 1, 1, 2, 2, 2, 3, 3, 3, 3};
-  constexpr int kJ[16] = {0, 0, 1, 0, 1, 2, 0, 0, 1, 0, 1, 2, 0, 1, 2, 3};
-  I = kI[t];
-  J = kJ[t];
-  isl = t < 6;
+// The operand fragments of one 16-row block for the four 32-wide dk blocks:
+// K rows (kfrags) or Q rows (qfrags) 16X + c, 16-byte column group q.
+struct Frag {
+  bf16x8 f[4];
+};
+__device__ __forceinline__ Frag kfrags(const ChunkSmem& sm, int kf, int X) {
+  Frag r;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) r.f[b] = kfrag(sm.K, kf, X, b);
+  return r;
+}
+__device__ __forceinline__ Frag qfrags(const ChunkSmem& sm, int X, int q, int c) {
+  Frag r;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) r.f[b] = lds8(&sm.Q[16 * X + c][32 * b + 8 * q]);
+  return r;
+}
+// Tiles of the chunk's matrices, as accumulators holding row 4q + r, column c:
+// tile(K_J, K_I) = (K K^T)[16I+c][16J+4q+r] and tile(K_J, Q_I) =
+// (Q K^T)[16I+c][16J+4q+r]: lane c owns row 16I+c of L or P.
+__device__ __forceinline__ f32x4 tile(const Frag& colJ, const Frag& rowI) {
+  f32x4 t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int b = 0; b < 4; ++b) t = mfma32(colJ.f[b], rowI.f[b], t);
+  return t;
+}
+
+// The 16 blocks besides the diagonal blocks of L (6 off-diagonal blocks of L,
+// the 10 blocks of P (I, J), J <= I), four per wave for waves 4-7, grouped so
+// that a wave's four tiles share operand blocks (4-5 blocks of 16 rows).
+// Each wave's code is straight-line: all its LDS operand reads are in flight
+// together instead of one tile's reads at a time.
+__device__ __forceinline__ void other_blocks(ChunkSmem& sm, int w, int kf, int q, int c) {
+  if (w == 4) {
+    const Frag k0 = kfrags(sm, kf, 0), k1 = kfrags(sm, kf, 1), k2 = kfrags(sm, kf, 2),
+               k3 = kfrags(sm, kf, 3), q3 = qfrags(sm, 3, q, c);
+    put_l(sm, tile(k0, k3), 3, 0, q, c);
+    put_l(sm, tile(k1, k3), 3, 1, q, c);
+    put_l(sm, tile(k2, k3), 3, 2, q, c);
+    put_p(sm, tile(k3, q3), 3, 3, q, c);
+  } else if (w == 5) {
+    const Frag k0 = kfrags(sm, kf, 0), k1 = kfrags(sm, kf, 1), k2 = kfrags(sm, kf, 2),
+               q3 = qfrags(sm, 3, q, c);
+    put_p(sm, tile(k0, q3), 3, 0, q, c);
+    put_p(sm, tile(k1, q3), 3, 1, q, c);
+    put_p(sm, tile(k2, q3), 3, 2, q, c);
+    put_l(sm, tile(k0, k2), 2, 0, q, c);
+  } else if (w == 6) {
+    const Frag k0 = kfrags(sm, kf, 0), k1 = kfrags(sm, kf, 1), k2 = kfrags(sm, kf, 2),
+               q2 = qfrags(sm, 2, q, c);
+    put_p(sm, tile(k0, q2), 2, 0, q, c);
+    put_p(sm, tile(k1, q2), 2, 1, q, c);
+    put_p(sm, tile(k2, q2), 2, 2, q, c);
+    put_l(sm, tile(k1, k2), 2, 1, q, c);
+  } else if (w == 7) {
+    const Frag k0 = kfrags(sm, kf, 0), k1 = kfrags(sm, kf, 1), q0 = qfrags(sm, 0, q, c),
+               q1 = qfrags(sm, 1, q, c);
+    put_p(sm, tile(k0, q0), 0, 0, q, c);
+    put_p(sm, tile(k0, q1), 1, 0, q, c);
+    put_p(sm, tile(k1, q1), 1, 1, q, c);
+    put_l(sm, tile(k0, k1), 1, 0, q, c);
+  }
 }
 }  // namespace
 
@@ -517,50 +588,70 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
   // write-out layout: thread (tokens tid/16 and 32 + tid/16, 8 output rows
   // from 8 * (tid % 16)); 16 lanes cover one token's 256-byte row
   const int oi = tid >> 4, od = 8 * (tid & 15);
+  u32x4 nw = {0u, 0u, 0u, 0u};  // GATED: the norm weights of rows od..od+7
+  if constexpr (GATED) nw = *reinterpret_cast<const u32x4*>(norm_w + od);
   // Blocks of P above the diagonal are never written: zero them once.
   for (int e = tid; e < kC * kLdP / 4; e += NT) reinterpret_cast<uint2*>(&sm.P[0][0])[e] = make_uint2(0u, 0u);
 
-  // chunk inputs, prefetched one chunk ahead: k and q units, this lane's v
-  // values (tokens 16I + 4q + r, state row dv0 + c; out-of-chunk reads give 0)
-  uint4 kv[UK], qv[UK];
-  uint16_t vpre[16];
-  float pb = 0.f, pl = 0.f;
-  const int voff = (4 * q0 * Hv * kDv + c0l) * 2;  // byte offset of this lane's first v value
-  auto load_inputs = [&](int c) {
-    const int n = min(kC, en - c);
+  // chunk inputs, prefetched one chunk ahead: 16-byte units of the k, q and
+  // v rows (thread e: row e/16, elements 8(e%16)..+7) and, for lane l, token
+  // l's beta (raw bf16) and log decay; 8 loads per wave and chunk. A CU
+  // passes these 48 KiB per chunk through its texture units at ~64 B per
+  // cycle, and a wave that issues into a full queue stalls, so the four
+  // groups go out at four points of the chunk (k in (b), q in (c), v in (d),
+  // the gates in (e)). Every read goes through a buffer resource whose size
+  // ends at the chunk's last token (0 past the end of the sequence), so rows
+  // beyond it read 0 without a branch: a load under a branch leaves a merge of
+  // its result with the zero of the other path, and the copy that merge needs
+  // makes the wave wait for the load right after issuing it instead of one
+  // chunk later. Sizes go through readfirstlane: a resource held in VGPRs
+  // would need a waterfall loop around each load.
+  u32x4 kv[UK], qv[UK], vv[UK];
+  uint16_t pb = 0;
+  float pl = 0.f;
+  auto rows_of = [&](int c) { return __builtin_amdgcn_readfirstlane(max(0, min(kC, en - c))); };
+  // k (KQ = 0) or q (KQ = 1) rows of the chunk at token c
+  auto load_kq = [&](int c, auto KQ) {
+    const int n = rows_of(c);
+    const int bytes = __builtin_amdgcn_readfirstlane(n > 0 ? ((n - 1) * Hk + 1) * kDk * 2 : 0);
+    const uint16_t* src = (decltype(KQ)::value ? qn : kn) + ((size_t)c * Hk + hk) * kDk;
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, bytes, 0x00020000);
 #pragma unroll
     for (int u = 0; u < UK; ++u) {
-      // k unit: dk 8m..8m+7; q unit: pair-order group m = dk 32(m/4) + 4(m%4)
-      // .. +3 and the same 16 further on
-      const int e = tid + NT * u, i = e >> 4, m = e & 15;
-      kv[u] = make_uint4(0u, 0u, 0u, 0u);
-      qv[u] = kv[u];
-      if (i < n) {
-        const size_t row = ((size_t)(c + i) * Hk + hk) * kDk;
-        kv[u] = *reinterpret_cast<const uint4*>(kn + row + 8 * m);
-        const int dq = 32 * (m >> 2) + 4 * (m & 3);
-        const uint2 qa = *reinterpret_cast<const uint2*>(qn + row + dq);
-        const uint2 qb = *reinterpret_cast<const uint2*>(qn + row + dq + 16);
-        qv[u] = make_uint4(qa.x, qa.y, qb.x, qb.y);
-      }
-    }
-    // v through a buffer resource whose size ends at the chunk's last token
-    const int base = hv * kDv + dv0;
-    const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(vc + (size_t)c * Hv * kDv + base), (short)0, (n * Hv * kDv - base) * 2, 0x00020000);
-#pragma unroll
-    for (int I = 0; I < 4; ++I)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        vpre[4 * I + r] = __builtin_amdgcn_raw_buffer_load_b16(vr, voff + (16 * I + r) * Hv * kDv * 2, 0, 0);
-    pb = 0.f;
-    pl = 0.f;
-    if (w == 0 && lane0 < n) {
-      pb = bf2f(betav[(size_t)(c + lane0) * Hv + hv]);
-      pl = lgv[(size_t)(c + lane0) * Hv + hv];
+      const int e = tid + NT * u;
+      const int i = decltype(KQ)::value ? qrow(e) : e >> 4, m = decltype(KQ)::value ? qunit(e) : e & 15;
+      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, i * Hk * kDk * 2 + 16 * m, 0, 0);
+      if constexpr (decltype(KQ)::value) qv[u] = x; else kv[u] = x;
     }
   };
-  load_inputs(st);
+  auto load_v = [&](int c) {
+    const int n = rows_of(c);
+    const int bytes = __builtin_amdgcn_readfirstlane(n > 0 ? ((n - 1) * Hv + 1) * kDv * 2 : 0);
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(vc + ((size_t)c * Hv + hv) * kDv), (short)0, bytes, 0x00020000);
+#pragma unroll
+    for (int u = 0; u < UK; ++u) {
+      const int e = tid + NT * u, i = e >> 4, m = e & 15;
+      vv[u] = __builtin_amdgcn_raw_buffer_load_b128(r, i * Hv * kDv * 2 + 16 * m, 0, 0);
+    }
+  };
+  // every wave reads the 64 gate values (wave 0 uses them)
+  auto load_gates = [&](int c) {
+    const int n = rows_of(c);
+    const int g = __builtin_amdgcn_readfirstlane(n > 0 ? (n - 1) * Hv + 1 : 0);
+    const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(betav + (size_t)c * Hv + hv), (short)0, 2 * g, 0x00020000);
+    const __amdgpu_buffer_rsrc_t lr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(lgv + (size_t)c * Hv + hv), (short)0, 4 * g, 0x00020000);
+    pb = __builtin_amdgcn_raw_buffer_load_b16(br, lane0 * Hv * 2, 0, 0);
+    pl = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(lr, lane0 * Hv * 4, 0, 0));
+  };
+  using KLoad = std::integral_constant<int, 0>;
+  using QLoad = std::integral_constant<int, 1>;
+  load_kq(st, KLoad{});
+  load_kq(st, QLoad{});
+  load_v(st);
+  load_gates(st);
   for (int c0 = st; c0 < en; c0 += kC) {
     const int n = min(kC, en - c0);
     // Lane-derived values are recomputed in every chunk (a few VALU ops)
@@ -569,19 +660,26 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
     asm volatile("" : "+v"(lane));
     const int q = lane >> 4, c = lane & 15;
     const int kf = kseg(c, q), kt = kseg(4 * q + (c >> 2), c & 3);  // K operand lane constants
-    // (a) stage k (natural order, swizzled segments) and q (pair order); wave 0
-    // forms the decay prefix sums in log2 units
-#pragma unroll
-    for (int u = 0; u < UK; ++u)
-      asm volatile("" : "+v"(kv[u].x), "+v"(kv[u].y), "+v"(kv[u].z), "+v"(kv[u].w),
-                   "+v"(qv[u].x), "+v"(qv[u].y), "+v"(qv[u].z), "+v"(qv[u].w));
+    const int qs = 8 * (q ^ gsw(c));  // column of this lane's 16-byte group q in rows of NL and P
+    // (a) stage k (natural order, swizzled segments), q (pair order) and v;
+    // wave 0 forms the decay prefix sums in log2 units
 #pragma unroll
     for (int u = 0; u < UK; ++u) {
       // k: natural segments 2m, 2m + 1 stay adjacent and in order under the
-      // (even) swizzle, one 16-byte write; q: pair-order group m, one 16-byte write
+      // (even) swizzle, one 16-byte write
       const int e = tid + NT * u, i = e >> 4, m = e & 15;
-      *static_cast<uint4*>(__builtin_assume_aligned(&sm.K[kseg(i, 2 * m)], 16)) = kv[u];
-      *static_cast<uint4*>(__builtin_assume_aligned(&sm.Q[i][8 * m], 16)) = qv[u];
+      *static_cast<u32x4*>(__builtin_assume_aligned(&sm.K[kseg(i, 2 * m)], 16)) = kv[u];
+      *static_cast<u32x4*>(__builtin_assume_aligned(&sm.V[i][8 * m], 16)) = vv[u];
+      // q (unit qunit(e) of row qrow(e)): dk 8m..8m+3 and 8m+4..8m+7 go to
+      // pair-order places p and p + 8, p = 32(m/4) + 16(m%2) + 4((m/2)%2).
+      // An 8-byte write pass (16 lanes) covers units 0-7 or 8-15 of an even
+      // and the next odd row; the odd row writes its second half first, which
+      // puts the 16 writes in 32 distinct banks.
+      const int qi = qrow(e), qm = qunit(e);
+      const int p = 32 * (qm >> 2) + 16 * (qm & 1) + 4 * ((qm >> 1) & 1), odd = qi & 1;
+      const u32x2 qlo = {qv[u][0], qv[u][1]}, qhi = {qv[u][2], qv[u][3]};
+      *static_cast<u32x2*>(__builtin_assume_aligned(&sm.Q[qi][p + 8 * odd], 8)) = odd ? qhi : qlo;
+      *static_cast<u32x2*>(__builtin_assume_aligned(&sm.Q[qi][p + 8 - 8 * odd], 8)) = odd ? qlo : qhi;
     }
     if (w == 0) {
       // inclusive prefix sum over the 64 lanes on DPP: shifts within each
@@ -595,28 +693,25 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
       gsum += dpp_f<0x142, 0xA>(gsum);  // row_bcast:15
       gsum += dpp_f<0x143, 0xC>(gsum);  // row_bcast:31
       const float gC = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gsum), 63));
-      sm.beta[lane0] = pb;
+      sm.beta[lane0] = bf2f(pb);
       sm.G[lane0] = gsum;
       sm.eG[lane0] = __builtin_amdgcn_exp2f(gsum);
       sm.dec[lane0] = __builtin_amdgcn_exp2f(gC - gsum);
     }
-    uint16_t vcur[16];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) vcur[e] = vpre[e];
     __syncthreads();
-    if (c0 + kC < en) load_inputs(c0 + kC);
+    load_kq(c0 + kC, KLoad{});  // past the sequence end: no memory access, reads 0
 
     // (b) the chunk's matrices. Diagonal block I of L goes to wave I, which
     // forms it and inverts it, D_I = (I + L_II)^-1, by forward substitution
     // with four lanes per column: lane (j = l/4, p = l%4) sums the terms
     // k = p (mod 4) of each row and two DPP adds close the sum over its quad,
-    // so a row costs a handful of dependent VALU ops. Of the other 16 blocks,
-    // waves 4-7 take three each and waves 0-3 one each, which balances the two
-    // halves (measured).
+    // so a row costs a handful of dependent VALU ops. Waves 4-7 form the
+    // other 16 blocks, four each.
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       if (w != I) continue;
-      put_l(sm, tile_kk(sm, kf, I, I), I, I, q, c);
+      const Frag kI = kfrags(sm, kf, I);
+      put_l(sm, tile(kI, kI), I, I, q, c);
       // this wave's own Ld writes, read back by other lanes of the wave
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
       __builtin_amdgcn_wave_barrier();
@@ -645,18 +740,8 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
         Dp[(4 * m + pp) * kLdD + 4] = f2bf(tv[m] - bf2f(h));
       }
     }
-#pragma unroll
-    for (int t = 0; t < 16; ++t) {
-      constexpr int kOwn[16] = {4, 5, 6, 7, 4, 5, 0, 1, 2, 3, 6, 7, 4, 5, 6, 7};
-      if (w != kOwn[t]) continue;
-      int I, J;
-      bool isl;
-      other_block(t, I, J, isl);
-      if (isl)
-        put_l(sm, tile_kk(sm, kf, I, J), I, J, q, c);
-      else
-        put_p(sm, tile_kq(sm, kf, I, J, q, c), I, J, q, c);
-    }
+    other_blocks(sm, w, kf, q, c);
+    load_kq(c0 + kC, QLoad{});
     // (c) Y_I = K_I S^T (S hi and lo) and Zt_I = S Q_I^T (S hi) for this wave's
     // 16 state rows; the pair (acc[2b], acc[2b+1]) is the operand of dk block b
     f32x4 yk[4], zt[4];
@@ -682,6 +767,7 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
     }
     __syncthreads();
 
+    load_v(c0 + kC);
     // (d) R_I = beta (V - exp(G) Y_I), then V'_I = D_I (R_I - sum_{j<I} L_Ij V'_j)
     f32x4 vf[4];        // V' (f32), tokens 16I + 4q + r, state row dv0 + c
     bf16x8 vpd[4];      // cat(V'h, V'h)
@@ -692,12 +778,15 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
       const f32x4 bt = *reinterpret_cast<const f32x4*>(&sm.beta[16 * I + 4 * q]);
       const f32x4 eg = *reinterpret_cast<const f32x4*>(&sm.eG[16 * I + 4 * q]);
       f32x4 x;
+      // v of tokens 16I + 4q + r, state row dv0 + c (a transposing read: lane
+      // 4u + s of each 16-lane group reads row 4q + u, columns 4s..4s+3)
+      const s16x4 vt = vtr(sm, 16 * I + 4 * q + (c >> 2), dv0 + 4 * (c & 3));
 #pragma unroll
-      for (int r = 0; r < 4; ++r) x[r] = bt[r] * (bf2f(vcur[4 * I + r]) - eg[r] * yk[I][r]);
+      for (int r = 0; r < 4; ++r) x[r] = bt[r] * (bf2f((uint16_t)vt[r]) - eg[r] * yk[I][r]);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         if (j >= I) continue;
-        const bf16x8 nl = lds8(&sm.NL[16 * I + c][8 * (4 * j + q)]);  // -L hi | lo
+        const bf16x8 nl = lds8(&sm.NL[16 * I + c][32 * j + qs]);  // -L hi | lo
         x = mfma32(nl, vpd[j], x);   // (NLh + NLl) V'h
         x = mfma32(nl, vplz[j], x);  // NLh V'l
       }
@@ -713,6 +802,19 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
       vpd[I] = cat(vph[I], vph[I]);
       vplz[I] = cat(vl, kZero4);
     }
+    load_gates(c0 + kC);
+    // GATED: z of this thread's two write-out tokens of this chunk, read here
+    // so that it arrives during (e) and (f); a token past the chunk's end
+    // reads the chunk's last row instead (its output is not written), which
+    // keeps the loads unconditional
+    u32x4 zv[2];
+    if constexpr (GATED) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int i = min(oi + 32 * h, n - 1);
+        zv[h] = *reinterpret_cast<const u32x4*>(zrow + (size_t)(c0 + i) * xs + (size_t)hv * kDv + od);
+      }
+    }
     // (e) O^T_I = exp(G) Zt_I + V'^T P^T: rows dv0 + 4q + r, token 16I + c
     // y (bf16) into the LDS rows; with GATED each wave's sum of y^2 per token
 #pragma unroll
@@ -721,7 +823,7 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
         if (2 * p > I) continue;
-        o = mfma32(cat(vph[2 * p], vph[2 * p + 1]), lds8(&sm.P[16 * I + c][32 * p + 8 * q]), o);
+        o = mfma32(cat(vph[2 * p], vph[2 * p + 1]), lds8(&sm.P[16 * I + c][32 * p + qs]), o);
       }
       const uint2 yb = make_uint2(f2bf2(o[0], o[1]), f2bf2(o[2], o[3]));
       *reinterpret_cast<uint2*>(&sm.Y[16 * I + c][dv0 + 4 * q]) = yb;
@@ -764,7 +866,9 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
     for (int h = 0; h < 2; ++h) {
       const int i = oi + 32 * h;
       if (i >= n) continue;
-      const uint4 yv = *reinterpret_cast<const uint4*>(&sm.Y[i][od]);
+      const uint2 ya = *reinterpret_cast<const uint2*>(&sm.Y[i][od]);
+      const uint2 yb = *reinterpret_cast<const uint2*>(&sm.Y[i][od + 4]);
+      const uint4 yv = make_uint4(ya.x, ya.y, yb.x, yb.y);
       const size_t row = ((size_t)(c0 + i) * Hv + hv) * kDv + od;
       if (y != nullptr) *reinterpret_cast<uint4*>(y + row) = yv;
       if constexpr (GATED) {
@@ -772,11 +876,9 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
         const f32x4 p1 = *reinterpret_cast<const f32x4*>(&sm.ysq[i][4]);
         const float tot = ((p0[0] + p0[1]) + (p0[2] + p0[3])) + ((p1[0] + p1[1]) + (p1[2] + p1[3]));
         const float rn = 1.0f / sqrtf(tot / (float)kDv + norm_eps);
-        const uint4 zv = *reinterpret_cast<const uint4*>(zrow + (size_t)(c0 + i) * xs + (size_t)hv * kDv + od);
-        const uint4 nv = *reinterpret_cast<const uint4*>(norm_w + od);  // the rows' norm weights
         const uint32_t yw[4] = {yv.x, yv.y, yv.z, yv.w};
-        const uint32_t zw[4] = {zv.x, zv.y, zv.z, zv.w};
-        const uint32_t ww[4] = {nv.x, nv.y, nv.z, nv.w};
+        const uint32_t zw[4] = {zv[h][0], zv[h][1], zv[h][2], zv[h][3]};
+        const uint32_t ww[4] = {nw[0], nw[1], nw[2], nw[3]};
         uint32_t ow[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
