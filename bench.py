@@ -218,6 +218,20 @@ def prefill_summary(L, n, P, elapsed, gpu_s):
     }
 
 
+def one_prompt_summary(args):
+    """One prompt of prefill_len tokens per layer call: the latency case, where
+    the split path (chunk records for all chunks at once, then 4 groups per
+    value head: 128 work-groups) runs instead of the fused chunk kernel (32)."""
+    L, P = args.layers, args.prefill_len
+    el, gpu_s, flags = prefill_measure(L, 1, P, args.seed, reps=2)
+    if flags:
+        print(f"one-prompt prefill pool status flags 0x{flags:x}", file=sys.stderr)
+        return None
+    s = prefill_summary(L, 1, P, el, gpu_s)
+    return {"workload": s["workload"], "tokens_per_s": s["tokens_per_s"],
+            "ms_per_layer": s["ms_per_layer"], "tflops": s["roofline"]["achieved"]}
+
+
 def prefill_bench(args):
     """The chunked prefill alone; prints one JSON line."""
     L, n, P = args.layers, args.prefill_seqs, args.prefill_len
@@ -226,6 +240,9 @@ def prefill_bench(args):
         print(f"pool status flags 0x{flags:x}", file=sys.stderr)
         return 1
     summ = prefill_summary(L, n, P, elapsed, gpu_s)
+    summ["one_prompt"] = one_prompt_summary(args)
+    if summ["one_prompt"] is None:
+        return 1
     out = {
         "metric": "GDN chunked prefill tokens/s (packed varlen, all layers)",
         "value": summ["tokens_per_s"],
@@ -238,6 +255,7 @@ def prefill_bench(args):
         "config": {"workload": summ["workload"], "layers": L, "sequences": n,
                    "tokens_per_sequence": P},
         "roofline": summ["roofline"],
+        "one_prompt": summ["one_prompt"],
     }
     print(json.dumps(out), flush=True)
     return 0
@@ -877,6 +895,9 @@ def main(argv=None):
             print(f"prefill pool status flags 0x{p_flags:x}", file=sys.stderr)
             return 1
         prefill = prefill_summary(args.layers, args.prefill_seqs, args.prefill_len, p_el, p_gpu)
+        prefill["one_prompt"] = one_prompt_summary(args)
+        if prefill["one_prompt"] is None:
+            return 1
     out = {
         "metric": METRIC,
         "value": round(tok_s, 1),

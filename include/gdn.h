@@ -40,9 +40,11 @@
  *   - One pool is not reentrant: calls that touch the same slots must be
  *     ordered on one stream by the caller. gdn_prefill_varlen uses a device
  *     workspace held by the pool, so its calls on a pool must be ordered on
- *     one stream; a call with a new maximum total_tokens synchronizes its
- *     stream and reallocates it, later calls at or below that size allocate
- *     nothing. gdn_decode allocates nothing.
+ *     one stream; a call that needs more workspace than the pool holds
+ *     (it grows with total_tokens, and for a few long sequences also holds
+ *     their chunk records) synchronizes its stream and reallocates it, later
+ *     calls at or below that size allocate nothing; gdn_pool_reserve sizes it
+ *     for any call up to a token count. gdn_decode allocates nothing.
  *   - The decode entries launch kernels only (no memset nodes, no host
  *     synchronisation), so a decode step over every layer can be captured in
  *     one HIP graph and replayed: gdn_decode, gdn_decode_gated, gdn_recurrent,
@@ -212,7 +214,12 @@ gdn_status gdn_decode_gated(gdn_pool* pool, int32_t layer, const int32_t* slot_i
  * a cu_seqlens that breaks these latches GDN_FLAG_BAD_SEQLENS (the kernels
  * clamp every bound they read). Uses the chunked (WY form, chunk 64)
  * algorithm; results equal the token-by-token recurrence within f32/bf16
- * rounding. */
+ * rounding. Two schedules give the same bits: one work-group per (sequence,
+ * value head), or, for a few long sequences (at most 96 sequence-heads, 1024
+ * tokens per sequence on average, 262,144 tokens per call), the chunks'
+ * state-independent blocks formed for all chunks at once and 2 or 4
+ * work-groups per (sequence, value head). The environment variable
+ * GDN_PREFILL_WAVES = 8 (the first), 4 or 2 (the second) forces one. */
 gdn_status gdn_prefill_varlen(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
                               const int32_t* cu_seqlens, int32_t nseq,
                               int32_t total_tokens, const uint16_t* mixed_qkv,
@@ -222,7 +229,8 @@ gdn_status gdn_prefill_varlen(gdn_pool* pool, int32_t layer, const int32_t* slot
 
 /* gdn_prefill_varlen for callers that cannot allocate device memory (code
  * under HIP graph capture, serving loops that forbid hipMalloc). No
- * counterpart in the reference. Same arguments, kernels and results; the
+ * counterpart in the reference. Same arguments and results (always the
+ * one-group-per-head schedule); the
  * workspace is a fixed 16 MiB array per device held by the library until the
  * process ends, instead of the pool's grown buffer. A call whose workspace
  * (16,576 bytes per token at 16 key / 32 value heads: up to 1012 tokens)
@@ -330,7 +338,8 @@ gdn_status gdn_layer_create(const gdn_layer_desc* desc, gdn_layer** out);
 gdn_status gdn_layer_destroy(gdn_layer* layer);
 
 /* Size the pool's activation buffer and prefill workspace for calls of up
- * to max_tokens tokens (decode batch size or packed prefill tokens). */
+ * to max_tokens tokens (decode batch size or packed prefill tokens), the
+ * chunk records of the few-long-sequences schedule included. */
 gdn_status gdn_pool_reserve(gdn_pool* pool, int32_t max_tokens, void* stream);
 
 /* S = 1 step of B sequences: x [B, x_stride] -> out [B, out_stride], state of

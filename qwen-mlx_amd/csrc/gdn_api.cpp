@@ -525,7 +525,11 @@ static gdn_status prefill_common(gdn_pool* pool, int32_t layer, const int32_t* s
   DeviceGuard guard(pool->d.device);
   st = debug_check_slots(pool, slot_ids, nseq, stream, who);
   if (st) return st;
-  const size_t need = gdn::prefill_workspace_bytes(pool->R, pool->d.num_k_heads, total_tokens);
+  // the fixed scratch of the no-allocation entry holds the fused path's workspace only
+  const int waves =
+      noalloc ? 8 : gdn::prefill_chunk_waves(pool->R, pool->d.num_k_heads, nseq, total_tokens);
+  const size_t need = gdn::prefill_workspace_bytes(pool->R, pool->d.num_k_heads, total_tokens, nseq,
+                                                   waves, out && !y);
   void* ws = nullptr;
   size_t ws_bytes = 0;
   if (noalloc) {
@@ -535,7 +539,7 @@ static gdn_status prefill_common(gdn_pool* pool, int32_t layer, const int32_t* s
                   "%s: %d tokens need %zu bytes of workspace; its fixed scratch holds %zu "
                   "(%zu bytes per token at these head counts)",
                   who, total_tokens, need, ws_bytes,
-                  gdn::prefill_workspace_bytes(pool->R, pool->d.num_k_heads, 1));
+                  gdn::prefill_workspace_bytes(pool->R, pool->d.num_k_heads, 1, 1, 8, false));
     hipError_t e = gdn::noalloc_scratch(&ws);
     if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
   } else {
@@ -566,6 +570,7 @@ static gdn_status prefill_common(gdn_pool* pool, int32_t layer, const int32_t* s
   a.norm_eps = norm_eps;
   a.out = out;
   a.status = pool->d_status;
+  a.waves = waves;
   a.workspace = ws;
   a.workspace_bytes = ws_bytes;
   a.stream = as_stream(stream);
@@ -890,8 +895,8 @@ gdn_status gdn_pool_reserve(gdn_pool* pool, int32_t max_tokens, void* stream) {
   st = ensure_buffer(pool->act, pool->act_bytes, layer_act_bytes(pool, max_tokens), stream,
                      "layer activation");
   if (st) return st;
-  return ensure_workspace(pool, gdn::prefill_workspace_bytes(pool->R, pool->d.num_k_heads,
-                                                             max_tokens), stream, "prefill");
+  return ensure_workspace(pool, gdn::prefill_workspace_reserve_bytes(pool->R, pool->d.num_k_heads,
+                                                                     max_tokens), stream, "prefill");
 }
 
 gdn_status gdn_layer_decode(gdn_layer* L, const int32_t* slot_ids, int32_t B, const uint16_t* x,

@@ -186,6 +186,7 @@ struct PrefillArgs {
   float norm_eps;
   uint16_t* out;          // [T, Hv, Dv] = silu(z) * rms_norm(y), or null
   uint32_t* status;
+  int waves;             // prefill_chunk_waves of the call (8: fused chunk kernel)
   void* workspace;       // device scratch sized by prefill_workspace_bytes
   size_t workspace_bytes;
   hipStream_t stream;
@@ -240,7 +241,9 @@ hipError_t launch_recurrent(const RecurrentArgs& a);
 hipError_t launch_slots(const SlotArgs& a);
 hipError_t launch_validate(const int32_t* slot_ids, int n, int num_slots, uint32_t* status,
                            hipStream_t stream);
-size_t prefill_workspace_bytes(int R, int Hk, int total_tokens);
+int prefill_chunk_waves(int R, int Hk, int nseq, int total_tokens);
+size_t prefill_workspace_bytes(int R, int Hk, int total_tokens, int nseq, int waves, bool y_scratch);
+size_t prefill_workspace_reserve_bytes(int R, int Hk, int max_tokens);
 // Fixed per-device workspace of gdn_prefill_varlen_noalloc (gdn_prefill.hip).
 size_t noalloc_scratch_bytes();
 hipError_t noalloc_scratch(void** out);

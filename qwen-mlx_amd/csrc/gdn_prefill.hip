@@ -11,6 +11,8 @@
 // Workspace layout (each region 256-byte aligned):
 //   qn [T,Hk,Dk] bf16 | kn [T,Hk,Dk] bf16 | vc [T,Hv,Dv] bf16 | beta [T,Hv] bf16 | lg [T,Hv] f32
 
+#include <algorithm>
+#include <cstdlib>
 #include <mutex>
 #include <type_traits>
 
@@ -24,6 +26,12 @@ constexpr float kQNormW = 0.0078125f;
 constexpr float kKNormW = 0.08837890625f;
 constexpr float kNormEps = 1e-6f;
 constexpr int kTT = 64;  // tokens per qkv_kernel work-group
+// The split path is taken for prompts of at least kSplitMinTokens tokens on
+// average and calls of at most kSplitMaxTokens tokens (its records take 272
+// bytes per token and value head).
+constexpr int kSplitMinTokens = 1024;
+constexpr int kSplitMaxTokens = 1 << 18;
+constexpr int kRecStride = 17408;  // bytes per chunk record (kRecBytes)
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -33,9 +41,11 @@ struct Workspace {
   uint16_t* vc;
   uint16_t* beta;
   float* lg;
+  uint16_t* rec;  // split path: chunk records [floor(T/64) + nseq][Hv] of 17,408 bytes
+  uint16_t* y;    // split path with the gated epilogue and no y from the caller: [T, Hv, Dv]
 };
 
-size_t carve(void* base, int R, int Hk, int T, Workspace* w) {
+size_t carve(void* base, int R, int Hk, int T, int nseq, int waves, bool y_scratch, Workspace* w) {
   const int Hv = Hk * R;
   size_t off = 0;
   char* p = static_cast<char*>(base);
@@ -50,6 +60,12 @@ size_t carve(void* base, int R, int Hk, int T, Workspace* w) {
   ws.vc = static_cast<uint16_t*>(take((size_t)T * Hv * kDv * 2));
   ws.beta = static_cast<uint16_t*>(take((size_t)T * Hv * 2));
   ws.lg = static_cast<float*>(take((size_t)T * Hv * 4));
+  ws.rec = nullptr;
+  ws.y = nullptr;
+  if (waves < 8) {
+    ws.rec = static_cast<uint16_t*>(take((size_t)(T / 64 + nseq) * Hv * kRecStride));
+    if (y_scratch) ws.y = static_cast<uint16_t*>(take((size_t)T * Hv * kDv * 2));
+  }
   if (w) *w = ws;
   return off;
 }
@@ -413,8 +429,14 @@ __device__ __forceinline__ s16x4 vtr(const ChunkSmem& sm, int row, int col) {
   return __builtin_bit_cast(s16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(p));
 }
 
-// f32 -> bf16 hi + lo (hi + lo carries ~16 mantissa bits)
+// f32 -> bf16 hi + lo (hi + lo carries ~16 mantissa bits). The arithmetic
+// shared by the fused and the split path is written so that the compiler
+// cannot fuse a product with a following add in one kernel and not in the
+// other (it decides per basic block): explicit fmaf where a fused operation is
+// meant, contraction off where a product is rounded on its own. Both paths
+// then give the same bits.
 __device__ __forceinline__ void split4(const f32x4& x, s16x4& hi, s16x4& lo) {
+#pragma clang fp contract(off)
   const uint32_t h0 = f2bf2(x[0], x[1]), h1 = f2bf2(x[2], x[3]);
   const uint32_t l0 = f2bf2(x[0] - bf_lo(h0), x[1] - bf_hi(h0));
   const uint32_t l1 = f2bf2(x[2] - bf_lo(h1), x[3] - bf_hi(h1));
@@ -427,7 +449,8 @@ __device__ __forceinline__ s16x4 hi4(const f32x4& x) {
 
 // L block (I, J), J <= I: an off-diagonal block as -L hi/lo into NL (row
 // 16I+c, columns 16J+4q..+3), a diagonal block into Ld in f32.
-__device__ __forceinline__ void put_l(ChunkSmem& sm, const f32x4& t, int I, int J, int q, int c) {
+template <class S>
+__device__ __forceinline__ void put_l(S& sm, const f32x4& t, int I, int J, int q, int c) {
   const int i = 16 * I + c;
   const float Gi = sm.G[i], bi = sm.beta[i];
   const f32x4 Gj = *reinterpret_cast<const f32x4*>(&sm.G[16 * J + 4 * q]);
@@ -449,7 +472,8 @@ __device__ __forceinline__ void put_l(ChunkSmem& sm, const f32x4& t, int I, int 
   }
 }
 // P block (I, J), J <= I: row 16I+c, columns 16J+4q..+3 at their pair-order place.
-__device__ __forceinline__ void put_p(ChunkSmem& sm, const f32x4& t, int I, int J, int q, int c) {
+template <class S>
+__device__ __forceinline__ void put_p(S& sm, const f32x4& t, int I, int J, int q, int c) {
   const int i = 16 * I + c;
   const float Gi = sm.G[i];
   const f32x4 Gj = *reinterpret_cast<const f32x4*>(&sm.G[16 * J + 4 * q]);
@@ -468,13 +492,15 @@ __device__ __forceinline__ void put_p(ChunkSmem& sm, const f32x4& t, int I, int 
 struct Frag {
   bf16x8 f[4];
 };
-__device__ __forceinline__ Frag kfrags(const ChunkSmem& sm, int kf, int X) {
+template <class S>
+__device__ __forceinline__ Frag kfrags(const S& sm, int kf, int X) {
   Frag r;
 #pragma unroll
   for (int b = 0; b < 4; ++b) r.f[b] = kfrag(sm.K, kf, X, b);
   return r;
 }
-__device__ __forceinline__ Frag qfrags(const ChunkSmem& sm, int X, int q, int c) {
+template <class S>
+__device__ __forceinline__ Frag qfrags(const S& sm, int X, int q, int c) {
   Frag r;
 #pragma unroll
   for (int b = 0; b < 4; ++b) r.f[b] = lds8(&sm.Q[16 * X + c][32 * b + 8 * q]);
@@ -495,7 +521,8 @@ __device__ __forceinline__ f32x4 tile(const Frag& colJ, const Frag& rowI) {
 // that a wave's four tiles share operand blocks (4-5 blocks of 16 rows).
 // Each wave's code is straight-line: all its LDS operand reads are in flight
 // together instead of one tile's reads at a time.
-__device__ __forceinline__ void other_blocks(ChunkSmem& sm, int w, int kf, int q, int c) {
+template <class S>
+__device__ __forceinline__ void other_blocks(S& sm, int w, int kf, int q, int c) {
   if (w == 4) {
     const Frag k0 = kfrags(sm, kf, 0), k1 = kfrags(sm, kf, 1), k2 = kfrags(sm, kf, 2),
                k3 = kfrags(sm, kf, 3), q3 = qfrags(sm, 3, q, c);
@@ -526,7 +553,134 @@ __device__ __forceinline__ void other_blocks(ChunkSmem& sm, int w, int kf, int q
     put_l(sm, tile(k0, k1), 1, 0, q, c);
   }
 }
+
+// Wave 0, lane l = token l of the chunk (raw bf16 beta b, log decay lg):
+// beta, the cumulative decay G in log2 units (an inclusive prefix sum over the
+// 64 lanes on DPP: shifts within each 16-lane row, then row 0's and row 2's
+// totals into rows 1 and 3 (row_bcast:15), then the first half's total into
+// rows 2 and 3 (row_bcast:31)), exp2(G) and the decay to the chunk's end.
+template <class S>
+__device__ __forceinline__ void form_gates(S& sm, uint16_t b, float lg, int lane) {
+#pragma clang fp contract(off)
+  float gsum = lg * 1.4426950408889634f;
+  gsum += dpp_f<0x111, 0xF>(gsum);  // row_shr:1
+  gsum += dpp_f<0x112, 0xF>(gsum);  // row_shr:2
+  gsum += dpp_f<0x114, 0xF>(gsum);  // row_shr:4
+  gsum += dpp_f<0x118, 0xF>(gsum);  // row_shr:8
+  gsum += dpp_f<0x142, 0xA>(gsum);  // row_bcast:15
+  gsum += dpp_f<0x143, 0xC>(gsum);  // row_bcast:31
+  const float gC = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gsum), 63));
+  sm.beta[lane] = bf2f(b);
+  sm.G[lane] = gsum;
+  sm.eG[lane] = __builtin_amdgcn_exp2f(gsum);
+  sm.dec[lane] = __builtin_amdgcn_exp2f(gC - gsum);
+}
+
+// Wave I (0..3): diagonal block I of L and its inverse D_I = (I + L_II)^-1 by
+// forward substitution with four lanes per column: lane (j = l/4, p = l%4)
+// sums the terms k = p (mod 4) of each row and two DPP adds close the sum
+// over its quad, so a row costs a handful of dependent VALU ops.
+template <class S>
+__device__ __forceinline__ void invert_diag(S& sm, int I, int kf, int q, int c, int lane) {
+  const Frag kI = kfrags(sm, kf, I);
+  put_l(sm, tile(kI, kI), I, I, q, c);
+  // this wave's own Ld writes, read back by other lanes of the wave
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  const int j = lane >> 2, pp = lane & 3;
+  const float* Lb = &sm.Ld[I * kLdLB + 4 * pp];
+  float tv[4] = {pp == 0 && j == 0 ? 1.f : 0.f, 0.f, 0.f, 0.f};  // t_{4m+p} of column j
+  f32x4 row = *reinterpret_cast<const f32x4*>(&Lb[kLdL]);
+#pragma unroll
+  for (int i = 1; i < 16; ++i) {
+    const f32x4 cur = row;
+    if (i + 1 < 16) row = *reinterpret_cast<const f32x4*>(&Lb[(i + 1) * kLdL]);
+    float part = 0.f;
+#pragma unroll
+    for (int m = 0; m <= (i - 1) >> 2; ++m) part = fmaf(cur[m], tv[m], part);
+    part += dpp_f<0xB1, 0xF>(part);  // quad_perm xor 1
+    part += dpp_f<0x4E, 0xF>(part);  // quad_perm xor 2
+    const float ti = (i == j ? 1.f : 0.f) - part;
+    if (pp == (i & 3)) tv[i >> 2] = ti;
+  }
+  // rows 4m + p of column j, hi and lo
+  uint16_t* Dp = &sm.D[I * kLdDB + 8 * (j >> 2) + (j & 3)];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const uint16_t h = f2bf(tv[m]);
+    Dp[(4 * m + pp) * kLdD] = h;
+    Dp[(4 * m + pp) * kLdD + 4] = f2bf(tv[m] - bf2f(h));
+  }
+}
+
+// Record of one (chunk, value head) for the split path: the operands of the
+// chunk's state products that do not depend on the state, in 16-byte units u
+// (rec_slot gives each unit's place in the LDS layouts above):
+//   [0, 384)      -L, rows 16..63: row 16I + i (I = 1..3) holds the 4I column
+//                 groups of its blocks left of the diagonal (hi/lo per 4 columns)
+//   [384, 640)    D, block I, row i: 4 groups
+//   [640, 1024)   P, rows 0..31 groups 0-3, rows 32..63 groups 0-7 (pair order;
+//                 the halves above the diagonal are 0)
+//   [1024, 1072)  beta, exp2(G), exp2(G_C - G): 16 units each (f32)
+constexpr int kRecUnits = 1072;
+constexpr int kRecBytes = kRecStride;  // record stride (256-byte aligned)
+static_assert(kRecBytes >= kRecUnits * 16 && kRecBytes % 256 == 0, "record stride");
+template <class S>
+__device__ __forceinline__ void* rec_slot(S& sm, int u) {
+  if (u < 384) {
+    int row, g;
+    if (u < 64) {
+      row = 16 + (u >> 2);
+      g = u & 3;
+    } else if (u < 192) {
+      row = 32 + ((u - 64) >> 3);
+      g = (u - 64) & 7;
+    } else {
+      const int off = u - 192, r = off / 12;
+      row = 48 + r;
+      g = off - 12 * r;
+    }
+    return &sm.NL[row][8 * (g ^ gsw(row))];
+  }
+  if (u < 640) {
+    const int v = u - 384;
+    return &sm.D[(v >> 6) * kLdDB + ((v >> 2) & 15) * kLdD + 8 * (v & 3)];
+  }
+  if (u < 1024) {
+    const int v = u - 640;
+    const int row = v < 128 ? v >> 2 : 32 + ((v - 128) >> 3);
+    const int g = v < 128 ? v & 3 : (v - 128) & 7;
+    return &sm.P[row][8 * (g ^ gsw(row))];
+  }
+  const int v = u - 1024, k = 4 * (v & 15);
+  return v < 16 ? &sm.beta[k] : v < 32 ? &sm.eG[k] : &sm.dec[k];
+}
+
+// Sum of squares of 4 bf16 outputs, and the RMSNormGated output of 8 rows
+// (silu(z) * bf16(w * bf16(y * rn))), shared by the chunk kernel's epilogue
+// and the split path's separate epilogue so that both give the same bits.
+__device__ __forceinline__ float sumsq4(float a, float b, float c, float d) {
+  return fmaf(b, b, a * a) + fmaf(d, d, c * c);
+}
+__device__ __forceinline__ float rms_scale(float tot, float eps) {
+  return 1.0f / sqrtf(tot / (float)kDv + eps);
+}
+__device__ __forceinline__ u32x4 norm_gate8(const u32x4& yv, const u32x4& zv, const u32x4& nw, float rn) {
+  u32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float o0 = silu_bf16(bf_lo(zv[e])) * rbf(bf_lo(nw[e]) * rbf(bf_lo(yv[e]) * rn));
+    const float o1 = silu_bf16(bf_hi(zv[e])) * rbf(bf_hi(nw[e]) * rbf(bf_hi(yv[e]) * rn));
+    o[e] = f2bf2(o0, o1);
+  }
+  return o;
+}
 }  // namespace
+
+// Record slot of chunk k of sequence s (first token st): floor(st/64) + s + k.
+// Over a call the slots are distinct and below floor(T/64) + nseq: sequence s
+// has at most floor(st_{s+1}/64) - floor(st_s/64) + 1 chunks.
+inline int rec_slots(int T, int nseq) { return T / kC + nseq; }
 
 // With GATED the RMSNormGated epilogue (qwen3_5.rs:660-665) runs on the
 // chunk's outputs: out[t, hv, :] = silu(z) * rms_norm(y, norm_w, norm_eps)
@@ -540,38 +694,55 @@ __device__ __forceinline__ void other_blocks(ChunkSmem& sm, int w, int kf, int q
 // 1.79 ms with 64 of 4, 2.26 ms with 128 of 2). The chunk's outputs go
 // through LDS and leave as whole 256-byte rows.
 //
-// 1D grid of Hv * nseq groups. Work-groups are dealt to the 8 XCDs
-// round-robin; the R groups that read one key head's k and q are numbered 8
-// apart, so they run on one XCD and fetch those rows from HBM once.
-template <int R, bool GATED>
-__global__ __launch_bounds__(512) void prefill_chunk_kernel(
+// Split path (W = 2 or 4): the chunk's blocks of L and P, the inverses D_I
+// and the gates come from the records of prefill_form_kernel, and each
+// (sequence, value head) has 8/W groups of W waves, each group 16W state
+// rows; without the block formation the groups need no barrier between
+// the products and the solve. The split path has no GATED epilogue (the
+// norm runs over all 128 rows of a head; prefill_norm_gate_kernel does it).
+//
+// 1D grid of Hv * nseq * (8/W) groups. Work-groups are dealt to the 8 XCDs
+// round-robin; the R * 8/W groups that read one key head's k and q are
+// numbered 8 apart, so they run on one XCD and fetch those rows once.
+template <int R, bool GATED, int W>
+__global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
     float* __restrict__ state, const int32_t* __restrict__ slot_ids,
     const int32_t* __restrict__ cu, int num_slots, int Hk, int T,
     const uint16_t* __restrict__ qn, const uint16_t* __restrict__ kn,
     const uint16_t* __restrict__ vc, const float* __restrict__ lgv,
-    const uint16_t* __restrict__ betav, uint16_t* __restrict__ y,
+    const uint16_t* __restrict__ betav, const uint16_t* __restrict__ rec, uint16_t* __restrict__ y,
     const uint16_t* __restrict__ zrow, int64_t xs, const uint16_t* __restrict__ norm_w,
     float norm_eps, uint16_t* __restrict__ out, uint32_t* __restrict__ status) {
-  constexpr int NT = 512;
-  constexpr int UK = kC * kDk / 8 / NT;  // 16-byte input units per thread and matrix
+  static_assert(W == 2 || W == 4 || W == 8, "8 waves (fused) or a split of 2 or 4");
+  static_assert(W == 8 || !GATED, "the split path has no epilogue");
+  constexpr bool FUSED = W == 8;
+  constexpr int NT = 64 * W;
+  constexpr int UK = kC * kDk / 8 / NT;         // 16-byte k (and q) units per thread
+  constexpr int UV = 2;                         // 16-byte v units per thread (2W per row)
+  constexpr int UR = (kRecUnits + NT - 1) / NT; // 16-byte record units per thread
+  constexpr int M = R * (8 / W);                // groups per (sequence, key head)
   __shared__ ChunkSmem sm;
   const int Hv = Hk * R;
-  int hv, s;
+  int hv, s, split;
   {
     const int L = blockIdx.x;
-    if ((int)gridDim.x % (8 * R) == 0) {
-      const int m = L >> 3, g = (L & 7) + 8 * (m / R);
-      s = g / Hk;
-      hv = (g % Hk) * R + m % R;
+    int g, m;
+    if ((int)gridDim.x % (8 * M) == 0) {
+      m = (L >> 3) % M;
+      g = (L & 7) + 8 * ((L >> 3) / M);
     } else {
-      hv = L % Hv;
-      s = L / Hv;
+      m = L % M;
+      g = L / M;
     }
+    s = g / Hk;
+    hv = (g % Hk) * R + m % R;
+    split = m / R;
   }
   const int hk = hv / R;
   const int tid = threadIdx.x, lane0 = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, scalar
-  const int dv0 = 16 * w;                                  // this wave's first state row
+  const int dvb = 16 * W * split;                          // the group's first state row
+  const int dv0 = dvb + 16 * w;                            // this wave's first state row
   const int slot = slot_ids[s];
   if ((unsigned)slot >= (unsigned)num_slots) {
     if (tid == 0 && blockIdx.x == 0) flag_status(status, GDN_FLAG_BAD_SLOT);
@@ -585,13 +756,14 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
   f32x4 acc[8];  // S^T tiles: dk rows 16a + 4q + r, state row dv0 + c
 #pragma unroll
   for (int a = 0; a < 8; ++a) acc[a] = *reinterpret_cast<const f32x4*>(gstate + 16 * a);
-  // write-out layout: thread (tokens tid/16 and 32 + tid/16, 8 output rows
-  // from 8 * (tid % 16)); 16 lanes cover one token's 256-byte row
-  const int oi = tid >> 4, od = 8 * (tid & 15);
+  // write-out layout: thread (tokens oi and oi + 32, 8 output rows from od);
+  // 2W lanes cover one token's 32W-byte part of the row
+  const int oi = tid / (2 * W), od = dvb + 8 * (tid % (2 * W));
   u32x4 nw = {0u, 0u, 0u, 0u};  // GATED: the norm weights of rows od..od+7
   if constexpr (GATED) nw = *reinterpret_cast<const u32x4*>(norm_w + od);
   // Blocks of P above the diagonal are never written: zero them once.
-  for (int e = tid; e < kC * kLdP / 4; e += NT) reinterpret_cast<uint2*>(&sm.P[0][0])[e] = make_uint2(0u, 0u);
+  if constexpr (FUSED)
+    for (int e = tid; e < kC * kLdP / 4; e += NT) reinterpret_cast<uint2*>(&sm.P[0][0])[e] = make_uint2(0u, 0u);
 
   // chunk inputs, prefetched one chunk ahead: 16-byte units of the k, q and
   // v rows (thread e: row e/16, elements 8(e%16)..+7) and, for lane l, token
@@ -606,7 +778,7 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
   // makes the wave wait for the load right after issuing it instead of one
   // chunk later. Sizes go through readfirstlane: a resource held in VGPRs
   // would need a waterfall loop around each load.
-  u32x4 kv[UK], qv[UK], vv[UK];
+  u32x4 kv[UK], qv[UK], vv[UV], rv[UR];
   uint16_t pb = 0;
   float pl = 0.f;
   auto rows_of = [&](int c) { return __builtin_amdgcn_readfirstlane(max(0, min(kC, en - c))); };
@@ -624,16 +796,28 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
       if constexpr (decltype(KQ)::value) qv[u] = x; else kv[u] = x;
     }
   };
+  // v: the group's 16W columns of the chunk's rows (unit e: row e/(2W),
+  // columns dvb + 8(e%(2W)) ..)
   auto load_v = [&](int c) {
     const int n = rows_of(c);
-    const int bytes = __builtin_amdgcn_readfirstlane(n > 0 ? ((n - 1) * Hv + 1) * kDv * 2 : 0);
+    const int bytes = __builtin_amdgcn_readfirstlane(n > 0 ? ((n - 1) * Hv + 1) * kDv * 2 - 2 * dvb : 0);
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(vc + ((size_t)c * Hv + hv) * kDv), (short)0, bytes, 0x00020000);
+        (void*)(vc + ((size_t)c * Hv + hv) * kDv + dvb), (short)0, bytes, 0x00020000);
 #pragma unroll
-    for (int u = 0; u < UK; ++u) {
-      const int e = tid + NT * u, i = e >> 4, m = e & 15;
+    for (int u = 0; u < UV; ++u) {
+      const int e = tid + NT * u, i = e / (2 * W), m = e % (2 * W);
       vv[u] = __builtin_amdgcn_raw_buffer_load_b128(r, i * Hv * kDv * 2 + 16 * m, 0, 0);
     }
+  };
+  // split path: the record of the chunk at token c (none past the sequence end)
+  auto load_rec = [&](int c) {
+    const int n = rows_of(c);
+    const int x = st / kC + s + (c - st) / kC;
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(rec + ((size_t)x * Hv + hv) * (kRecBytes / 2)), (short)0, n > 0 ? kRecUnits * 16 : 0,
+        0x00020000);
+#pragma unroll
+    for (int j = 0; j < UR; ++j) rv[j] = __builtin_amdgcn_raw_buffer_load_b128(r, 16 * (tid + NT * j), 0, 0);
   };
   // every wave reads the 64 gate values (wave 0 uses them)
   auto load_gates = [&](int c) {
@@ -646,12 +830,22 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
     pb = __builtin_amdgcn_raw_buffer_load_b16(br, lane0 * Hv * 2, 0, 0);
     pl = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(lr, lane0 * Hv * 4, 0, 0));
   };
+  // split path: the LDS byte offsets of this thread's record units, the same
+  // for every chunk
+  uint32_t roff[FUSED ? 1 : UR];
+  if constexpr (!FUSED) {
+#pragma unroll
+    for (int j = 0; j < UR; ++j) {
+      const int u = min(tid + NT * j, kRecUnits - 1);
+      roff[j] = static_cast<uint32_t>(static_cast<char*>(rec_slot(sm, u)) - reinterpret_cast<char*>(&sm));
+    }
+  }
   using KLoad = std::integral_constant<int, 0>;
   using QLoad = std::integral_constant<int, 1>;
   load_kq(st, KLoad{});
   load_kq(st, QLoad{});
   load_v(st);
-  load_gates(st);
+  if constexpr (FUSED) load_gates(st); else load_rec(st);
   for (int c0 = st; c0 < en; c0 += kC) {
     const int n = min(kC, en - c0);
     // Lane-derived values are recomputed in every chunk (a few VALU ops)
@@ -669,7 +863,6 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
       // (even) swizzle, one 16-byte write
       const int e = tid + NT * u, i = e >> 4, m = e & 15;
       *static_cast<u32x4*>(__builtin_assume_aligned(&sm.K[kseg(i, 2 * m)], 16)) = kv[u];
-      *static_cast<u32x4*>(__builtin_assume_aligned(&sm.V[i][8 * m], 16)) = vv[u];
       // q (unit qunit(e) of row qrow(e)): dk 8m..8m+3 and 8m+4..8m+7 go to
       // pair-order places p and p + 8, p = 32(m/4) + 16(m%2) + 4((m/2)%2).
       // An 8-byte write pass (16 lanes) covers units 0-7 or 8-15 of an even
@@ -681,66 +874,30 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
       *static_cast<u32x2*>(__builtin_assume_aligned(&sm.Q[qi][p + 8 * odd], 8)) = odd ? qhi : qlo;
       *static_cast<u32x2*>(__builtin_assume_aligned(&sm.Q[qi][p + 8 - 8 * odd], 8)) = odd ? qlo : qhi;
     }
-    if (w == 0) {
-      // inclusive prefix sum over the 64 lanes on DPP: shifts within each
-      // 16-lane row, then row 0's and row 2's totals into rows 1 and 3
-      // (row_bcast:15), then the first half's total into rows 2 and 3 (row_bcast:31)
-      float gsum = pl * 1.4426950408889634f;
-      gsum += dpp_f<0x111, 0xF>(gsum);  // row_shr:1
-      gsum += dpp_f<0x112, 0xF>(gsum);  // row_shr:2
-      gsum += dpp_f<0x114, 0xF>(gsum);  // row_shr:4
-      gsum += dpp_f<0x118, 0xF>(gsum);  // row_shr:8
-      gsum += dpp_f<0x142, 0xA>(gsum);  // row_bcast:15
-      gsum += dpp_f<0x143, 0xC>(gsum);  // row_bcast:31
-      const float gC = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gsum), 63));
-      sm.beta[lane0] = bf2f(pb);
-      sm.G[lane0] = gsum;
-      sm.eG[lane0] = __builtin_amdgcn_exp2f(gsum);
-      sm.dec[lane0] = __builtin_amdgcn_exp2f(gC - gsum);
+#pragma unroll
+    for (int u = 0; u < UV; ++u) {
+      const int e = tid + NT * u, i = e / (2 * W), m = e % (2 * W);
+      *static_cast<u32x4*>(__builtin_assume_aligned(&sm.V[i][dvb + 8 * m], 16)) = vv[u];
+    }
+    if constexpr (FUSED) {
+      if (w == 0) form_gates(sm, pb, pl, lane0);
+    } else {
+#pragma unroll
+      for (int j = 0; j < UR; ++j)
+        if (tid + NT * j < kRecUnits)
+          *static_cast<u32x4*>(__builtin_assume_aligned(reinterpret_cast<char*>(&sm) + roff[j], 16)) = rv[j];
     }
     __syncthreads();
     load_kq(c0 + kC, KLoad{});  // past the sequence end: no memory access, reads 0
 
-    // (b) the chunk's matrices. Diagonal block I of L goes to wave I, which
-    // forms it and inverts it, D_I = (I + L_II)^-1, by forward substitution
-    // with four lanes per column: lane (j = l/4, p = l%4) sums the terms
-    // k = p (mod 4) of each row and two DPP adds close the sum over its quad,
-    // so a row costs a handful of dependent VALU ops. Waves 4-7 form the
-    // other 16 blocks, four each.
+    if constexpr (FUSED) {
+      // (b) the chunk's matrices: waves 0-3 the diagonal blocks of L and their
+      // inverses, waves 4-7 the other 16 blocks of L and P
 #pragma unroll
-    for (int I = 0; I < 4; ++I) {
-      if (w != I) continue;
-      const Frag kI = kfrags(sm, kf, I);
-      put_l(sm, tile(kI, kI), I, I, q, c);
-      // this wave's own Ld writes, read back by other lanes of the wave
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      const int j = lane0 >> 2, pp = lane0 & 3;
-      const float* Lb = &sm.Ld[I * kLdLB + 4 * pp];
-      float tv[4] = {pp == 0 && j == 0 ? 1.f : 0.f, 0.f, 0.f, 0.f};  // t_{4m+p} of column j
-      f32x4 row = *reinterpret_cast<const f32x4*>(&Lb[kLdL]);
-#pragma unroll
-      for (int i = 1; i < 16; ++i) {
-        const f32x4 cur = row;
-        if (i + 1 < 16) row = *reinterpret_cast<const f32x4*>(&Lb[(i + 1) * kLdL]);
-        float part = 0.f;
-#pragma unroll
-        for (int m = 0; m <= (i - 1) >> 2; ++m) part += cur[m] * tv[m];
-        part += dpp_f<0xB1, 0xF>(part);  // quad_perm xor 1
-        part += dpp_f<0x4E, 0xF>(part);  // quad_perm xor 2
-        const float ti = (i == j ? 1.f : 0.f) - part;
-        if (pp == (i & 3)) tv[i >> 2] = ti;
-      }
-      // rows 4m + p of column j, hi and lo
-      uint16_t* Dp = &sm.D[I * kLdDB + 8 * (j >> 2) + (j & 3)];
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const uint16_t h = f2bf(tv[m]);
-        Dp[(4 * m + pp) * kLdD] = h;
-        Dp[(4 * m + pp) * kLdD + 4] = f2bf(tv[m] - bf2f(h));
-      }
+      for (int I = 0; I < 4; ++I)
+        if (w == I) invert_diag(sm, I, kf, q, c, lane0);  // block index a compile-time constant
+      other_blocks(sm, w, kf, q, c);
     }
-    other_blocks(sm, w, kf, q, c);
     load_kq(c0 + kC, QLoad{});
     // (c) Y_I = K_I S^T (S hi and lo) and Zt_I = S Q_I^T (S hi) for this wave's
     // 16 state rows; the pair (acc[2b], acc[2b+1]) is the operand of dk block b
@@ -752,7 +909,10 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
     }
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      asm volatile("" ::: "memory");  // bound live ranges: one dk block at a time
+      // fused: bound live ranges, one dk block at a time (two waves per SIMD
+      // share its registers); the split path has the registers to keep every
+      // block's operand reads in flight together
+      if constexpr (FUSED) asm volatile("" ::: "memory");
       s16x4 h0, l0, h1, l1;
       split4(acc[2 * b], h0, l0);
       split4(acc[2 * b + 1], h1, l1);
@@ -765,33 +925,31 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
         zt[I] = mfma32(sh, lds8(&sm.Q[16 * I + c][32 * b + 8 * q]), zt[I]);
       }
     }
-    __syncthreads();
+    if constexpr (FUSED) __syncthreads();  // the blocks formed in (b)
 
     load_v(c0 + kC);
-    // (d) R_I = beta (V - exp(G) Y_I), then V'_I = D_I (R_I - sum_{j<I} L_Ij V'_j)
-    f32x4 vf[4];        // V' (f32), tokens 16I + 4q + r, state row dv0 + c
-    bf16x8 vpd[4];      // cat(V'h, V'h)
-    bf16x8 vplz[4];     // cat(V'l, 0)
-    s16x4 vph[4];
+    // (d) R_I = beta (V - exp(G) Y_I), then V'_I = D_I (R_I - sum_{j<I} L_Ij V'_j),
+    // right-looking: as soon as V'_I is known it is added into the right-hand
+    // sides of the blocks below it, so the chain between two blocks is two
+    // MFMAs, not all of the later block's terms. Each x_J still adds its terms
+    // in the order R_J, j = 0, 1, ..
+    f32x4 x[4];         // right-hand sides, tokens 16I + 4q + r, state row dv0 + c
+    f32x4 vf[4];        // V' (f32)
+    s16x4 vph[4];       // V'h
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       const f32x4 bt = *reinterpret_cast<const f32x4*>(&sm.beta[16 * I + 4 * q]);
       const f32x4 eg = *reinterpret_cast<const f32x4*>(&sm.eG[16 * I + 4 * q]);
-      f32x4 x;
       // v of tokens 16I + 4q + r, state row dv0 + c (a transposing read: lane
       // 4u + s of each 16-lane group reads row 4q + u, columns 4s..4s+3)
       const s16x4 vt = vtr(sm, 16 * I + 4 * q + (c >> 2), dv0 + 4 * (c & 3));
 #pragma unroll
-      for (int r = 0; r < 4; ++r) x[r] = bt[r] * (bf2f((uint16_t)vt[r]) - eg[r] * yk[I][r]);
+      for (int r = 0; r < 4; ++r) x[I][r] = bt[r] * fmaf(-eg[r], yk[I][r], bf2f((uint16_t)vt[r]));
+    }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (j >= I) continue;
-        const bf16x8 nl = lds8(&sm.NL[16 * I + c][32 * j + qs]);  // -L hi | lo
-        x = mfma32(nl, vpd[j], x);   // (NLh + NLl) V'h
-        x = mfma32(nl, vplz[j], x);  // NLh V'l
-      }
+    for (int I = 0; I < 4; ++I) {
       s16x4 xh, xl;
-      split4(x, xh, xl);
+      split4(x[I], xh, xl);
       const bf16x8 d = lds8(&sm.D[I * kLdDB + c * kLdD + 8 * q]);  // D hi | lo
       f32x4 v = {0.f, 0.f, 0.f, 0.f};
       v = mfma32(d, cat(xh, xh), v);     // (Dh + Dl) xh
@@ -799,10 +957,15 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
       vf[I] = v;
       s16x4 vl;
       split4(v, vph[I], vl);
-      vpd[I] = cat(vph[I], vph[I]);
-      vplz[I] = cat(vl, kZero4);
+      const bf16x8 vpd = cat(vph[I], vph[I]), vplz = cat(vl, kZero4);
+#pragma unroll
+      for (int J = I + 1; J < 4; ++J) {
+        const bf16x8 nl = lds8(&sm.NL[16 * J + c][32 * I + qs]);  // -L_JI hi | lo
+        x[J] = mfma32(nl, vpd, x[J]);   // (NLh + NLl) V'h
+        x[J] = mfma32(nl, vplz, x[J]);  // NLh V'l
+      }
     }
-    load_gates(c0 + kC);
+    if constexpr (FUSED) load_gates(c0 + kC); else load_rec(c0 + kC);
     // GATED: z of this thread's two write-out tokens of this chunk, read here
     // so that it arrives during (e) and (f); a token past the chunk's end
     // reads the chunk's last row instead (its output is not written), which
@@ -828,8 +991,7 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
       const uint2 yb = make_uint2(f2bf2(o[0], o[1]), f2bf2(o[2], o[3]));
       *reinterpret_cast<uint2*>(&sm.Y[16 * I + c][dv0 + 4 * q]) = yb;
       if constexpr (GATED) {
-        const float y0 = bf_lo(yb.x), y1 = bf_hi(yb.x), y2 = bf_lo(yb.y), y3 = bf_hi(yb.y);
-        float ss = (y0 * y0 + y1 * y1) + (y2 * y2 + y3 * y3);
+        float ss = sumsq4(bf_lo(yb.x), bf_hi(yb.x), bf_lo(yb.y), bf_hi(yb.y));
         ss += __shfl_xor(ss, 16, 64);
         ss += __shfl_xor(ss, 32, 64);
         if (q == 0) sm.ysq[16 * I + c][w] = ss;
@@ -875,18 +1037,8 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
         const f32x4 p0 = *reinterpret_cast<const f32x4*>(&sm.ysq[i][0]);
         const f32x4 p1 = *reinterpret_cast<const f32x4*>(&sm.ysq[i][4]);
         const float tot = ((p0[0] + p0[1]) + (p0[2] + p0[3])) + ((p1[0] + p1[1]) + (p1[2] + p1[3]));
-        const float rn = 1.0f / sqrtf(tot / (float)kDv + norm_eps);
-        const uint32_t yw[4] = {yv.x, yv.y, yv.z, yv.w};
-        const uint32_t zw[4] = {zv[h][0], zv[h][1], zv[h][2], zv[h][3]};
-        const uint32_t ww[4] = {nw[0], nw[1], nw[2], nw[3]};
-        uint32_t ow[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float o0 = silu_bf16(bf_lo(zw[e])) * rbf(bf_lo(ww[e]) * rbf(bf_lo(yw[e]) * rn));
-          const float o1 = silu_bf16(bf_hi(zw[e])) * rbf(bf_hi(ww[e]) * rbf(bf_hi(yw[e]) * rn));
-          ow[e] = f2bf2(o0, o1);
-        }
-        *reinterpret_cast<uint4*>(out + row) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+        const u32x4 o = norm_gate8(u32x4{yv.x, yv.y, yv.z, yv.w}, zv[h], nw, rms_scale(tot, norm_eps));
+        *reinterpret_cast<u32x4*>(out + row) = o;
       }
     }
   }
@@ -895,8 +1047,157 @@ __global__ __launch_bounds__(512) void prefill_chunk_kernel(
     *reinterpret_cast<f32x4*>(gstate + 16 * a) = acc[a];
 }
 
-size_t prefill_workspace_bytes(int R, int Hk, int total_tokens) {
-  return carve(nullptr, R, Hk, total_tokens, nullptr);
+// Shared memory of prefill_form_kernel: the block-forming part of ChunkSmem.
+struct __attribute__((aligned(16))) FormSmem {
+  uint16_t K[4 * kKBlk];
+  uint16_t Q[kC][kLdQ];
+  uint16_t P[kC][kLdP];
+  uint16_t NL[kC][kLdN];
+  uint16_t D[4 * kLdDB];
+  float Ld[4 * kLdLB];
+  float beta[kC], G[kC], eG[kC], dec[kC];
+};
+
+// Split path, step 1 of 2: for every (chunk, value head) of the call at once,
+// the chunk's blocks of L and P, the inverses D_I and the gates, formed by the
+// same code as in the chunk kernel's step (b), written as the chunk's record
+// (see rec_slot). Item = (record slot x, value head); slots that hold no
+// chunk (see rec_slots) exit. 8 waves: waves 0-3 invert the diagonal blocks,
+// waves 4-7 form the other 16. The R heads of one (slot, key head) are
+// numbered 8 apart, so they run on one XCD and share its k and q rows.
+template <int R>
+__global__ __launch_bounds__(512) void prefill_form_kernel(
+    const int32_t* __restrict__ cu, int nseq, int Hk, int T, const uint16_t* __restrict__ qn,
+    const uint16_t* __restrict__ kn, const float* __restrict__ lgv,
+    const uint16_t* __restrict__ betav, uint16_t* __restrict__ rec) {
+  constexpr int NT = 512;
+  __shared__ FormSmem sm;
+  const int Hv = Hk * R;
+  int g, r;
+  {
+    const int L = blockIdx.x;
+    if ((int)gridDim.x % (8 * R) == 0) {
+      const int m = L >> 3;
+      g = (L & 7) + 8 * (m / R);
+      r = m % R;
+    } else {
+      g = L / R;
+      r = L % R;
+    }
+  }
+  const int x = g / Hk, hk = g % Hk, hv = hk * R + r;
+  // the sequence of slot x: the largest s with floor(st_s / 64) + s <= x
+  int lo = 0, hi = nseq - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (min(max(cu[mid], 0), T) / kC + mid <= x) lo = mid; else hi = mid - 1;
+  }
+  const int s = lo;
+  const int st = min(max(cu[s], 0), T), en = min(max(cu[s + 1], st), T);
+  // (a slot below the sequence's first one only with a malformed cu_seqlens)
+  if (x < st / kC + s) return;
+  const int c0 = st + kC * (x - st / kC - s);
+  if (c0 >= en) return;
+  const int n = min(kC, en - c0);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q = lane >> 4, c = lane & 15, kf = kseg(c, q);
+  // P's halves above the diagonal belong to the record: zero P first
+  for (int e = tid; e < kC * kLdP / 4; e += NT) reinterpret_cast<uint2*>(&sm.P[0][0])[e] = make_uint2(0u, 0u);
+  // k (natural order, swizzled segments) and q (pair order) of the chunk's
+  // rows, 0 beyond its last token; two 16-byte units per thread and matrix
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int e = tid + NT * u, i = e >> 4, m = e & 15;
+    u32x4 kv = {0u, 0u, 0u, 0u}, qv = kv;
+    if (i < n) {
+      const size_t row = ((size_t)(c0 + i) * Hk + hk) * kDk;
+      kv = *reinterpret_cast<const u32x4*>(kn + row + 8 * m);
+      qv = *reinterpret_cast<const u32x4*>(qn + row + 8 * m);
+    }
+    *static_cast<u32x4*>(__builtin_assume_aligned(&sm.K[kseg(i, 2 * m)], 16)) = kv;
+    const int p = 32 * (m >> 2) + 16 * (m & 1) + 4 * ((m >> 1) & 1);
+    *static_cast<u32x2*>(__builtin_assume_aligned(&sm.Q[i][p], 8)) = u32x2{qv[0], qv[1]};
+    *static_cast<u32x2*>(__builtin_assume_aligned(&sm.Q[i][p + 8], 8)) = u32x2{qv[2], qv[3]};
+  }
+  if (w == 0) {
+    uint16_t b = 0;
+    float lg = 0.f;
+    if (lane < n) {
+      b = betav[(size_t)(c0 + lane) * Hv + hv];
+      lg = lgv[(size_t)(c0 + lane) * Hv + hv];
+    }
+    form_gates(sm, b, lg, lane);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int I = 0; I < 4; ++I)
+    if (w == I) invert_diag(sm, I, kf, q, c, lane);
+  other_blocks(sm, w, kf, q, c);
+  __syncthreads();
+  uint16_t* dst = rec + ((size_t)x * Hv + hv) * (kRecBytes / 2);
+  for (int u = tid; u < kRecUnits; u += NT)
+    *reinterpret_cast<u32x4*>(dst + 8 * u) = *static_cast<const u32x4*>(__builtin_assume_aligned(rec_slot(sm, u), 16));
+}
+
+// Split path, RMSNormGated epilogue (qwen3_5.rs:660-665) over y written by the
+// chunk kernel: out[t, hv, :] = silu(z) * bf16(w * bf16(y * rn)). 16 lanes per
+// (token, value head), lane j rows 8j..8j+7; the sum of y^2 runs in the order
+// of the chunk kernel's own epilogue (per 4 rows, then per 16, then over the
+// 8 groups of 16 pairwise), so that both paths give the same bits.
+__global__ __launch_bounds__(256) void prefill_norm_gate_kernel(
+    const uint16_t* __restrict__ y, const uint16_t* __restrict__ zrow, int64_t xs,
+    const uint16_t* __restrict__ norm_w, float norm_eps, uint16_t* __restrict__ out, int T, int Hv) {
+  const int item = blockIdx.x * 16 + (threadIdx.x >> 4), j = threadIdx.x & 15;
+  if (item >= T * Hv) return;  // a whole 16-lane group
+  const int t = item / Hv, hv = item % Hv;
+  const size_t row = ((size_t)t * Hv + hv) * kDv + 8 * j;
+  const u32x4 yv = *reinterpret_cast<const u32x4*>(y + row);
+  const u32x4 zv = *reinterpret_cast<const u32x4*>(zrow + (size_t)t * xs + (size_t)hv * kDv + 8 * j);
+  const u32x4 nw = *reinterpret_cast<const u32x4*>(norm_w + 8 * j);
+  // lane 2k: rows 16k..16k+7 (the chunk kernel's lanes q = 0, 1 of wave k),
+  // lane 2k + 1: rows 16k+8..16k+15 (q = 2, 3)
+  float p = sumsq4(bf_lo(yv[0]), bf_hi(yv[0]), bf_lo(yv[1]), bf_hi(yv[1])) +
+            sumsq4(bf_lo(yv[2]), bf_hi(yv[2]), bf_lo(yv[3]), bf_hi(yv[3]));
+  p += __shfl_xor(p, 1, 16);
+  p += __shfl_xor(p, 2, 16);
+  p += __shfl_xor(p, 4, 16);
+  p += __shfl_xor(p, 8, 16);
+  *reinterpret_cast<u32x4*>(out + row) = norm_gate8(yv, zv, nw, rms_scale(p, norm_eps));
+}
+
+// Waves per work-group of the chunk kernel for a call: 8 runs the fused
+// chunk kernel alone (one group per (sequence, value head)); 2 or 4 run the
+// split path (prefill_form_kernel, then 8/W groups per (sequence, value
+// head)) where the fused kernel would leave most CUs idle: few sequences of
+// many chunks. The environment variable GDN_PREFILL_WAVES = 2, 4 or 8 forces
+// a path (tests compare the paths with it).
+int prefill_chunk_waves(int R, int Hk, int nseq, int total_tokens) {
+  if (const char* v = getenv("GDN_PREFILL_WAVES")) {
+    const int f = atoi(v);
+    if (f == 2 || f == 4 || f == 8) return total_tokens > 0 ? f : 8;
+  }
+  if (nseq <= 0 || total_tokens <= 0 || total_tokens > kSplitMaxTokens) return 8;
+  if (total_tokens / nseq < kSplitMinTokens) return 8;
+  // measured on 16,384-token prompts (32 value heads): one or two prompts
+  // 1.10 / 1.30 ms split against 1.36 / 1.50 ms fused per call; four prompts
+  // 1.80 ms with 4-wave groups against 1.76 ms fused
+  const int groups = nseq * Hk * R;
+  return groups <= 64 ? 2 : groups <= 96 ? 4 : 8;
+}
+
+size_t prefill_workspace_bytes(int R, int Hk, int total_tokens, int nseq, int waves, bool y_scratch) {
+  return carve(nullptr, R, Hk, total_tokens, nseq, waves, y_scratch, nullptr);
+}
+
+size_t prefill_workspace_reserve_bytes(int R, int Hk, int max_tokens) {
+  // the largest call the split path takes: every sequence count it picks,
+  // the gated epilogue's y scratch included
+  size_t most = prefill_workspace_bytes(R, Hk, max_tokens, 1, 8, false);
+  if (max_tokens > kSplitMaxTokens) max_tokens = kSplitMaxTokens;
+  for (int nseq = 1; nseq * Hk * R <= 96 && nseq <= max_tokens; ++nseq)
+    most = std::max(most, prefill_workspace_bytes(R, Hk, max_tokens, nseq, 2, true));
+  return most;
 }
 
 // ---------------------------------------------------- no-allocation scratch --
@@ -930,12 +1231,35 @@ hipError_t noalloc_scratch(void** out) {
   return hipSuccess;
 }
 
+template <int R, int W>
+static hipError_t launch_split(const PrefillArgs& a, const Workspace& ws) {
+  const int Hv = a.Hk * R;
+  const int D = 2 * a.Hk * kDk + Hv * kDv;
+  hipLaunchKernelGGL(prefill_form_kernel<R>, dim3(rec_slots(a.total_tokens, a.nseq) * Hv), dim3(512),
+                     0, a.stream, a.cu_seqlens, a.nseq, a.Hk, a.total_tokens, ws.qn, ws.kn, ws.lg,
+                     ws.beta, ws.rec);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  uint16_t* yb = a.y ? a.y : ws.y;
+  hipLaunchKernelGGL((prefill_chunk_kernel<R, false, W>), dim3(Hv * a.nseq * (8 / W)), dim3(64 * W), 0,
+                     a.stream, a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk, a.total_tokens,
+                     ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, ws.rec, yb, nullptr, a.xstride, nullptr,
+                     0.0f, nullptr, a.status);
+  e = hipGetLastError();
+  if (e != hipSuccess || !a.out) return e;
+  const long items = (long)a.total_tokens * Hv;
+  hipLaunchKernelGGL(prefill_norm_gate_kernel, dim3((unsigned)((items + 15) / 16)), dim3(256), 0,
+                     a.stream, yb, a.mixed + D, a.xstride, a.norm_w, a.norm_eps, a.out,
+                     a.total_tokens, Hv);
+  return hipGetLastError();
+}
+
 template <int R>
 static hipError_t launch_prefill_r(const PrefillArgs& a) {
   const int Hv = a.Hk * R;
   const int D = 2 * a.Hk * kDk + Hv * kDv;
   Workspace ws;
-  carve(a.workspace, R, a.Hk, a.total_tokens, &ws);
+  carve(a.workspace, R, a.Hk, a.total_tokens, a.nseq, a.waves, a.out && !a.y, &ws);
   if (a.total_tokens > 0) {
     hipLaunchKernelGGL(prefill_qkv_kernel<R>, dim3(2 * a.Hk + Hv, (a.total_tokens + kTT - 1) / kTT),
                        dim3(256), 0, a.stream, a.conv, a.slot_ids, a.cu_seqlens, a.nseq,
@@ -950,16 +1274,18 @@ static hipError_t launch_prefill_r(const PrefillArgs& a) {
                      a.total_tokens, a.mixed, a.xstride, a.status);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (a.waves == 2) return launch_split<R, 2>(a, ws);
+  if (a.waves == 4) return launch_split<R, 4>(a, ws);
   const int units = Hv * a.nseq;
   if (a.out)
-    hipLaunchKernelGGL((prefill_chunk_kernel<R, true>), dim3(units), dim3(512), 0, a.stream,
+    hipLaunchKernelGGL((prefill_chunk_kernel<R, true, 8>), dim3(units), dim3(512), 0, a.stream,
                        a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk, a.total_tokens,
-                       ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, a.y, a.mixed + D, a.xstride,
+                       ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, nullptr, a.y, a.mixed + D, a.xstride,
                        a.norm_w, a.norm_eps, a.out, a.status);
   else
-    hipLaunchKernelGGL((prefill_chunk_kernel<R, false>), dim3(units), dim3(512), 0, a.stream,
+    hipLaunchKernelGGL((prefill_chunk_kernel<R, false, 8>), dim3(units), dim3(512), 0, a.stream,
                        a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk, a.total_tokens,
-                       ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, a.y, nullptr, a.xstride, nullptr,
+                       ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, nullptr, a.y, nullptr, a.xstride, nullptr,
                        0.0f, nullptr, a.status);
   return hipGetLastError();
 }

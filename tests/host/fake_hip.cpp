@@ -110,9 +110,15 @@ hipError_t launch_decode(const DecodeArgs&) { return hipSuccess; }
 hipError_t launch_recurrent(const RecurrentArgs&) { return hipSuccess; }
 hipError_t launch_slots(const SlotArgs&) { return hipSuccess; }
 hipError_t launch_validate(const int32_t*, int, int, uint32_t*, hipStream_t) { return hipSuccess; }
-size_t prefill_workspace_bytes(int R, int Hk, int T) {
+int prefill_chunk_waves(int, int, int, int) { return 8; }
+size_t prefill_workspace_bytes(int R, int Hk, int T, int nseq, int waves, bool y_scratch) {
   const size_t Hv = (size_t)Hk * R;
-  return (size_t)T * (2 * (size_t)Hk * kDk * 2 + Hv * kDv * 2 + Hv * 6) + 5 * 256;
+  size_t b = (size_t)T * (2 * (size_t)Hk * kDk * 2 + Hv * kDv * 2 + Hv * 6) + 5 * 256;
+  if (waves < 8) b += (size_t)(T / 64 + nseq) * Hv * 17408 + (y_scratch ? (size_t)T * Hv * kDv * 2 : 0);
+  return b;
+}
+size_t prefill_workspace_reserve_bytes(int R, int Hk, int T) {
+  return prefill_workspace_bytes(R, Hk, T, 1, 2, true);
 }
 static unsigned char g_scratch[(size_t)16 << 20];
 size_t noalloc_scratch_bytes() { return sizeof(g_scratch); }

@@ -232,3 +232,74 @@ def test_prefill_gated_matches_oracle_and_plain_prefill(gpu, Hk, Hv):
     assert worst <= OUT_REL_TOL and worst_own <= Y_TOL
     for pool in pools:
         assert pool.check() == 0
+
+
+@pytest.fixture
+def prefill_waves(monkeypatch):
+    """Force the prefill's path: GDN_PREFILL_WAVES = 8 (fused chunk kernel),
+    4 or 2 (split path: prefill_form_kernel, then 2 or 4 groups per head)."""
+    def force(w):
+        monkeypatch.setenv("GDN_PREFILL_WAVES", str(w))
+    return force
+
+
+@pytest.mark.parametrize("Hk,Hv", [(16, 32), (4, 16), (2, 8)])
+def test_prefill_split_path_matches_fused(gpu, prefill_waves, Hk, Hv):
+    """The split path (chunk records formed by prefill_form_kernel for all
+    chunks at once, then 2 or 4 groups of 4 or 2 waves per head running only
+    the state products, and for the gated call the separate epilogue) gives
+    the same bits as the fused chunk kernel: the same products in the same
+    order. Lengths cover partial chunks, an empty sequence, a chunk boundary
+    and sequences that start mid-way through a 64-token slot; states start
+    nonzero. Also the split path against the oracle."""
+    import gdn_amd
+    import torch
+    lens = [700, 0, 1, 64, 129, 333]
+    say("gdn_prefill_varlen split vs fused", f"lens={lens} Hk={Hk} Hv={Hv}")
+    rng = np.random.default_rng(560 + Hk + Hv)
+    n, D = len(lens), conv_dim(Hk, Hv)
+    p = gen_layer_params(rng, Hk, Hv)
+    st0, cs0 = gen_states(rng, n, Hk, Hv, state_std=0.05)
+    T = sum(lens)
+    mixed, ab = gen_tokens(rng, T, Hk, Hv)
+    z = O.f32_to_bf16(rng.standard_normal((T, Hv * DV)).astype(np.float32))
+    norm_w = O.f32_to_bf16((1.0 + 0.1 * rng.standard_normal(DV)).astype(np.float32))
+    qkvz = np.zeros((T, D + Hv * DV), np.uint16)
+    qkvz[:, :D] = mixed
+    qkvz[:, D:] = z
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    slots = rng.permutation(n + 2)[:n].astype(np.int32)
+    ids = _ids(slots)
+    args = (dev(p["A_log"]), dev(p["dt_bias"]), dev(p["conv_w"]))
+    res = {}
+    for w in (8, 4, 2):
+        prefill_waves(w)
+        pool = gdn_amd.Pool(1, n + 2, Hk, Hv)
+        pool.write(0, ids, dev(st0), dev(cs0))
+        y = torch.zeros((T, Hv, DV), dtype=torch.int16, device=gpu)
+        pool.prefill(0, ids, dev(cu), T, dev(mixed), dev(ab), *args, y)
+        s, c = _read(pool, 0, slots, gpu)
+        gpool = gdn_amd.Pool(1, n + 2, Hk, Hv)
+        gpool.write(0, ids, dev(st0), dev(cs0))
+        out = torch.zeros((T, Hv, DV), dtype=torch.int16, device=gpu)
+        gpool.prefill_gated(0, ids, dev(cu), T, dev(qkvz), dev(ab), *args, dev(norm_w), 1e-6, out)
+        gs, gc = _read(gpool, 0, slots, gpu)
+        assert pool.check() == 0 and gpool.check() == 0
+        assert np.array_equal(s, gs) and np.array_equal(c, gc)
+        res[w] = (host(y), s, c, host(out))
+        pool.close()
+        gpool.close()
+    for w in (4, 2):
+        for a, b, what in zip(res[8], res[w], ("y", "state", "conv", "gated out")):
+            assert np.array_equal(a, b), f"W={w}: {what} differs from the fused path"
+    y2, s2 = res[2][0], res[2][1]
+    worst_y, worst_s = 0.0, 0.0
+    for i, L in enumerate(lens):
+        a, b = cu[i], cu[i + 1]
+        yr, _, sr = O.prefill(cs0[i], st0[i], mixed[a:b], ab[a:b], p["A_log"], p["dt_bias"],
+                              p["conv_w"], Hk, Hv)
+        if L:
+            worst_y = max(worst_y, float(np.max(np.abs(O.bf16_to_f32(y2[a:b]) - O.bf16_to_f32(yr)))))
+        worst_s = max(worst_s, rel_l2(s2[i], sr))
+    say("split path |dy|", worst_y, "state relL2", worst_s)
+    assert worst_y <= Y_TOL and worst_s <= STATE_TOL
