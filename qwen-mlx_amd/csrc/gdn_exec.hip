@@ -11,6 +11,7 @@ namespace {
 
 constexpr int kRowThreads = 256;
 constexpr int kMaxHiddenPerThread = 16;  // hidden <= 4096
+constexpr int kMaxSlices = 8;            // K slices of a deferred projection (K <= 4096 in 512s)
 
 // Block-wide f32 sum (every thread gets the result); red holds 4 floats.
 __device__ __forceinline__ float block_sum(float v, float* red) {
@@ -47,11 +48,13 @@ __global__ __launch_bounds__(kRowThreads) void embed_kernel(const uint16_t* __re
 // bit-identical to the two-launch form.
 //   hn = bf16(w * bf16(h * rsqrt(mean(h^2) + eps)))
 // grid n, block 256; thread t owns the 8 elements from 8t + 2048j (16-byte
-// accesses; hidden a multiple of 8, at most 4096).
+// accesses; hidden a multiple of 8, at most 4096). NS = nslice (0: d or no
+// add), a template argument so that every slice's loads go out together.
+template <int NS>
 __global__ __launch_bounds__(kRowThreads) void add_norm_kernel(uint16_t* __restrict__ h,
                                                                const uint16_t* __restrict__ d,
                                                                const float* __restrict__ dp,
-                                                               int nslice, int npad, int hidden,
+                                                               int npad, int hidden,
                                                                const uint16_t* __restrict__ w,
                                                                float eps,
                                                                uint16_t* __restrict__ hn) {
@@ -66,15 +69,23 @@ __global__ __launch_bounds__(kRowThreads) void add_norm_kernel(uint16_t* __restr
     if (c < hidden) {
       uint4 hv = *reinterpret_cast<const uint4*>(h + row + c);
       const uint32_t* hw = reinterpret_cast<const uint32_t*>(&hv);
-      if (d != nullptr || dp != nullptr) {
+      if (NS > 0 || d != nullptr) {
         uint32_t dw[4];
-        if (dp != nullptr) {
+        if constexpr (NS > 0) {
+          // every slice's loads first (one round trip), then the adds in slice order
           const float* src = dp + (size_t)blockIdx.x * npad + c;
-          v4f t0 = *reinterpret_cast<const v4f*>(src), t1 = *reinterpret_cast<const v4f*>(src + 4);
-          for (int sl = 1; sl < nslice; ++sl) {
+          v4f p0[NS > 0 ? NS : 1], p1[NS > 0 ? NS : 1];
+#pragma unroll
+          for (int sl = 0; sl < NS; ++sl) {
             const float* ps = src + (size_t)sl * 64 * npad;
-            t0 += *reinterpret_cast<const v4f*>(ps);
-            t1 += *reinterpret_cast<const v4f*>(ps + 4);
+            p0[sl] = *reinterpret_cast<const v4f*>(ps);
+            p1[sl] = *reinterpret_cast<const v4f*>(ps + 4);
+          }
+          v4f t0 = p0[0], t1 = p1[0];
+#pragma unroll
+          for (int sl = 1; sl < NS; ++sl) {
+            t0 += p0[sl];
+            t1 += p1[sl];
           }
           dw[0] = f2bf2(t0[0], t0[1]);
           dw[1] = f2bf2(t0[2], t0[3]);
@@ -219,10 +230,22 @@ hipError_t launch_add_norm(uint16_t* h, const uint16_t* d, const QPartial* dp, i
   if (n <= 0) return hipSuccess;
   if (hidden > kRowThreads * kMaxHiddenPerThread || hidden % 8) return hipErrorInvalidValue;
   const bool part = dp != nullptr && dp->nslice > 0;
-  if (part && (n > 64 || dp->Npad < hidden || dp->Npad % 8)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(add_norm_kernel, dim3(n), dim3(kRowThreads), 0, s, h, part ? nullptr : d,
-                     part ? dp->part : nullptr, part ? dp->nslice : 0, part ? dp->Npad : 0,
-                     hidden, w, eps, hn);
+  if (part && (n > 64 || dp->Npad < hidden || dp->Npad % 8 || dp->nslice > kMaxSlices))
+    return hipErrorInvalidValue;
+  const float* pp = part ? dp->part : nullptr;
+  const uint16_t* dd = part ? nullptr : d;
+  const int np = part ? dp->Npad : 0;
+  switch (part ? dp->nslice : 0) {
+#define GDN_ADD_NORM(NS)                                                                          \
+  case NS:                                                                                        \
+    hipLaunchKernelGGL(add_norm_kernel<NS>, dim3(n), dim3(kRowThreads), 0, s, h, dd, pp, np, hidden, \
+                       w, eps, hn);                                                               \
+    break;
+    GDN_ADD_NORM(0) GDN_ADD_NORM(1) GDN_ADD_NORM(2) GDN_ADD_NORM(3) GDN_ADD_NORM(4)
+    GDN_ADD_NORM(5) GDN_ADD_NORM(6) GDN_ADD_NORM(7) GDN_ADD_NORM(8)
+#undef GDN_ADD_NORM
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

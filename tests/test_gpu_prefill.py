@@ -40,12 +40,28 @@ def _read(pool, layer, slots, gpu):
     return host(s), host(c)
 
 
-def test_prefill_mixed_batch_config3(gpu):
+@pytest.fixture
+def prefill_waves(monkeypatch):
+    """Force the prefill's path: GDN_PREFILL_WAVES = 8 (fused chunk kernel),
+    4 or 2 (split path: prefill_form_kernel, then 2 or 4 groups per head);
+    0 leaves the choice to the library."""
+    def force(w):
+        if w:
+            monkeypatch.setenv("GDN_PREFILL_WAVES", str(w))
+        else:
+            monkeypatch.delenv("GDN_PREFILL_WAVES", raising=False)
+    return force
+
+
+@pytest.mark.parametrize("waves", [0, 4])
+def test_prefill_mixed_batch_config3(gpu, prefill_waves, waves):
     """4 prefills {128, 512, 1000, 2048} (the 1000 one ends in a partial
     64-token chunk) + 28 single-token decodes in one layer, then 3 decode
-    steps for all 32 sequences from the handed-off states."""
+    steps for all 32 sequences from the handed-off states; with the library's
+    choice of schedule and with the split schedule forced."""
     import gdn_amd
     import torch
+    prefill_waves(waves)
     Hk, Hv = 16, 32
     lens = [128, 512, 1000, 2048]
     say("gdn_prefill_varlen", f"config3 lens={lens} + 28 decode, seed=500")
@@ -129,12 +145,16 @@ def test_prefill_edge_lengths_from_nonzero_state(gpu, Hk, Hv):
     assert pool.check() == 0
 
 
-def test_prefill_bad_cu_seqlens_are_flagged_and_clamped(gpu):
+@pytest.mark.parametrize("waves", [8, 2])
+def test_prefill_bad_cu_seqlens_are_flagged_and_clamped(gpu, prefill_waves, waves):
     """cu_seqlens must start at 0, not decrease and end at total_tokens; each
     violation latches GDN_FLAG_BAD_SEQLENS while the kernels clamp the bounds,
-    so nothing outside the inputs or the named slots is touched."""
+    so nothing outside the inputs or the named slots is touched. Both
+    schedules (waves = 8: fused chunk kernel; 2: chunk records, then the split
+    chunk kernel, whose record slots come from the clamped bounds)."""
     import torch
     import gdn_amd
+    prefill_waves(waves)
     Hk, Hv = 2, 4
     D = conv_dim(Hk, Hv)
     rng = np.random.default_rng(620)
@@ -232,15 +252,6 @@ def test_prefill_gated_matches_oracle_and_plain_prefill(gpu, Hk, Hv):
     assert worst <= OUT_REL_TOL and worst_own <= Y_TOL
     for pool in pools:
         assert pool.check() == 0
-
-
-@pytest.fixture
-def prefill_waves(monkeypatch):
-    """Force the prefill's path: GDN_PREFILL_WAVES = 8 (fused chunk kernel),
-    4 or 2 (split path: prefill_form_kernel, then 2 or 4 groups per head)."""
-    def force(w):
-        monkeypatch.setenv("GDN_PREFILL_WAVES", str(w))
-    return force
 
 
 @pytest.mark.parametrize("Hk,Hv", [(16, 32), (4, 16), (2, 8)])
