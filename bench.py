@@ -385,8 +385,11 @@ def exec_bench(args):
     norm-gate, 4-bit out_proj 4096 -> 2048), 4-bit lm_head 2048 -> vocab,
     greedy pick; `slots`-slot pools, B sequences prefilled with 16-token
     prompts. Random weights; tokens are the executor's own picks. Prints one
-    JSON line; the step time includes the host side (staging, launches, the
-    wait for the picked tokens)."""
+    JSON line. `value` times the double-buffered loop (gdn_exec_submit_next:
+    each step queued on the device picks of the step before while that one
+    runs, as src/bin/qwen_mlx_infer.rs:136-187 does); host_fed_ms_per_step
+    times submit + collect with the picks through the host. Both include the
+    host side (staging, launches, the wait for the picked tokens)."""
     import torch
 
     import gdn_amd
@@ -412,7 +415,7 @@ def exec_bench(args):
         NA = L // 3
         Hq, Hkv = ATT_HQ, ATT_HKV
         nqkv = Hq * 2 * ATT_HD + 2 * Hkv * ATT_HD
-        grow = P + args.warmup + args.steps + 1
+        grow = P + args.warmup + 2 * args.steps + 1
         per_seq = -(-grow // ATT_PAGE)
         kv = gdn_amd.KVCache(NA, args.slots, B * per_seq + 8, per_seq, Hq, Hkv,
                              max_step_tokens=max(B, 4 * P, 64))
@@ -450,10 +453,22 @@ def exec_bench(args):
     for _ in range(args.warmup):
         cur = ex.decode_batch(ids, cur)
     torch.cuda.synchronize()
+    # host-fed: every step's picks go to the host and come back as the next
+    # step's tokens (submit, then collect)
     t0 = time.perf_counter()
     for _ in range(args.steps):
         ex.submit_batch(ids, cur)
         cur = ex.collect_batch(B)
+    fed_elapsed = time.perf_counter() - t0
+    # chained (the double-buffered decode): each step is queued on the device
+    # picks of the one before it while that one runs, and collected after
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ex.submit_batch(ids, cur)
+    for _ in range(args.steps - 1):
+        ex.submit_next(B)
+        cur = ex.collect_batch(B)
+    cur = ex.collect_batch(B)
     elapsed = time.perf_counter() - t0
     flags = pool.check()
     if flags:
@@ -491,6 +506,10 @@ def exec_bench(args):
                                  f"{P}-token prompts",
                    "layers": L, "attention_layers": NA, "batch": B, "slots": args.slots,
                    "hidden": QL_HIDDEN, "vocab": V, "prompt_tokens": P},
+        "host_fed_ms_per_step": round(fed_elapsed / args.steps * 1e3, 4),
+        "timing": "wall clock over the steps, each queued on the previous step's device picks "
+                  "(gdn_exec_submit_next) and collected after; host_fed_ms_per_step: submit + "
+                  "collect per step, the picks through the host",
         "prefill_ms_per_sequence": {"prompt_tokens": P, "one_per_call": round(pre_one * 1e3, 3),
                                     f"{g}_per_call": round(pre_batched * 1e3, 3)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,

@@ -457,9 +457,9 @@ gdn_status gdn_exec_decode_batch(gdn_exec* exec, const uint64_t* seq_ids, const 
                                  int32_t B, uint32_t* next_tokens);
 
 /* ModelExecutor::submit_batch / collect_batch (executor.rs:31-42): queue the
- * step and return at once; collect waits for it. One batch in flight at a
- * time (a second submit before collect fails). A prefill between the two is
- * allowed (it waits for the batch).
+ * step and return at once; collect waits for it. A submit with a step still
+ * uncollected fails (gdn_exec_submit_next below may queue a second one). A
+ * prefill between the two is allowed (it waits for the batch).
  * A decode step replays HIP graphs: the first step at a batch size B
  * captures the step's launches (on a private stream) as one graph per span
  * between attention calls, which run eagerly because their launch shape
@@ -469,7 +469,20 @@ gdn_status gdn_exec_decode_batch(gdn_exec* exec, const uint64_t* seq_ids, const 
  * selects. A batch size whose capture fails runs eagerly. */
 gdn_status gdn_exec_submit_batch(gdn_exec* exec, const uint64_t* seq_ids, const uint32_t* tokens,
                                  int32_t B);
+/* Collects the oldest uncollected step (of at most two, see below). */
 gdn_status gdn_exec_collect_batch(gdn_exec* exec, uint32_t* next_tokens, int32_t B);
+
+/* The double-buffered decode of src/bin/qwen_mlx_infer.rs:136-187 (step N+1
+ * built on step N's unevaluated token array, then async-evaluated before
+ * step N is read): queue one more decode step for the sequences of the last
+ * submitted step, in the same order, each fed the token that step picks, read
+ * on the device (no host round trip). The step may be uncollected: then two
+ * are, and collect_batch returns them oldest first. B must be that step's B.
+ * Fails (queueing nothing) with nothing to follow -- no step submitted since
+ * the executor was created or since the last prefill or release -- and with
+ * two steps uncollected. Tokens are those of submit_batch fed the collected
+ * picks, bit for bit. */
+gdn_status gdn_exec_submit_next(gdn_exec* exec, int32_t B);
 
 /* The sequence is finished (its Sequence and state dropped): its slot goes
  * back to the pool. Work already queued on the slot still completes first. */

@@ -304,11 +304,17 @@ gdn_status layer_decode(gdn_layer* L, const int32_t* slot_ids, int32_t B, const 
 // pending): the f32 partials of a deferred projection with N == hidden.
 hipError_t launch_add_norm(uint16_t* h, const uint16_t* d, const QPartial* dp, int n, int hidden,
                            const uint16_t* w, float eps, uint16_t* hn, hipStream_t s);
+// h = table[tok[i]] and hn = rms_norm(h) * w in one launch (launch_embed
+// followed by launch_add_norm with no addend, bit for bit).
+hipError_t launch_embed_norm(const uint16_t* table, const int32_t* tok, int n, int vocab,
+                             int hidden, const uint16_t* w, float eps, uint16_t* h, uint16_t* hn,
+                             hipStream_t s);
 hipError_t launch_gather_rows(const uint16_t* src, const int32_t* idx, int n, int hidden,
                               uint16_t* dst, hipStream_t s);
 // Greedy pick in two passes; pv / pi hold n * argmax_chunks(vocab) partials.
+// out_host (or null): a device-mapped pinned host copy of out.
 int argmax_chunks(int vocab);
 hipError_t launch_argmax(const uint16_t* logits, int64_t ld, int n, int vocab, float* pv, int* pi,
-                         int32_t* out, hipStream_t s);
+                         int32_t* out, int32_t* out_host, hipStream_t s);
 
 }  // namespace gdn

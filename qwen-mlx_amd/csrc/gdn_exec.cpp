@@ -11,10 +11,17 @@
 // place; the attention layers' KV cache (when the stack has attention layers)
 // is keyed by the same slot ids and planned once per step (gdn_kv_step).
 // Device work of a step, in stream order:
-//   H2D of the (slot, token) block -> embedding rows -> per decoder layer:
-//   residual add + rms-norm, then gdn_layer_decode (GDN) or q|k|v projection,
-//   gdn_attn_forward and o_proj (attention) -> final add + norm -> lm_head ->
-//   argmax -> D2H of the B picked tokens, then an event that collect waits for.
+//   H2D of the (slot, token) block -> per decoder layer: residual add +
+//   rms-norm (the first one reading the embedding rows), then
+//   gdn_layer_decode (GDN) or q|k|v projection, gdn_attn_forward and o_proj
+//   (attention) -> final add + norm -> lm_head -> argmax into the token half
+//   of the device (slot, token) block and into a device-mapped pinned host
+//   slot, then an event that collect waits for.
+// Since the picks land where the next step's embedding reads its tokens, a
+// chained step (gdn_exec_submit_next) is the same device work without the H2D
+// copy, queued while the step before it still runs: the double-buffered decode
+// of src/bin/qwen_mlx_infer.rs:136-187, which builds step N+1 on step N's
+// unevaluated token array.
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -79,12 +86,12 @@ struct gdn_exec {
   int hidden = 0, vocab = 0, max_batch = 0, max_prompt = 0, rows = 0;
   int device = 0;
   hipStream_t stream = nullptr;
-  hipEvent_t done = nullptr;         // a submitted batch's tokens are in p_next
+  hipEvent_t done[2] = {nullptr, nullptr};  // step i's picks are in p_next + i * max_batch
   hipEvent_t pre_copied = nullptr;   // the prefill block has left p_pre
   // device buffers
-  int32_t* d_dec = nullptr;   // [2 * max_batch]: slots, then tokens
+  int32_t* d_dec = nullptr;   // [2 * max_batch]: slots, then tokens (a step's picks replace them)
   int32_t* d_pre = nullptr;   // prefill block, pre_words(): slots, cu, last rows, tokens
-  int32_t* d_next = nullptr;  // [max_batch] picked tokens
+  int32_t* d_next = nullptr;  // [max_batch] a prefill's picked tokens
   uint16_t* h = nullptr;      // residual stream [rows, hidden]
   uint16_t* hn = nullptr;     // normed rows fed to a layer
   uint16_t* mix = nullptr;    // layer output rows
@@ -99,12 +106,15 @@ struct gdn_exec {
   // staged while a batch is in flight does not overwrite it)
   int32_t* p_dec = nullptr;
   int32_t* p_pre = nullptr;
-  int32_t* p_next = nullptr;   // a batch's picked tokens
+  int32_t* p_next = nullptr;   // [2 * max_batch] picked tokens of the uncollected steps
+  int32_t* p_next_dev = nullptr;  // p_next as the device addresses it (written by argmax)
   int32_t* p_first = nullptr;  // a prefill's first tokens [max_batch]
   std::vector<int32_t> ones;   // ntok = 1 per decode sequence
   std::unordered_map<uint64_t, int32_t> slot_of;
-  bool inflight = false;
-  int32_t inflight_B = 0;
+  // uncollected decode steps, oldest first: pend_n of them from ring entry pend_head
+  int pend_n = 0, pend_head = 0;
+  int32_t pend_B[2] = {0, 0};
+  int32_t chain_B = 0;  // rows of the last submitted step a chained step may follow (0: none)
   int32_t logits_rows = 0;
   // Decode steps replay HIP graphs, one per batch size: the step's launches
   // between attention calls captured once as segments (an attention call's
@@ -112,7 +122,7 @@ struct gdn_exec {
   bool use_graphs = true;
   hipStream_t cap = nullptr;  // private stream the segments are captured on
   struct StepGraphs {
-    std::vector<hipGraphExec_t> seg;
+    std::vector<hipGraphExec_t> seg[2];  // per pinned pick slot the step writes
     bool failed = false;  // capture refused (e.g. a debug check syncing): run eagerly
   };
   std::unordered_map<int32_t, StepGraphs> graphs;
@@ -125,7 +135,8 @@ void exec_release(gdn_exec* x) {
   if (x->stream) (void)hipStreamSynchronize(x->stream);
   else (void)hipDeviceSynchronize();
   for (auto& kv : x->graphs)
-    for (hipGraphExec_t g : kv.second.seg) (void)hipGraphExecDestroy(g);
+    for (auto& v : kv.second.seg)
+      for (hipGraphExec_t g : v) (void)hipGraphExecDestroy(g);
   if (x->cap) (void)hipStreamDestroy(x->cap);
   for (void* p : {(void*)x->d_dec, (void*)x->d_pre, (void*)x->d_next, (void*)x->h, (void*)x->hn,
                   (void*)x->mix, (void*)x->logits, (void*)x->d_pv, (void*)x->d_pi, (void*)x->qkv,
@@ -133,7 +144,8 @@ void exec_release(gdn_exec* x) {
     if (p) (void)hipFree(p);
   for (void* p : {(void*)x->p_dec, (void*)x->p_pre, (void*)x->p_next, (void*)x->p_first})
     if (p) (void)hipHostFree(p);
-  if (x->done) (void)hipEventDestroy(x->done);
+  for (hipEvent_t ev : x->done)
+    if (ev) (void)hipEventDestroy(ev);
   if (x->pre_copied) (void)hipEventDestroy(x->pre_copied);
   for (auto& sv : x->slot_of) {
     (void)gdn_slot_free(x->pool, sv.second);
@@ -161,17 +173,32 @@ size_t pre_words(int max_batch, int max_prompt) {
   return 3 * (size_t)max_batch + 1 + (size_t)max_prompt;
 }
 
-// The model body over n rows of h that hold the embedded tokens: every
-// decoder layer with its residual seam. Prefill rows are nseq packed
+// The first seam of the stack: h = the embedding rows of toks, hn = its
+// rms-norm; later seams add the previous mixer's output first.
+gdn_status seam(gdn_exec* x, size_t p, int n, const int32_t* toks) {
+  if (p == 0)
+    HIP_TRY(gdn::launch_embed_norm(x->embed, toks, n, x->vocab, x->hidden, x->norm_w[0], x->eps,
+                                   x->h, x->hn, x->stream),
+            "embedding + norm");
+  else
+    HIP_TRY(gdn::launch_add_norm(x->h, x->mix, &x->pend, n, x->hidden, x->norm_w[p], x->eps,
+                                 x->hn, x->stream),
+            "residual add + norm");
+  x->pend = gdn::QPartial{};
+  return GDN_OK;
+}
+
+// The model body over n rows of the tokens toks: every decoder layer with its
+// residual seam (an empty stack only embeds). Prefill rows are nseq packed
 // sequences. The KV step for these rows is planned before this runs.
-gdn_status run_layers(gdn_exec* x, int n, bool prefill, int nseq = 0) {
+gdn_status run_layers(gdn_exec* x, int n, bool prefill, const int32_t* toks, int nseq = 0) {
   const int32_t* slots = prefill ? x->d_pre : x->d_dec;
   const int qw = 2 * x->Hq * 256, kw = x->Hkv * 256;  // q|gate and k widths of a qkv row
+  if (x->stack.empty())
+    HIP_TRY(gdn::launch_embed(x->embed, toks, n, x->vocab, x->hidden, x->h, x->stream),
+            "embedding");
   for (size_t p = 0; p < x->stack.size(); ++p) {
-    HIP_TRY(gdn::launch_add_norm(x->h, p == 0 ? nullptr : x->mix, p == 0 ? nullptr : &x->pend,
-                                 n, x->hidden, x->norm_w[p], x->eps, x->hn, x->stream),
-            "residual add + norm");
-    x->pend = gdn::QPartial{};
+    GDN_TRY(seam(x, p, n, toks));
     const int e = x->stack[p];
     if (e < 0) {
       const int ai = -e - 1;
@@ -206,21 +233,18 @@ gdn_status attn_call(gdn_exec* x, int ai) {
 // call): segment 0 starts with the embedding, every segment but the last ends
 // with an attention layer's q|k|v projection, the next one starts with its
 // output projection, and the last ends with lm_head and the greedy pick into
-// d_next. The segments and the attention calls between them, in order, are
-// the step.
-gdn_status decode_seg(gdn_exec* x, int B, int k) {
+// the token half of d_dec and into pinned pick slot ps. The segments and the
+// attention calls between them, in order, are the step.
+gdn_status decode_seg(gdn_exec* x, int B, int k, int ps) {
+  int32_t* const toks = x->d_dec + x->max_batch;
   int seg = 0;
-  if (k == 0)
-    HIP_TRY(gdn::launch_embed(x->embed, x->d_dec + x->max_batch, B, x->vocab, x->hidden, x->h,
-                              x->stream),
+  if (k == 0 && x->stack.empty())
+    HIP_TRY(gdn::launch_embed(x->embed, toks, B, x->vocab, x->hidden, x->h, x->stream),
             "embedding");
   for (size_t p = 0; p < x->stack.size(); ++p) {
     const int e = x->stack[p];
     if (seg == k) {
-      HIP_TRY(gdn::launch_add_norm(x->h, p == 0 ? nullptr : x->mix, p == 0 ? nullptr : &x->pend,
-                                   B, x->hidden, x->norm_w[p], x->eps, x->hn, x->stream),
-              "residual add + norm");
-      x->pend = gdn::QPartial{};
+      GDN_TRY(seam(x, p, B, toks));
       if (e >= 0) {
         GDN_TRY(gdn::layer_decode(x->layers[e], x->d_dec, B, x->hn, x->hidden, x->mix, x->hidden,
                                   x->stream, &x->pend));
@@ -244,17 +268,19 @@ gdn_status decode_seg(gdn_exec* x, int B, int k) {
           "final norm");
   x->pend = gdn::QPartial{};
   GDN_TRY(gdn_qlinear_forward(x->head, x->hn, x->hidden, B, x->logits, x->vocab, x->stream));
-  HIP_TRY(gdn::launch_argmax(x->logits, x->vocab, B, x->vocab, x->d_pv, x->d_pi, x->d_next,
-                             x->stream),
+  // the picks overwrite the step's input tokens (the embedding has read them)
+  HIP_TRY(gdn::launch_argmax(x->logits, x->vocab, B, x->vocab, x->d_pv, x->d_pi, toks,
+                             x->p_next_dev + (size_t)ps * x->max_batch, x->stream),
           "argmax");
   return GDN_OK;
 }
 
-// Captures the B-row decode step's segments into graphs (once per B). A
-// capture that fails leaves the batch size on the eager path.
+// Captures the B-row decode step's segments into graphs, one set per pinned
+// pick slot (once per B). A capture that fails leaves the batch size on the
+// eager path.
 gdn_exec::StepGraphs& step_graphs(gdn_exec* x, int B) {
   gdn_exec::StepGraphs& sg = x->graphs[B];
-  if (!sg.seg.empty() || sg.failed) return sg;
+  if (!sg.seg[0].empty() || sg.failed) return sg;
   const int nseg = (int)x->attn.size() + 1;
   if (!x->cap && hipStreamCreateWithFlags(&x->cap, hipStreamNonBlocking) != hipSuccess) {
     (void)hipGetLastError();
@@ -264,32 +290,57 @@ gdn_exec::StepGraphs& step_graphs(gdn_exec* x, int B) {
   hipStream_t saved = x->stream;
   x->stream = x->cap;
   const gdn::QPartial pend0 = x->pend;
-  for (int k = 0; k < nseg && !sg.failed; ++k) {
-    hipGraph_t g = nullptr;
-    hipGraphExec_t ge = nullptr;
-    if (hipStreamBeginCapture(x->cap, hipStreamCaptureModeThreadLocal) != hipSuccess) {
-      sg.failed = true;
-      break;
+  for (int ps = 0; ps < 2; ++ps)
+    for (int k = 0; k < nseg && !sg.failed; ++k) {
+      hipGraph_t g = nullptr;
+      hipGraphExec_t ge = nullptr;
+      if (hipStreamBeginCapture(x->cap, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+        sg.failed = true;
+        break;
+      }
+      const gdn_status st = decode_seg(x, B, k, ps);
+      const hipError_t e = hipStreamEndCapture(x->cap, &g);
+      if (st != GDN_OK || e != hipSuccess || !g ||
+          hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess)
+        sg.failed = true;
+      else
+        sg.seg[ps].push_back(ge);
+      if (g) (void)hipGraphDestroy(g);
     }
-    const gdn_status st = decode_seg(x, B, k);
-    const hipError_t e = hipStreamEndCapture(x->cap, &g);
-    if (st != GDN_OK || e != hipSuccess || !g ||
-        hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess)
-      sg.failed = true;
-    else
-      sg.seg.push_back(ge);
-    if (g) (void)hipGraphDestroy(g);
-  }
   x->stream = saved;
   x->pend = pend0;
   if (sg.failed) {
     (void)hipGetLastError();
-    for (hipGraphExec_t ge : sg.seg) (void)hipGraphExecDestroy(ge);
-    sg.seg.clear();
+    for (auto& v : sg.seg) {
+      for (hipGraphExec_t ge : v) (void)hipGraphExecDestroy(ge);
+      v.clear();
+    }
   }
   return sg;
 }
 
+// Queues the device work of a decode step over the B rows of the device
+// (slot, token) block, its picks going to the next free pinned slot, and that
+// slot's event. The attention layers' KV step is planned already.
+gdn_status queue_step(gdn_exec* x, int32_t B) {
+  const int nseg = (int)x->attn.size() + 1;
+  const int e = (x->pend_head + x->pend_n) & 1;
+  gdn_exec::StepGraphs* sg = x->use_graphs ? &step_graphs(x, B) : nullptr;
+  const bool replay = sg && !sg->seg[e].empty();
+  for (int k = 0; k < nseg; ++k) {
+    if (replay)
+      HIP_TRY(hipGraphLaunch(sg->seg[e][k], x->stream), "decode step graph");
+    else
+      GDN_TRY(decode_seg(x, B, k, e));
+    if (k + 1 < nseg) GDN_TRY(attn_call(x, k));
+  }
+  x->logits_rows = B;
+  HIP_TRY(hipEventRecord(x->done[e], x->stream), "decode step event");
+  x->pend_B[e] = B;
+  ++x->pend_n;
+  x->chain_B = B;
+  return GDN_OK;
+}
 
 }  // namespace
 
@@ -410,9 +461,12 @@ gdn_status gdn_exec_create(const gdn_exec_desc* desc, void* stream, gdn_exec** o
             hipMalloc(&x->d_pi, sizeof(int) * d.max_batch * gdn::argmax_chunks(vocab)) == hipSuccess &&
             hipHostMalloc(&x->p_dec, sizeof(int32_t) * 2 * d.max_batch, 0) == hipSuccess &&
             hipHostMalloc(&x->p_pre, sizeof(int32_t) * pre_words(d.max_batch, d.max_prompt), 0) == hipSuccess &&
-            hipHostMalloc(&x->p_next, sizeof(int32_t) * d.max_batch, 0) == hipSuccess &&
+            hipHostMalloc(&x->p_next, sizeof(int32_t) * 2 * d.max_batch,
+                          hipHostMallocMapped | hipHostMallocCoherent) == hipSuccess &&
+            hipHostGetDevicePointer((void**)&x->p_next_dev, x->p_next, 0) == hipSuccess &&
             hipHostMalloc(&x->p_first, sizeof(int32_t) * d.max_batch, 0) == hipSuccess &&
-            hipEventCreateWithFlags(&x->done, hipEventDisableTiming) == hipSuccess &&
+            hipEventCreateWithFlags(&x->done[0], hipEventDisableTiming) == hipSuccess &&
+            hipEventCreateWithFlags(&x->done[1], hipEventDisableTiming) == hipSuccess &&
             hipEventCreateWithFlags(&x->pre_copied, hipEventDisableTiming) == hipSuccess &&
             (nqkv == 0 ||
              (hipMalloc(&x->qkv, (size_t)x->rows * nqkv * sizeof(uint16_t)) == hipSuccess &&
@@ -463,6 +517,7 @@ gdn_status gdn_exec_prefill_batch(gdn_exec* x, int32_t nseq, const uint64_t* seq
       return efail(GDN_ERR_INVALID, "gdn_exec_prefill: token %d at %lld outside [0, %d)",
                    prompts[t], (long long)t, x->vocab);
   DevScope dev(x->device);
+  x->chain_B = 0;  // the next decode step takes its tokens from the host
   // The pinned block is free once the previous prefill's copy has run (a
   // prefill that failed after queueing it may not have waited).
   HIP_TRY(hipEventSynchronize(x->pre_copied), "gdn_exec_prefill");
@@ -560,9 +615,7 @@ gdn_status gdn_exec_prefill_batch(gdn_exec* x, int32_t nseq, const uint64_t* seq
   HIP_TRY_RETIRE(hipEventRecord(x->pre_copied, x->stream), "prompt copy event");
   GDN_TRY_RETIRE(gdn_slots_zero(x->pool, GDN_ALL_LAYERS, x->d_pre, nseq, x->stream));
   const int n = (int)total;
-  HIP_TRY_RETIRE(gdn::launch_embed(x->embed, d_toks, n, x->vocab, x->hidden, x->h, x->stream),
-                 "embedding");
-  GDN_TRY_RETIRE(run_layers(x, n, true, nseq));
+  GDN_TRY_RETIRE(run_layers(x, n, true, d_toks, nseq));
   // final residual add + norm of every row, then each prompt's last row
   HIP_TRY_RETIRE(gdn::launch_add_norm(x->h, x->stack.empty() ? nullptr : x->mix,
                                       x->stack.empty() ? nullptr : &x->pend, n, x->hidden,
@@ -574,7 +627,7 @@ gdn_status gdn_exec_prefill_batch(gdn_exec* x, int32_t nseq, const uint64_t* seq
   GDN_TRY_RETIRE(
       gdn_qlinear_forward(x->head, x->mix, x->hidden, nseq, x->logits, x->vocab, x->stream));
   HIP_TRY_RETIRE(gdn::launch_argmax(x->logits, x->vocab, nseq, x->vocab, x->d_pv, x->d_pi,
-                                    x->d_next, x->stream),
+                                    x->d_next, nullptr, x->stream),
                  "argmax");
   HIP_TRY_RETIRE(hipMemcpyAsync(x->p_first, x->d_next, sizeof(int32_t) * nseq,
                                 hipMemcpyDeviceToHost, x->stream),
@@ -595,7 +648,7 @@ gdn_status gdn_exec_prefill(gdn_exec* x, uint64_t seq_id, const int32_t* prompt,
 gdn_status gdn_exec_submit_batch(gdn_exec* x, const uint64_t* seq_ids, const uint32_t* tokens,
                                  int32_t B) {
   if (!x) return efail(GDN_ERR_INVALID, "gdn_exec_submit_batch: NULL executor");
-  if (x->inflight)
+  if (x->pend_n > 0)
     return efail(GDN_ERR_INVALID, "gdn_exec_submit_batch: a submitted batch is not collected yet");
   if (B < 1 || B > x->max_batch)
     return efail(GDN_ERR_INVALID, "gdn_exec_submit_batch: B = %d outside [1, %d]", B,
@@ -613,45 +666,51 @@ gdn_status gdn_exec_submit_batch(gdn_exec* x, const uint64_t* seq_ids, const uin
     if (tokens[b] >= (uint32_t)x->vocab)
       return efail(GDN_ERR_INVALID, "gdn_exec_submit_batch: token %u outside [0, %d)", tokens[b],
                    x->vocab);
-    x->p_dec[b] = it->second;
+  }
+  for (int b = 0; b < B; ++b) {
+    x->p_dec[b] = x->slot_of[seq_ids[b]];
     x->p_dec[x->max_batch + b] = (int32_t)tokens[b];
   }
   DevScope dev(x->device);
+  x->chain_B = 0;
   // plan the attention layers' KV step first: it fails (changing nothing)
   // when the cache is out of pages, before any device work is queued
   if (x->kv) GDN_TRY(gdn_kv_step(x->kv, B, x->p_dec, x->ones.data(), x->stream));
   HIP_TRY(hipMemcpyAsync(x->d_dec, x->p_dec, sizeof(int32_t) * 2 * x->max_batch,
                          hipMemcpyHostToDevice, x->stream),
           "batch copy");
-  const int nseg = (int)x->attn.size() + 1;
-  gdn_exec::StepGraphs* sg = x->use_graphs ? &step_graphs(x, B) : nullptr;
-  const bool replay = sg && !sg->seg.empty();
-  for (int k = 0; k < nseg; ++k) {
-    if (replay)
-      HIP_TRY(hipGraphLaunch(sg->seg[k], x->stream), "decode step graph");
-    else
-      GDN_TRY(decode_seg(x, B, k));
-    if (k + 1 < nseg) GDN_TRY(attn_call(x, k));
-  }
-  HIP_TRY(hipMemcpyAsync(x->p_next, x->d_next, sizeof(int32_t) * B, hipMemcpyDeviceToHost,
-                         x->stream),
-          "token copy");
-  x->logits_rows = B;
-  HIP_TRY(hipEventRecord(x->done, x->stream), "gdn_exec_submit_batch event");
-  x->inflight = true;
-  x->inflight_B = B;
-  return GDN_OK;
+  return queue_step(x, B);
+}
+
+gdn_status gdn_exec_submit_next(gdn_exec* x, int32_t B) {
+  if (!x) return efail(GDN_ERR_INVALID, "gdn_exec_submit_next: NULL executor");
+  if (x->chain_B == 0)
+    return efail(GDN_ERR_INVALID,
+                 "gdn_exec_submit_next: no decode step to follow (none submitted since the "
+                 "last prefill or release)");
+  if (B != x->chain_B)
+    return efail(GDN_ERR_INVALID, "gdn_exec_submit_next: B = %d, the step it follows has %d", B,
+                 x->chain_B);
+  if (x->pend_n == 2)
+    return efail(GDN_ERR_INVALID, "gdn_exec_submit_next: two submitted steps are not collected yet");
+  DevScope dev(x->device);
+  // the same slots (p_dec is written only by gdn_exec_submit_batch)
+  if (x->kv) GDN_TRY(gdn_kv_step(x->kv, B, x->p_dec, x->ones.data(), x->stream));
+  return queue_step(x, B);
 }
 
 gdn_status gdn_exec_collect_batch(gdn_exec* x, uint32_t* next_tokens, int32_t B) {
   if (!x || !next_tokens) return efail(GDN_ERR_INVALID, "gdn_exec_collect_batch: NULL argument");
-  if (!x->inflight) return efail(GDN_ERR_INVALID, "gdn_exec_collect_batch: nothing submitted");
-  if (B != x->inflight_B)
+  if (x->pend_n == 0) return efail(GDN_ERR_INVALID, "gdn_exec_collect_batch: nothing submitted");
+  const int e = x->pend_head;
+  if (B != x->pend_B[e])
     return efail(GDN_ERR_INVALID, "gdn_exec_collect_batch: B = %d, submitted %d", B,
-                 x->inflight_B);
-  x->inflight = false;
-  HIP_TRY(hipEventSynchronize(x->done), "gdn_exec_collect_batch");
-  for (int b = 0; b < B; ++b) next_tokens[b] = (uint32_t)x->p_next[b];
+                 x->pend_B[e]);
+  x->pend_head ^= 1;
+  --x->pend_n;
+  HIP_TRY(hipEventSynchronize(x->done[e]), "gdn_exec_collect_batch");
+  const int32_t* picks = x->p_next + (size_t)e * x->max_batch;
+  for (int b = 0; b < B; ++b) next_tokens[b] = (uint32_t)picks[b];
   return GDN_OK;
 }
 
@@ -669,6 +728,7 @@ gdn_status gdn_exec_release(gdn_exec* x, uint64_t seq_id) {
                  (unsigned long long)seq_id);
   // Work already queued on the slot runs before any later prefill re-zeroes
   // it (one stream), so the slot can be handed out again at once.
+  x->chain_B = 0;
   GDN_TRY(gdn_slot_free(x->pool, it->second));
   if (x->kv) GDN_TRY(gdn_kv_release(x->kv, it->second));
   x->slot_of.erase(it);

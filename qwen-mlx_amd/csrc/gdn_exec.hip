@@ -47,27 +47,38 @@ __global__ __launch_bounds__(kRowThreads) void embed_kernel(const uint16_t* __re
 // projection's own slice-sum kernel would have stored, so the result is
 // bit-identical to the two-launch form.
 //   hn = bf16(w * bf16(h * rsqrt(mean(h^2) + eps)))
+// With EMB the row comes from the embedding table instead (h = table[tok[i]],
+// written out; no add): the stack's first seam fused with the embedding.
 // grid n, block 256; thread t owns the 8 elements from 8t + 2048j (16-byte
 // accesses; hidden a multiple of 8, at most 4096). NS = nslice (0: d or no
-// add), a template argument so that every slice's loads go out together.
-template <int NS>
+// add), a template argument so that every slice's loads go out together; the
+// norm weights are loaded with them.
+template <int NS, bool EMB>
 __global__ __launch_bounds__(kRowThreads) void add_norm_kernel(uint16_t* __restrict__ h,
                                                                const uint16_t* __restrict__ d,
                                                                const float* __restrict__ dp,
                                                                int npad, int hidden,
                                                                const uint16_t* __restrict__ w,
                                                                float eps,
-                                                               uint16_t* __restrict__ hn) {
+                                                               uint16_t* __restrict__ hn,
+                                                               const uint16_t* __restrict__ table,
+                                                               const int32_t* __restrict__ tok,
+                                                               int vocab) {
   __shared__ float red[4];
   constexpr int J = kMaxHiddenPerThread / 8;
   const size_t row = (size_t)blockIdx.x * hidden;
+  const uint16_t* src = h + row;
+  if constexpr (EMB) src = table + (size_t)min(max(tok[blockIdx.x], 0), vocab - 1) * hidden;
   float v[J][8];
+  uint4 wv[J];
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const int c = 8 * (threadIdx.x + kRowThreads * j);
     if (c < hidden) {
-      uint4 hv = *reinterpret_cast<const uint4*>(h + row + c);
+      wv[j] = *reinterpret_cast<const uint4*>(w + c);
+      uint4 hv = *reinterpret_cast<const uint4*>(src + c);
+      if constexpr (EMB) *reinterpret_cast<uint4*>(h + row + c) = hv;
       const uint32_t* hw = reinterpret_cast<const uint32_t*>(&hv);
       if (NS > 0 || d != nullptr) {
         uint32_t dw[4];
@@ -119,8 +130,7 @@ __global__ __launch_bounds__(kRowThreads) void add_norm_kernel(uint16_t* __restr
   for (int j = 0; j < J; ++j) {
     const int c = 8 * (threadIdx.x + kRowThreads * j);
     if (c < hidden) {
-      const uint4 wv = *reinterpret_cast<const uint4*>(w + c);
-      const uint32_t* ww = reinterpret_cast<const uint32_t*>(&wv);
+      const uint32_t* ww = reinterpret_cast<const uint32_t*>(&wv[j]);
       uint32_t o[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e)
@@ -185,7 +195,8 @@ __global__ __launch_bounds__(kRowThreads) void argmax_part_kernel(const uint16_t
 
 __global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restrict__ pv,
                                                           const int* __restrict__ pi, int nchunk,
-                                                          int32_t* __restrict__ out) {
+                                                          int32_t* __restrict__ out,
+                                                          int32_t* __restrict__ out_host) {
   const int r = blockIdx.x;
   float bv = -INFINITY;
   int bi = INT_MAX;
@@ -197,7 +208,10 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restric
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1)
     better(bv, bi, __shfl_xor(bv, off, 64), __shfl_xor(bi, off, 64));
-  if (threadIdx.x == 0) out[r] = bi == INT_MAX ? 0 : bi;
+  if (threadIdx.x == 0) {
+    out[r] = bi == INT_MAX ? 0 : bi;
+    if (out_host) out_host[r] = bi == INT_MAX ? 0 : bi;
+  }
 }
 
 // dst[i, :] = src[idx[i], :] (the last row of each packed prompt). grid n,
@@ -238,8 +252,8 @@ hipError_t launch_add_norm(uint16_t* h, const uint16_t* d, const QPartial* dp, i
   switch (part ? dp->nslice : 0) {
 #define GDN_ADD_NORM(NS)                                                                          \
   case NS:                                                                                        \
-    hipLaunchKernelGGL(add_norm_kernel<NS>, dim3(n), dim3(kRowThreads), 0, s, h, dd, pp, np, hidden, \
-                       w, eps, hn);                                                               \
+    hipLaunchKernelGGL((add_norm_kernel<NS, false>), dim3(n), dim3(kRowThreads), 0, s, h, dd, pp, \
+                       np, hidden, w, eps, hn, nullptr, nullptr, 0);                              \
     break;
     GDN_ADD_NORM(0) GDN_ADD_NORM(1) GDN_ADD_NORM(2) GDN_ADD_NORM(3) GDN_ADD_NORM(4)
     GDN_ADD_NORM(5) GDN_ADD_NORM(6) GDN_ADD_NORM(7) GDN_ADD_NORM(8)
@@ -249,17 +263,27 @@ hipError_t launch_add_norm(uint16_t* h, const uint16_t* d, const QPartial* dp, i
   return hipGetLastError();
 }
 
+hipError_t launch_embed_norm(const uint16_t* table, const int32_t* tok, int n, int vocab,
+                             int hidden, const uint16_t* w, float eps, uint16_t* h, uint16_t* hn,
+                             hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  if (hidden > kRowThreads * kMaxHiddenPerThread || hidden % 8) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((add_norm_kernel<0, true>), dim3(n), dim3(kRowThreads), 0, s, h, nullptr,
+                     nullptr, 0, hidden, w, eps, hn, table, tok, vocab);
+  return hipGetLastError();
+}
+
 int argmax_chunks(int vocab) { return (vocab + kArgChunk - 1) / kArgChunk; }
 
 hipError_t launch_argmax(const uint16_t* logits, int64_t ld, int n, int vocab, float* pv, int* pi,
-                         int32_t* out, hipStream_t s) {
+                         int32_t* out, int32_t* out_host, hipStream_t s) {
   if (n <= 0) return hipSuccess;
   const int nc = argmax_chunks(vocab);
   hipLaunchKernelGGL(argmax_part_kernel, dim3(nc, n), dim3(kRowThreads), 0, s, logits, ld, vocab,
                      nc, pv, pi);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(argmax_final_kernel, dim3(n), dim3(64), 0, s, pv, pi, nc, out);
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(n), dim3(64), 0, s, pv, pi, nc, out, out_host);
   return hipGetLastError();
 }
 

@@ -70,6 +70,7 @@ SIGNATURES = {
     "gdn_exec_decode_batch": ([_VP, _VP, _VP, _I32, _VP], ctypes.c_int),
     "gdn_exec_submit_batch": ([_VP, _VP, _VP, _I32], ctypes.c_int),
     "gdn_exec_collect_batch": ([_VP, _VP, _I32], ctypes.c_int),
+    "gdn_exec_submit_next": ([_VP, _I32], ctypes.c_int),
     "gdn_exec_release": ([_VP, ctypes.c_uint64], ctypes.c_int),
     "gdn_exec_max_batch_size": ([_VP], _I32),
     "gdn_exec_supports_pipeline": ([_VP], _I32),
@@ -567,6 +568,12 @@ class Executor:
     def submit_batch(self, seq_ids, tokens) -> int:
         B, s, t = self._batch(seq_ids, tokens)
         _check(self.lib.gdn_exec_submit_batch(self.handle, s, t, B))
+        return B
+
+    def submit_next(self, B: int) -> int:
+        """Queue another step for the last submitted batch, fed its picks on the
+        device (the double-buffered decode, src/bin/qwen_mlx_infer.rs:136-187)."""
+        _check(self.lib.gdn_exec_submit_next(self.handle, B))
         return B
 
     def collect_batch(self, B: int) -> list:

@@ -30,6 +30,10 @@ hipError_t hipFree(void* ptr) {
   return hipSuccess;
 }
 hipError_t hipHostMalloc(void** ptr, size_t size, unsigned int) { return hipMalloc(ptr, size); }
+hipError_t hipHostGetDevicePointer(void** dev, void* host, unsigned int) {
+  *dev = host;
+  return hipSuccess;
+}
 hipError_t hipHostFree(void* ptr) { return hipFree(ptr); }
 hipError_t hipMemset(void* dst, int value, size_t n) {
   std::memset(dst, value, n);
@@ -147,9 +151,15 @@ hipError_t launch_gather_rows(const uint16_t*, const int32_t*, int, int, uint16_
   return hipSuccess;
 }
 int argmax_chunks(int vocab) { return (vocab + 8191) / 8192; }
+hipError_t launch_embed_norm(const uint16_t*, const int32_t*, int, int, int, const uint16_t*, float,
+                             uint16_t*, uint16_t*, hipStream_t) {
+  return gdn_fake::fail_embed ? hipErrorLaunchFailure : hipSuccess;
+}
 hipError_t launch_argmax(const uint16_t*, int64_t, int n, int, float*, int*, int32_t* out,
-                         hipStream_t) {
+                         int32_t* out_host, hipStream_t) {
   for (int i = 0; i < n; ++i) out[i] = 0;
+  if (out_host)
+    for (int i = 0; i < n; ++i) out_host[i] = 0;
   return hipSuccess;
 }
 

@@ -218,6 +218,17 @@ static int test_exec() {
   CHECK(gdn_exec_collect_batch(ex, next, 2) == GDN_ERR_INVALID);
   CHECK(gdn_exec_collect_batch(ex, next, 3) == GDN_OK);
   CHECK(gdn_exec_collect_batch(ex, next, 3) == GDN_ERR_INVALID);      // nothing submitted
+  // chained steps: the last submitted step's B, at most two uncollected, oldest first
+  CHECK(gdn_exec_submit_next(ex, 3) == GDN_OK);
+  CHECK(gdn_exec_submit_next(ex, 2) == GDN_ERR_INVALID);
+  CHECK(gdn_exec_submit_next(ex, 3) == GDN_OK);
+  CHECK(gdn_exec_submit_next(ex, 3) == GDN_ERR_INVALID);
+  CHECK(gdn_exec_submit_batch(ex, ids, toks, 3) == GDN_ERR_INVALID);
+  CHECK(gdn_exec_collect_batch(ex, next, 2) == GDN_ERR_INVALID);
+  CHECK(gdn_exec_collect_batch(ex, next, 3) == GDN_OK);
+  CHECK(gdn_exec_submit_next(ex, 3) == GDN_OK);
+  for (int k = 0; k < 2; ++k) CHECK(gdn_exec_collect_batch(ex, next, 3) == GDN_OK);
+  CHECK(gdn_exec_collect_batch(ex, next, 3) == GDN_ERR_INVALID);
   uint64_t bad[2] = {1, 9};
   CHECK(gdn_exec_decode_batch(ex, bad, toks, 2, next) == GDN_ERR_INVALID);
   uint64_t twice[2] = {1, 1};
@@ -230,6 +241,7 @@ static int test_exec() {
   CHECK(gdn_exec_seq_slot(ex, 1, &slot1) == GDN_OK);
   std::vector<int32_t> longp(256, 5);
   CHECK(gdn_exec_prefill(ex, 1, longp.data(), 256, &t) == GDN_ERR_OOM);
+  CHECK(gdn_exec_submit_next(ex, 3) == GDN_ERR_INVALID);  // a prefill ends the chain
   CHECK(gdn_exec_seq_slot(ex, 1, &slot_after) == GDN_OK && slot_after == slot1);
   int32_t fp2 = 0;
   CHECK(gdn_kv_free_pages(kv, &fp2) == GDN_OK && fp2 == free_pages);

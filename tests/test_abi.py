@@ -114,6 +114,7 @@ def test_layer_and_executor_entries_reject_null_on_host():
     assert lib.gdn_exec_decode_batch(None, ids, toks, 1, toks) == E
     assert lib.gdn_exec_submit_batch(None, ids, toks, 1) == E
     assert lib.gdn_exec_collect_batch(None, toks, 1) == E
+    assert lib.gdn_exec_submit_next(None, 1) == E
     assert lib.gdn_exec_release(None, 1) == E
     assert lib.gdn_exec_max_batch_size(None) == 0
     assert lib.gdn_exec_supports_pipeline(None) == 0

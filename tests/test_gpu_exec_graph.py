@@ -121,3 +121,52 @@ def test_graph_replay_matches_eager(gpu, hybrid):
         step([3, 4, 1], f"B3 again {k}")
     eager.close()
     graph.close()
+
+
+@pytest.mark.parametrize("hybrid", [False, True], ids=["gdn_only", "hybrid"])
+def test_chained_steps_match_host_fed(gpu, hybrid):
+    """gdn_exec_submit_next: steps fed their predecessor's picks on the device,
+    one queued ahead of each collect, against the same steps fed from the host
+    (launched kernel by kernel): the tokens of every step and the last step's
+    logits are identical, also after a batch-size change; a release ends the
+    chain."""
+    import gdn_amd
+
+    W = _weights(np.random.default_rng(2700 + hybrid), hybrid)
+    fed, chained = _executor(W, False), _executor(W, True)
+    rng = np.random.default_rng(11)
+    prompts = [list(rng.integers(0, VOCAB, n)) for n in (12, 33, 7)]
+    ids = [1, 2, 3]
+    first = fed.prefill_batch(ids, prompts)
+    assert chained.prefill_batch(ids, prompts) == first
+
+    def host_fed(ids_, cur, n):
+        out = []
+        for _ in range(n):
+            cur = fed.decode_batch(ids_, cur)
+            out.append(cur)
+        return out
+
+    def run_chained(ids_, cur, n):
+        B = len(ids_)
+        chained.submit_batch(ids_, cur)
+        out = []
+        for _ in range(n - 1):
+            chained.submit_next(B)
+            out.append(chained.collect_batch(B))
+        out.append(chained.collect_batch(B))
+        return out
+
+    ref = host_fed(ids, first, 7)
+    assert run_chained(ids, first, 7) == ref
+    assert np.array_equal(fed.logits().cpu().numpy(), chained.logits().cpu().numpy())
+    cur = dict(zip(ids, ref[-1]))
+    sub = [3, 1]
+    ref2 = host_fed(sub, [cur[i] for i in sub], 4)
+    assert run_chained(sub, [cur[i] for i in sub], 4) == ref2
+    assert np.array_equal(fed.logits().cpu().numpy(), chained.logits().cpu().numpy())
+    chained.release(2)
+    with pytest.raises(gdn_amd.GdnError):
+        chained.submit_next(2)
+    fed.close()
+    chained.close()
