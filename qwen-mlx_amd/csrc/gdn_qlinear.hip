@@ -39,6 +39,14 @@ __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+// s_waitcnt vmcnt(n) (gfx9 encoding; expcnt and lgkmcnt left at their maximum)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
 // One packed dword (nibble order k0 k2 k4 k6 k1 k3 k5 k7 of eight consecutive
 // k) -> the MFMA operand dwords (128+q_k0, 128+q_k1), ..., (128+q_k6, 128+q_k7).
 // m = 0x000F000F held in a VGPR: with one literal left, (v & m) | e selects a
@@ -289,13 +297,195 @@ __global__ __launch_bounds__(256) void qlinear_kernel(
   }
 }
 
-// s_waitcnt vmcnt(n) (gfx9 encoding; expcnt and lgkmcnt left at their maximum)
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+
+// Very wide layers at decode sizes (lm_head): the tile of qlinear_kernel (64
+// rows, every wave all of them and NW column fragments), with x copied into
+// LDS by DMA (buffer_load ... lds: wave w copies rows 4w + 16j .. +3 of the
+// stage, 1 KiB per load, lane L to byte 16 L of those rows, i.e. physical
+// chunk L % 16 of row 4w + 16j + L / 16, which holds logical chunk
+// (L % 16) ^ (row % 16) -- the swizzle of qlinear_kernel) instead of through
+// registers. That frees the staging registers, and the register budget of
+// three waves per SIMD (three 48 KiB work-groups per CU) holds without
+// spills. Each stage ends with this wave's copies of the next stage landed
+// (vmcnt 0) and a bare barrier: an LDS fence would also count the copies.
+// The two buffers are separate arrays, so that the compiler can tell copies
+// into one from reads of the other. K a multiple of 256 (whole stage pairs).
+template <int MW, int NW, int WM, int WN>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void qlinear_wide_kernel(
+    const uint16_t* __restrict__ x, int64_t xs, int M, int K, const u32x4* __restrict__ wp,
+    const uint16_t* __restrict__ sp, const uint16_t* __restrict__ bias,
+    const uint16_t* __restrict__ nsc, int N, uint16_t* __restrict__ y, int64_t ys) {
+  static_assert(WM * WN == 4, "four waves per work-group");
+  constexpr int MT = 16 * MW * WM, NT = 16 * NW * WN;
+  constexpr int XROW = kStageK * 2;  // bytes per staged x row
+  constexpr int SJ = MT / 16;        // 1 KiB copies per wave per stage
+  __shared__ __align__(16) uint8_t xl0[MT * XROW];
+  __shared__ __align__(16) uint8_t xl1[MT * XROW];
+  __shared__ float sx[kMaxGroups * MT];  // X_g[m] at sx[g*MT + m]
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int G = K >> 6, P = K >> 7;
+  const int m0 = blockIdx.y * MT;
+  const int f0 = blockIdx.x * (NT / 16) + wn * NW;  // first column fragment of the wave
+  const int r16 = lane & 15, c4 = lane >> 4;
+
+  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)x, (short)0, (int)(((int64_t)(M - 1) * xs + K) * 2), 0x00020000);
+  auto copy_x = [&](int p, uint8_t* dst) {
+#pragma unroll
+    for (int j = 0; j < SJ; ++j) {
+      const int rl = 4 * wave + 16 * j;  // first row of the load
+      const int row = rl + (lane >> 4);
+      const int r = min(m0 + row, M - 1);
+      const int lc = (lane & 15) ^ (row & 15);
+      const int voff = (int)((r * xs + p * kStageK + 8 * lc) * 2);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          xrs, (void __attribute__((address_space(3)))*)(dst + rl * XROW), 16, voff, 0, 0, 0);
+    }
+  };
+  const u32x4* wsrc[NW];
+  const u32x4* ssrc[NW];
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    wsrc[i] = wp + (int64_t)(f0 + i) * P * 64 + lane;
+    ssrc[i] = reinterpret_cast<const u32x4*>(sp) + (int64_t)(f0 + i) * P * 4 + c4;
+  }
+
+  u32x4 wc[NW], sc[NW], wnx[NW], snx[NW];
+  copy_x(0, xl0);
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    wc[i] = wsrc[i][0];
+    sc[i] = ssrc[i][0];
+  }
+  wait_vm<0>();
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup", "global");
+
+  f32x4 T[NW][MW];
+#pragma unroll
+  for (int i = 0; i < NW; ++i)
+#pragma unroll
+    for (int u = 0; u < MW; ++u) T[i][u] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  uint32_t nib = 0x000F000Fu;
+  asm volatile("" : "+v"(nib));  // keep the nibble mask in a VGPR
+
+  // stage p from buffer cur; the last stage reloads itself into the idle buffer
+  auto stage = [&](int p, uint8_t* cur, uint8_t* idle) {
+    const int pn = min(p + 1, P - 1);
+    copy_x(pn, idle);
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+      wnx[i] = wsrc[i][pn * 64];
+      snx[i] = ssrc[i][pn * 4];
+    }
+#pragma unroll
+    for (int gl = 0; gl < 2; ++gl) {
+      u32x4 X[MW][2];
+#pragma unroll
+      for (int u = 0; u < MW; ++u)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int row = (wm * MW + u) * 16 + r16;
+          const int ch = 8 * gl + 4 * h + c4;
+          X[u][h] = *reinterpret_cast<const u32x4*>(&cur[row * XROW + ((ch ^ r16) << 4)]);
+        }
+      // X_g of the row fragments this wave owns (u % WN == wn)
+#pragma unroll
+      for (int u = 0; u < MW; ++u)
+        if (u % WN == wn) {
+          f32x4 a = mfma(ones, X[u][0], zero);
+          a = mfma(ones, X[u][1], a);
+          sx[(2 * p + gl) * MT + (wm * MW + u) * 16 + r16] = a[0];  // the 4 lane groups agree
+        }
+#pragma unroll
+      for (int i = 0; i < NW; ++i) {
+        const u32x4 A0 = unpack_w(wc[i][2 * gl], nib), A1 = unpack_w(wc[i][2 * gl + 1], nib);
+        float s[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s[r] = gl ? bf_hi(sc[i][r]) : bf_lo(sc[i][r]);
+#pragma unroll
+        for (int u = 0; u < MW; ++u) {
+          f32x4 a = mfma(A0, X[u][0], zero);
+          a = mfma(A1, X[u][1], a);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) T[i][u][r] = fmaf(s[r], a[r], T[i][u][r]);
+        }
+      }
+    }
+    wait_vm<0>();  // this wave's copies of stage pn (and the next weights) have landed
+    wait_lgkm0();
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+      wc[i] = wnx[i];
+      sc[i] = snx[i];
+    }
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup", "global");
+  };
+  for (int p = 0; p < P; p += 2) {
+    stage(p, xl0, xl1);
+    stage(p + 1, xl1, xl0);
+  }
+
+  // sum_g (b_g - 128 s_g) X_g, X_g = hi + mid + lo exactly
+  for (int j = 0; j < G; j += 32) {
+    const bool gin = j + 8 * c4 < G;  // G is a multiple of 8
+#pragma unroll
+    for (int u = 0; u < MW; ++u) {
+      const int row = (wm * MW + u) * 16 + r16;
+      u32x4 hi, mid, lo;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        float v0 = 0.f, v1 = 0.f;
+        if (gin) {
+          v0 = sx[(j + 8 * c4 + e) * MT + row];
+          v1 = sx[(j + 8 * c4 + e + 1) * MT + row];
+        }
+        const uint32_t h = f2bf2(v0, v1);
+        const float r0 = v0 - bf_lo(h), r1 = v1 - bf_hi(h);
+        const uint32_t md = f2bf2(r0, r1);
+        hi[e >> 1] = h;
+        mid[e >> 1] = md;
+        lo[e >> 1] = f2bf2(r0 - bf_lo(md), r1 - bf_hi(md));
+      }
+#pragma unroll
+      for (int i = 0; i < NW; ++i) {
+        const int64_t n = (int64_t)(f0 + i) * 16 + r16;
+        u32x4 Ab = {0u, 0u, 0u, 0u}, As = {0u, 0u, 0u, 0u};
+        if (gin) {
+          Ab = *reinterpret_cast<const u32x4*>(bias + n * G + j + 8 * c4);
+          As = *reinterpret_cast<const u32x4*>(nsc + n * G + j + 8 * c4);
+        }
+        f32x4 t = T[i][u];
+        t = mfma(Ab, hi, t);
+        t = mfma(Ab, mid, t);
+        t = mfma(Ab, lo, t);
+        t = mfma(As, hi, t);
+        t = mfma(As, mid, t);
+        t = mfma(As, lo, t);
+        T[i][u] = t;
+      }
+    }
+  }
+
+#pragma unroll
+  for (int u = 0; u < MW; ++u) {
+    const int m = m0 + (wm * MW + u) * 16 + r16;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+      const int n = (f0 + i) * 16 + 4 * c4;
+      if (m < M && n < N) {
+        const f32x4 t = T[i][u];
+        *reinterpret_cast<u32x2*>(y + (int64_t)m * ys + n) = (u32x2){f2bf2(t[0], t[1]), f2bf2(t[2], t[3])};
+      }
+    }
+  }
 }
-__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
 // Decode shapes (M <= 64). A work-group owns 64 columns (four 16-wide
 // fragments) and the K slice of NW * SPW stages starting at stage
@@ -564,6 +754,16 @@ hipError_t launch_cfg(const QLinearArgs& a) {
   return hipGetLastError();
 }
 
+template <int MW, int NW, int WM, int WN>
+hipError_t launch_wide(const QLinearArgs& a) {
+  constexpr int MT = 16 * MW * WM, NT = 16 * NW * WN;
+  const dim3 grid(a.Npad / NT, (a.M + MT - 1) / MT);
+  hipLaunchKernelGGL((qlinear_wide_kernel<MW, NW, WM, WN>), grid, dim3(256), 0, a.stream, a.x, a.xs,
+                     a.M, a.K, reinterpret_cast<const u32x4*>(a.wp), a.sp, a.bias, a.nsc, a.N,
+                     a.y, a.ys);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_qlinear_pack(const QLinearPackArgs& a) {
@@ -605,10 +805,15 @@ int qlinear_decode_slices(int K, int Npad) {
 // There a 64 x 128 tile with every wave holding all 64 rows and two column
 // fragments (one row of four waves) took 140 us at M = 64, K = 2048, against
 // 196 us for the decode kernel, 159 us for the 2 x 2 wave grid and 157 us for
-// four column fragments per wave (256 VGPRs, one wave per SIMD).
+// four column fragments per wave (256 VGPRs, one wave per SIMD). The same tile
+// with x copied by DMA (qlinear_wide_kernel, three waves per SIMD) takes 128-130
+// us timed alone (142.7 for the register-staged form in the same harness;
+// 137 with DMA at two waves per SIMD; the register-staged form forced to three
+// waves spills and takes 182).
 hipError_t launch_qlinear(const QLinearArgs& a) {
   if (a.defer) *a.defer = QPartial{};
-  if (a.M <= 64 && a.Npad >= kWideDecodeN) return launch_cfg<4, 2, 1, 4>(a);
+  if (a.M <= 64 && a.Npad >= kWideDecodeN)
+    return a.K % 256 == 0 ? launch_wide<4, 2, 1, 4>(a) : launch_cfg<4, 2, 1, 4>(a);
   if (a.M <= 64) {
     const int ns = a.part ? qlinear_decode_slices(a.K, a.Npad) : 1;
     const int ksl = a.K / ns;  // K of a slice
