@@ -16,7 +16,7 @@
 //   gdn_layer_decode (GDN) or q|k|v projection, gdn_attn_forward and o_proj
 //   (attention) -> final add + norm -> lm_head -> argmax into the token half
 //   of the device (slot, token) block and into a device-mapped pinned host
-//   slot, then an event that collect waits for.
+//   slot, which collect polls (the host clears it to -1 before the step).
 // Since the picks land where the next step's embedding reads its tokens, a
 // chained step (gdn_exec_submit_next) is the same device work without the H2D
 // copy, queued while the step before it still runs: the double-buffered decode
@@ -86,7 +86,6 @@ struct gdn_exec {
   int hidden = 0, vocab = 0, max_batch = 0, max_prompt = 0, rows = 0;
   int device = 0;
   hipStream_t stream = nullptr;
-  hipEvent_t done[2] = {nullptr, nullptr};  // step i's picks are in p_next + i * max_batch
   hipEvent_t pre_copied = nullptr;   // the prefill block has left p_pre
   // device buffers
   int32_t* d_dec = nullptr;   // [2 * max_batch]: slots, then tokens (a step's picks replace them)
@@ -144,8 +143,6 @@ void exec_release(gdn_exec* x) {
     if (p) (void)hipFree(p);
   for (void* p : {(void*)x->p_dec, (void*)x->p_pre, (void*)x->p_next, (void*)x->p_first})
     if (p) (void)hipHostFree(p);
-  for (hipEvent_t ev : x->done)
-    if (ev) (void)hipEventDestroy(ev);
   if (x->pre_copied) (void)hipEventDestroy(x->pre_copied);
   for (auto& sv : x->slot_of) {
     (void)gdn_slot_free(x->pool, sv.second);
@@ -320,11 +317,14 @@ gdn_exec::StepGraphs& step_graphs(gdn_exec* x, int B) {
 }
 
 // Queues the device work of a decode step over the B rows of the device
-// (slot, token) block, its picks going to the next free pinned slot, and that
-// slot's event. The attention layers' KV step is planned already.
+// (slot, token) block, its picks going to the next free pinned slot, cleared
+// to -1 first (no device work writes it: its last step was collected). The
+// attention layers' KV step is planned already.
 gdn_status queue_step(gdn_exec* x, int32_t B) {
   const int nseg = (int)x->attn.size() + 1;
   const int e = (x->pend_head + x->pend_n) & 1;
+  volatile int32_t* slot = x->p_next + (size_t)e * x->max_batch;
+  for (int b = 0; b < B; ++b) slot[b] = -1;
   gdn_exec::StepGraphs* sg = x->use_graphs ? &step_graphs(x, B) : nullptr;
   const bool replay = sg && !sg->seg[e].empty();
   for (int k = 0; k < nseg; ++k) {
@@ -335,7 +335,6 @@ gdn_status queue_step(gdn_exec* x, int32_t B) {
     if (k + 1 < nseg) GDN_TRY(attn_call(x, k));
   }
   x->logits_rows = B;
-  HIP_TRY(hipEventRecord(x->done[e], x->stream), "decode step event");
   x->pend_B[e] = B;
   ++x->pend_n;
   x->chain_B = B;
@@ -465,8 +464,6 @@ gdn_status gdn_exec_create(const gdn_exec_desc* desc, void* stream, gdn_exec** o
                           hipHostMallocMapped | hipHostMallocCoherent) == hipSuccess &&
             hipHostGetDevicePointer((void**)&x->p_next_dev, x->p_next, 0) == hipSuccess &&
             hipHostMalloc(&x->p_first, sizeof(int32_t) * d.max_batch, 0) == hipSuccess &&
-            hipEventCreateWithFlags(&x->done[0], hipEventDisableTiming) == hipSuccess &&
-            hipEventCreateWithFlags(&x->done[1], hipEventDisableTiming) == hipSuccess &&
             hipEventCreateWithFlags(&x->pre_copied, hipEventDisableTiming) == hipSuccess &&
             (nqkv == 0 ||
              (hipMalloc(&x->qkv, (size_t)x->rows * nqkv * sizeof(uint16_t)) == hipSuccess &&
@@ -708,8 +705,24 @@ gdn_status gdn_exec_collect_batch(gdn_exec* x, uint32_t* next_tokens, int32_t B)
                  x->pend_B[e]);
   x->pend_head ^= 1;
   --x->pend_n;
-  HIP_TRY(hipEventSynchronize(x->done[e]), "gdn_exec_collect_batch");
-  const int32_t* picks = x->p_next + (size_t)e * x->max_batch;
+  // The greedy pick writes the step's tokens (>= 0) into the pinned slot, the
+  // step's last device work. Poll it; every 1024 polls ask the stream for an
+  // error, and a stream that has drained with picks missing is one.
+  volatile const int32_t* picks = x->p_next + (size_t)e * x->max_batch;
+  auto landed = [&]() {
+    for (int b = 0; b < B; ++b)
+      if (picks[b] < 0) return false;
+    return true;
+  };
+  for (uint64_t spin = 1; !landed(); ++spin) {
+    if (spin % 1024 != 0) continue;
+    const hipError_t q = hipStreamQuery(x->stream);
+    if (q == hipErrorNotReady) continue;
+    if (q != hipSuccess) return hfail(q, "gdn_exec_collect_batch");
+    if (!landed())
+      return efail(GDN_ERR_HIP, "gdn_exec_collect_batch: the step ended without its picks");
+    break;
+  }
   for (int b = 0; b < B; ++b) next_tokens[b] = (uint32_t)picks[b];
   return GDN_OK;
 }

@@ -92,6 +92,7 @@ hipError_t hipEventDestroy(hipEvent_t event) {
 }
 hipError_t hipEventRecord(hipEvent_t, hipStream_t) { return hipSuccess; }
 hipError_t hipEventSynchronize(hipEvent_t) { return hipSuccess; }
+hipError_t hipStreamQuery(hipStream_t) { return hipSuccess; }
 
 }  // extern "C"
 
