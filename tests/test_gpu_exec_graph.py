@@ -170,3 +170,30 @@ def test_chained_steps_match_host_fed(gpu, hybrid):
         chained.submit_next(2)
     fed.close()
     chained.close()
+
+
+def test_wide_head_pick_matches_host_argmax(gpu):
+    """An lm_head wide enough (131,136 columns, over 131,072; its last 128-column
+    tile part padding) to take the wide projection (x copied into LDS by DMA,
+    three waves per SIMD): every decode step's tokens equal the argmax of that
+    step's bf16 logits read back (first index of the maximum), on the
+    graph-replaying and the eager executor alike."""
+    V = 131136
+    rng = np.random.default_rng(2800)
+    W = _weights(rng, False)
+    W["embed"] = O.f32_to_bf16(rng.standard_normal((V, HIDDEN)).astype(np.float32))
+    W["head"] = quantize_w4(rng.standard_normal((V, HIDDEN)) * 0.05)
+    eager, graph = _executor(W, False), _executor(W, True)
+    ids = [1, 2, 3]
+    prompts = [list(rng.integers(0, V, n)) for n in (7, 19, 3)]
+    cur = graph.prefill_batch(ids, prompts)
+    assert eager.prefill_batch(ids, prompts) == cur
+    for step in range(4):
+        nxt = graph.decode_batch(ids, cur)
+        assert eager.decode_batch(ids, cur) == nxt, step
+        lg = O.bf16_to_f32(graph.logits().cpu().numpy().view(np.uint16))
+        assert lg.shape == (3, V)
+        assert [int(i) for i in np.argmax(lg, axis=1)] == nxt, step
+        cur = nxt
+    eager.close()
+    graph.close()
