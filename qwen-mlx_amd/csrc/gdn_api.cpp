@@ -757,7 +757,8 @@ gdn_status gdn_qlinear_forward(const gdn_qlinear* q, const uint16_t* x, int64_t 
 namespace gdn {
 
 gdn_status qlinear_forward(const gdn_qlinear* q, const uint16_t* x, int64_t x_stride, int32_t M,
-                           uint16_t* y, int64_t y_stride, void* stream, QPartial* defer) {
+                           uint16_t* y, int64_t y_stride, void* stream, QPartial* defer,
+                           const uint16_t* xsplit) {
   if (defer) *defer = QPartial{};
   if (!q) return fail(GDN_ERR_INVALID, "gdn_qlinear_forward: NULL layer");
   if (M < 0) return fail(GDN_ERR_INVALID, "gdn_qlinear_forward: M = %d < 0", M);
@@ -787,6 +788,7 @@ gdn_status qlinear_forward(const gdn_qlinear* q, const uint16_t* x, int64_t x_st
   a.ys = y_stride;
   a.part = q->part;
   a.defer = defer;
+  a.xsplit = M <= 64 ? xsplit : nullptr;
   a.stream = as_stream(stream);
   hipError_t e = gdn::launch_qlinear(a);
   if (e != hipSuccess) return hip_fail(e, "gdn_qlinear_forward launch");
@@ -908,7 +910,7 @@ gdn_status gdn_layer_decode(gdn_layer* L, const int32_t* slot_ids, int32_t B, co
 
 gdn_status gdn::layer_decode(gdn_layer* L, const int32_t* slot_ids, int32_t B, const uint16_t* x,
                              int64_t x_stride, uint16_t* out, int64_t out_stride, void* stream,
-                             QPartial* defer) {
+                             QPartial* defer, const uint16_t* xsplit) {
   if (defer) *defer = QPartial{};
   if (B == 0 && L) return GDN_OK;
   gdn_status st = layer_args(L, x, x_stride, out, out_stride, "gdn_layer_decode");
@@ -925,7 +927,7 @@ gdn_status gdn::layer_decode(gdn_layer* L, const int32_t* slot_ids, int32_t B, c
   const int64_t value = (int64_t)p->d.num_v_heads * p->d.head_v_dim;
   uint16_t* proj = static_cast<uint16_t*>(p->act);
   uint16_t* gated = proj + (size_t)B * L->proj_stride;
-  st = gdn_qlinear_forward(L->in_proj, x, x_stride, B, proj, L->proj_stride, stream);
+  st = qlinear_forward(L->in_proj, x, x_stride, B, proj, L->proj_stride, stream, nullptr, xsplit);
   if (st) return st;
   st = gdn_decode_gated(p, L->layer, slot_ids, B, proj, L->proj_stride, proj + p->D + value,
                         L->proj_stride, L->A_log, L->dt_bias, L->conv_w, L->norm_w, L->norm_eps,

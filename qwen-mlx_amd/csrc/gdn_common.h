@@ -228,6 +228,8 @@ struct QLinearArgs {
   float* part;        // K-slice partials [slices][64][Npad] f32 (decode shapes), or null
   QPartial* defer;    // non-null: a K-sliced call skips its slice sum and describes the
                       // partials here instead of writing y (nslice = 0 when y was written)
+  const uint16_t* xsplit;  // or null: x's 64-column group sums as three bf16 parts
+                           // [3][64][K/64] (launch_add_norm's), used by decode shapes
   hipStream_t stream;
 };
 
@@ -295,20 +297,24 @@ hipError_t launch_embed(const uint16_t* table, const int32_t* tok, int n, int vo
 // writes y and sets defer->nslice = 0. The partials sit in the projection's
 // own workspace until its next call.
 gdn_status qlinear_forward(const gdn_qlinear* q, const uint16_t* x, int64_t x_stride, int32_t M,
-                           uint16_t* y, int64_t y_stride, void* stream, QPartial* defer);
+                           uint16_t* y, int64_t y_stride, void* stream, QPartial* defer,
+                           const uint16_t* xsplit = nullptr);
 gdn_status layer_decode(gdn_layer* L, const int32_t* slot_ids, int32_t B, const uint16_t* x,
                         int64_t x_stride, uint16_t* out, int64_t out_stride, void* stream,
-                        QPartial* defer);
+                        QPartial* defer, const uint16_t* xsplit = nullptr);
 
 // d: bf16 rows [n, hidden], or null; dp (taken over d when it has slices
 // pending): the f32 partials of a deferred projection with N == hidden.
+// xsplit (or null; n <= 64): also the 64-column group sums of hn, each split
+// exactly into three bf16 parts, [3][64][hidden/64] (hi, mid, lo).
 hipError_t launch_add_norm(uint16_t* h, const uint16_t* d, const QPartial* dp, int n, int hidden,
-                           const uint16_t* w, float eps, uint16_t* hn, hipStream_t s);
+                           const uint16_t* w, float eps, uint16_t* hn, hipStream_t s,
+                           uint16_t* xsplit = nullptr);
 // h = table[tok[i]] and hn = rms_norm(h) * w in one launch (launch_embed
 // followed by launch_add_norm with no addend, bit for bit).
 hipError_t launch_embed_norm(const uint16_t* table, const int32_t* tok, int n, int vocab,
                              int hidden, const uint16_t* w, float eps, uint16_t* h, uint16_t* hn,
-                             hipStream_t s);
+                             hipStream_t s, uint16_t* xsplit = nullptr);
 hipError_t launch_gather_rows(const uint16_t* src, const int32_t* idx, int n, int hidden,
                               uint16_t* dst, hipStream_t s);
 // Greedy pick in two passes; pv / pi hold n * argmax_chunks(vocab) partials.

@@ -94,6 +94,7 @@ struct gdn_exec {
   uint16_t* h = nullptr;      // residual stream [rows, hidden]
   uint16_t* hn = nullptr;     // normed rows fed to a layer
   uint16_t* mix = nullptr;    // layer output rows
+  uint16_t* xsplit = nullptr; // group sums of <= 64 normed rows, split in three [3][64][hidden/64]
   gdn::QPartial pend{};       // the last mixer's output as pending K-slice partials (in place
                               // of mix rows when nslice > 0), added by the next residual seam
   uint16_t* logits = nullptr; // [max_batch, vocab]
@@ -138,7 +139,7 @@ void exec_release(gdn_exec* x) {
       for (hipGraphExec_t g : v) (void)hipGraphExecDestroy(g);
   if (x->cap) (void)hipStreamDestroy(x->cap);
   for (void* p : {(void*)x->d_dec, (void*)x->d_pre, (void*)x->d_next, (void*)x->h, (void*)x->hn,
-                  (void*)x->mix, (void*)x->logits, (void*)x->d_pv, (void*)x->d_pi, (void*)x->qkv,
+                  (void*)x->mix, (void*)x->xsplit, (void*)x->logits, (void*)x->d_pv, (void*)x->d_pi, (void*)x->qkv,
                   (void*)x->att})
     if (p) (void)hipFree(p);
   for (void* p : {(void*)x->p_dec, (void*)x->p_pre, (void*)x->p_next, (void*)x->p_first})
@@ -171,15 +172,16 @@ size_t pre_words(int max_batch, int max_prompt) {
 }
 
 // The first seam of the stack: h = the embedding rows of toks, hn = its
-// rms-norm; later seams add the previous mixer's output first.
-gdn_status seam(gdn_exec* x, size_t p, int n, const int32_t* toks) {
+// rms-norm; later seams add the previous mixer's output first. xsp (or null):
+// also hn's split group sums, for the next in_proj.
+gdn_status seam(gdn_exec* x, size_t p, int n, const int32_t* toks, uint16_t* xsp = nullptr) {
   if (p == 0)
     HIP_TRY(gdn::launch_embed_norm(x->embed, toks, n, x->vocab, x->hidden, x->norm_w[0], x->eps,
-                                   x->h, x->hn, x->stream),
+                                   x->h, x->hn, x->stream, xsp),
             "embedding + norm");
   else
     HIP_TRY(gdn::launch_add_norm(x->h, x->mix, &x->pend, n, x->hidden, x->norm_w[p], x->eps,
-                                 x->hn, x->stream),
+                                 x->hn, x->stream, xsp),
             "residual add + norm");
   x->pend = gdn::QPartial{};
   return GDN_OK;
@@ -241,10 +243,12 @@ gdn_status decode_seg(gdn_exec* x, int B, int k, int ps) {
   for (size_t p = 0; p < x->stack.size(); ++p) {
     const int e = x->stack[p];
     if (seg == k) {
-      GDN_TRY(seam(x, p, B, toks));
+      // a GDN layer's in_proj takes the group sums of its rows from the seam
+      uint16_t* const xsp = e >= 0 && B <= 64 && x->hidden % 64 == 0 ? x->xsplit : nullptr;
+      GDN_TRY(seam(x, p, B, toks, xsp));
       if (e >= 0) {
         GDN_TRY(gdn::layer_decode(x->layers[e], x->d_dec, B, x->hn, x->hidden, x->mix, x->hidden,
-                                  x->stream, &x->pend));
+                                  x->stream, &x->pend, xsp));
       } else {
         GDN_TRY(gdn_qlinear_forward(x->attn[-e - 1].qkv, x->hn, x->hidden, B, x->qkv, x->nqkv,
                                     x->stream));
@@ -455,6 +459,7 @@ gdn_status gdn_exec_create(const gdn_exec_desc* desc, void* stream, gdn_exec** o
             hipMalloc(&x->d_next, sizeof(int32_t) * d.max_batch) == hipSuccess &&
             hipMalloc(&x->h, act) == hipSuccess && hipMalloc(&x->hn, act) == hipSuccess &&
             hipMalloc(&x->mix, act) == hipSuccess &&
+            hipMalloc(&x->xsplit, (size_t)3 * 64 * (hidden / 64 + 1) * sizeof(uint16_t)) == hipSuccess &&
             hipMalloc(&x->logits, (size_t)d.max_batch * vocab * sizeof(uint16_t)) == hipSuccess &&
             hipMalloc(&x->d_pv, sizeof(float) * d.max_batch * gdn::argmax_chunks(vocab)) == hipSuccess &&
             hipMalloc(&x->d_pi, sizeof(int) * d.max_batch * gdn::argmax_chunks(vocab)) == hipSuccess &&

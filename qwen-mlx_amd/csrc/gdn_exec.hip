@@ -63,7 +63,8 @@ __global__ __launch_bounds__(kRowThreads) void add_norm_kernel(uint16_t* __restr
                                                                uint16_t* __restrict__ hn,
                                                                const uint16_t* __restrict__ table,
                                                                const int32_t* __restrict__ tok,
-                                                               int vocab) {
+                                                               int vocab,
+                                                               uint16_t* __restrict__ xsp) {
   __shared__ float red[4];
   constexpr int J = kMaxHiddenPerThread / 8;
   const size_t row = (size_t)blockIdx.x * hidden;
@@ -136,6 +137,24 @@ __global__ __launch_bounds__(kRowThreads) void add_norm_kernel(uint16_t* __restr
       for (int e = 0; e < 4; ++e)
         o[e] = f2bf2(bf_lo(ww[e]) * rbf(v[j][2 * e] * rn), bf_hi(ww[e]) * rbf(v[j][2 * e + 1] * rn));
       *reinterpret_cast<uint4*>(hn + row + c) = make_uint4(o[0], o[1], o[2], o[3]);
+      if (xsp) {  // the sum of the 64 columns of group c / 64 (8 threads), split in three
+        float gs = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gs += bf_lo(o[e]) + bf_hi(o[e]);
+        gs += __shfl_xor(gs, 1, 64);
+        gs += __shfl_xor(gs, 2, 64);
+        gs += __shfl_xor(gs, 4, 64);
+        if ((threadIdx.x & 7) == 0) {
+          const int G = hidden >> 6, g = c >> 6;
+          const uint16_t hi = f2bf(gs);
+          const float r = gs - bf2f(hi);
+          const uint16_t md = f2bf(r);
+          const size_t o0 = (size_t)blockIdx.x * G + g;
+          xsp[o0] = hi;
+          xsp[(size_t)64 * G + o0] = md;
+          xsp[(size_t)128 * G + o0] = f2bf(r - bf2f(md));
+        }
+      }
     }
   }
 }
@@ -240,12 +259,14 @@ hipError_t launch_embed(const uint16_t* table, const int32_t* tok, int n, int vo
 }
 
 hipError_t launch_add_norm(uint16_t* h, const uint16_t* d, const QPartial* dp, int n, int hidden,
-                           const uint16_t* w, float eps, uint16_t* hn, hipStream_t s) {
+                           const uint16_t* w, float eps, uint16_t* hn, hipStream_t s,
+                           uint16_t* xsplit) {
   if (n <= 0) return hipSuccess;
   if (hidden > kRowThreads * kMaxHiddenPerThread || hidden % 8) return hipErrorInvalidValue;
   const bool part = dp != nullptr && dp->nslice > 0;
   if (part && (n > 64 || dp->Npad < hidden || dp->Npad % 8 || dp->nslice > kMaxSlices))
     return hipErrorInvalidValue;
+  if (xsplit && (n > 64 || hidden % 64)) return hipErrorInvalidValue;
   const float* pp = part ? dp->part : nullptr;
   const uint16_t* dd = part ? nullptr : d;
   const int np = part ? dp->Npad : 0;
@@ -253,7 +274,7 @@ hipError_t launch_add_norm(uint16_t* h, const uint16_t* d, const QPartial* dp, i
 #define GDN_ADD_NORM(NS)                                                                          \
   case NS:                                                                                        \
     hipLaunchKernelGGL((add_norm_kernel<NS, false>), dim3(n), dim3(kRowThreads), 0, s, h, dd, pp, \
-                       np, hidden, w, eps, hn, nullptr, nullptr, 0);                              \
+                       np, hidden, w, eps, hn, nullptr, nullptr, 0, xsplit);                      \
     break;
     GDN_ADD_NORM(0) GDN_ADD_NORM(1) GDN_ADD_NORM(2) GDN_ADD_NORM(3) GDN_ADD_NORM(4)
     GDN_ADD_NORM(5) GDN_ADD_NORM(6) GDN_ADD_NORM(7) GDN_ADD_NORM(8)
@@ -265,11 +286,12 @@ hipError_t launch_add_norm(uint16_t* h, const uint16_t* d, const QPartial* dp, i
 
 hipError_t launch_embed_norm(const uint16_t* table, const int32_t* tok, int n, int vocab,
                              int hidden, const uint16_t* w, float eps, uint16_t* h, uint16_t* hn,
-                             hipStream_t s) {
+                             hipStream_t s, uint16_t* xsplit) {
   if (n <= 0) return hipSuccess;
   if (hidden > kRowThreads * kMaxHiddenPerThread || hidden % 8) return hipErrorInvalidValue;
+  if (xsplit && (n > 64 || hidden % 64)) return hipErrorInvalidValue;
   hipLaunchKernelGGL((add_norm_kernel<0, true>), dim3(n), dim3(kRowThreads), 0, s, h, nullptr,
-                     nullptr, 0, hidden, w, eps, hn, table, tok, vocab);
+                     nullptr, 0, hidden, w, eps, hn, table, tok, vocab, xsplit);
   return hipGetLastError();
 }
 

@@ -519,12 +519,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 // writes its f32 partial sums, correction of its own groups included, to
 // part[blockIdx.y][m][n] (row stride Npad), and qlinear_sum_kernel (or the
 // consumer of a deferred call) adds the slices in order and rounds once.
-template <int NW, int SPW>
+//
+// With XS the group sums come split from the caller (xsg [3][64][K/64], hi,
+// mid, lo: launch_add_norm's), one K slice only: no X_g products, no split.
+template <int NW, int SPW, bool XS>
 __global__ __launch_bounds__(64 * NW) void qlinear_decode_kernel(
     const uint16_t* __restrict__ x, int64_t xs, int M, int K, const u32x4* __restrict__ wp,
     const uint16_t* __restrict__ sp, const uint16_t* __restrict__ bias,
     const uint16_t* __restrict__ nsc, int N, uint16_t* __restrict__ y, int64_t ys,
-    float* __restrict__ part, int Npad) {
+    float* __restrict__ part, int Npad, const uint16_t* __restrict__ xsg) {
   constexpr int G = 2 * NW * SPW;  // groups of the slice
   constexpr int NG = 2 * SPW;      // groups of a wave
   constexpr int GJ = (G + 31) / 32;
@@ -598,6 +601,24 @@ __global__ __launch_bounds__(64 * NW) void qlinear_decode_kernel(
     As[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(nsc + o));
     if (!gin) Ab[j] = As[j] = (u32x4){0u, 0u, 0u, 0u};
   }
+  // the caller's split group sums of the rows of the tiles this wave finishes
+  u32x4 Xs[XS ? TPW : 1][3][GJ];
+  if constexpr (XS) {
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int u = (w * TPW + i) & 3;
+#pragma unroll
+      for (int j = 0; j < GJ; ++j) {
+        const bool gin = 32 * j + 8 * c4 < G;
+        const int64_t o = (int64_t)(16 * u + r16) * Gtot + 2 * pslice + (gin ? 32 * j + 8 * c4 : 0);
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+          Xs[i][k][j] = *reinterpret_cast<const u32x4*>(xsg + (int64_t)k * 64 * Gtot + o);
+          if (!gin) Xs[i][k][j] = (u32x4){0u, 0u, 0u, 0u};
+        }
+      }
+    }
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   // T[f][u]: D[m][n] for m = 16u + 4c4 + i, n = 16(fb+f) + r16
@@ -615,7 +636,7 @@ __global__ __launch_bounds__(64 * NW) void qlinear_decode_kernel(
 #pragma unroll
   for (int u = 0; u < 4; ++u) sel1[u] = (r16 >> 2) == u ? ones : (u32x4){0u, 0u, 0u, 0u};
   float xgv[NG];
-  constexpr int WS = 8 * SPW + 2 * GJ;  // weight, scale and correction loads
+  constexpr int WS = 8 * SPW + 2 * GJ + (XS ? 3 * TPW * GJ : 0);  // weight, scale, correction loads
 
 #pragma unroll
   for (int q = 0; q < NG; ++q) {
@@ -630,7 +651,7 @@ __global__ __launch_bounds__(64 * NW) void qlinear_decode_kernel(
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int u = 0; u < 4; ++u) X[j][u] = x_chunk(b, 16 * u + r16, 4 * j + c4);
-    {  // D[n][m] += X_g[16u + m] for n in 4u..4u+3: lane (r16, c4) gets X_g[16 c4 + r16]
+    if constexpr (!XS) {  // D[n][m] += X_g[16u + m] for n in 4u..4u+3: lane (r16, c4) gets X_g[16 c4 + r16]
       f32x4 xg = zero;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -658,8 +679,10 @@ __global__ __launch_bounds__(64 * NW) void qlinear_decode_kernel(
     __builtin_amdgcn_sched_barrier(0);
   }
 
+  if constexpr (!XS) {
 #pragma unroll
-  for (int q = 0; q < NG; ++q) sx[(2 * w * SPW + q) * 64 + 16 * c4 + r16] = xgv[q];
+    for (int q = 0; q < NG; ++q) sx[(2 * w * SPW + q) * 64 + 16 * c4 + r16] = xgv[q];
+  }
   // partial tiles into the wave's own buffers (all its copies have landed and been read)
 #pragma unroll
   for (int f = 0; f < 4; ++f)
@@ -671,7 +694,7 @@ __global__ __launch_bounds__(64 * NW) void qlinear_decode_kernel(
   lds_barrier();
 
   // X_g split once per work-group: thread -> row m, four groups
-  for (int idx = tid; idx < 64 * 8 * GJ; idx += 64 * NW) {
+  for (int idx = tid; !XS && idx < 64 * 8 * GJ; idx += 64 * NW) {
     const int m = idx & 63, g0 = 4 * (idx >> 6);
     uint32_t h2[2], m2[2], l2[2];
 #pragma unroll
@@ -689,7 +712,7 @@ __global__ __launch_bounds__(64 * NW) void qlinear_decode_kernel(
     *reinterpret_cast<u32x2*>(&xsp[1][m * XR + g0]) = (u32x2){m2[0], m2[1]};
     *reinterpret_cast<u32x2*>(&xsp[2][m * XR + g0]) = (u32x2){l2[0], l2[1]};
   }
-  lds_barrier();
+  if constexpr (!XS) lds_barrier();
 
   const int n = (fb + fo) * 16 + r16;
 #pragma unroll
@@ -703,9 +726,9 @@ __global__ __launch_bounds__(64 * NW) void qlinear_decode_kernel(
 #pragma unroll
     for (int jb = 0; jb < GJ; ++jb) {
       const int o = (16 * u + r16) * XR + 32 * jb + 8 * c4;
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(&xsp[0][o]);
-      const u32x4 mid = *reinterpret_cast<const u32x4*>(&xsp[1][o]);
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(&xsp[2][o]);
+      const u32x4 hi = XS ? Xs[XS ? i : 0][0][jb] : *reinterpret_cast<const u32x4*>(&xsp[0][o]);
+      const u32x4 mid = XS ? Xs[XS ? i : 0][1][jb] : *reinterpret_cast<const u32x4*>(&xsp[1][o]);
+      const u32x4 lo = XS ? Xs[XS ? i : 0][2][jb] : *reinterpret_cast<const u32x4*>(&xsp[2][o]);
       acc = mfma(hi, Ab[jb], acc);
       acc = mfma(mid, Ab[jb], acc);
       acc = mfma(lo, Ab[jb], acc);
@@ -819,13 +842,15 @@ hipError_t launch_qlinear(const QLinearArgs& a) {
     const int ksl = a.K / ns;  // K of a slice
     if (ksl == 512 || ksl == 1024 || ksl == 2048) {
       const u32x4* wp = reinterpret_cast<const u32x4*>(a.wp);
-      auto kern = ksl == 2048   ? qlinear_decode_kernel<8, 2>
-                  : ksl == 1024 ? qlinear_decode_kernel<8, 1>
-                                : qlinear_decode_kernel<4, 1>;
+      const bool xs = a.xsplit != nullptr && ns == 1 && ksl == 2048;
+      auto kern = xs            ? qlinear_decode_kernel<8, 2, true>
+                  : ksl == 2048 ? qlinear_decode_kernel<8, 2, false>
+                  : ksl == 1024 ? qlinear_decode_kernel<8, 1, false>
+                                : qlinear_decode_kernel<4, 1, false>;
       const int threads = ksl == 512 ? 256 : 512;
       hipLaunchKernelGGL(kern, dim3(a.Npad / 64, ns), dim3(threads), 0, a.stream, a.x, a.xs, a.M,
                          a.K, wp, a.sp, a.bias, a.nsc, a.N, a.y, a.ys, ns > 1 ? a.part : nullptr,
-                         a.Npad);
+                         a.Npad, xs ? a.xsplit : nullptr);
       hipError_t e = hipGetLastError();
       if (e != hipSuccess || ns == 1) return e;
       if (a.defer) {  // the consumer adds the slices

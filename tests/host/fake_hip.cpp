@@ -145,7 +145,7 @@ hipError_t launch_embed(const uint16_t*, const int32_t*, int, int, int, uint16_t
   return gdn_fake::fail_embed ? hipErrorLaunchFailure : hipSuccess;
 }
 hipError_t launch_add_norm(uint16_t*, const uint16_t*, const QPartial*, int, int, const uint16_t*,
-                           float, uint16_t*, hipStream_t) {
+                           float, uint16_t*, hipStream_t, uint16_t*) {
   return hipSuccess;
 }
 hipError_t launch_gather_rows(const uint16_t*, const int32_t*, int, int, uint16_t*, hipStream_t) {
@@ -153,7 +153,7 @@ hipError_t launch_gather_rows(const uint16_t*, const int32_t*, int, int, uint16_
 }
 int argmax_chunks(int vocab) { return (vocab + 8191) / 8192; }
 hipError_t launch_embed_norm(const uint16_t*, const int32_t*, int, int, int, const uint16_t*, float,
-                             uint16_t*, uint16_t*, hipStream_t) {
+                             uint16_t*, uint16_t*, hipStream_t, uint16_t*) {
   return gdn_fake::fail_embed ? hipErrorLaunchFailure : hipSuccess;
 }
 hipError_t launch_argmax(const uint16_t*, int64_t, int n, int, float*, int*, int32_t* out,
