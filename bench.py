@@ -67,6 +67,12 @@ def parse_args(argv=None):
                          "tokens per layer over --layers layers")
     ap.add_argument("--prefill-seqs", type=int, default=8)
     ap.add_argument("--prefill-len", type=int, default=16384)
+    ap.add_argument("--rmw-probe", action="store_true",
+                    help="read-modify-write probes of the decode launch's state bytes "
+                         "(lib/libgdn_probe.so) over slot placements; one JSON line")
+    ap.add_argument("--placements", default="scattered,contiguous,every8,every16",
+                    help="--rmw-probe placements (comma list of scattered, contiguous, "
+                         "every8, every16)")
     ap.add_argument("--rmw-ceiling", action="store_true",
                     help="only time a plain in-place multiply over 30 x 128 MiB buffers "
                          "(the decode's per-launch state bytes, read + write)")
@@ -130,6 +136,95 @@ def rmw_ceiling(layers: int = 30, mib: int = 128, reps: int = 8):
     nbytes = 2 * mib * (1 << 20)
     print(json.dumps({"rmw_ceiling_us_per_launch": round(us, 2), "bytes_per_launch": nbytes,
                       "GBps": round(nbytes / us * 1e-3, 1)}), flush=True)
+
+
+def placement_slots(name: str, batch: int, slots: int, seed: int):
+    """Slot ids of the batch: the workload's seeded scattered set (the same
+    draw as Workload), slots 0..B-1, or every 8th / 16th slot."""
+    import numpy as np
+    if name == "scattered":
+        return [int(s) for s in np.random.default_rng(seed).choice(slots, batch, replace=False)]
+    if name == "contiguous":
+        return list(range(batch))
+    if name.startswith("every"):
+        k = int(name[5:])
+        if k * (batch - 1) >= slots:
+            raise ValueError(f"{name}: {batch} slots do not fit in {slots}")
+        return [k * i for i in range(batch)]
+    raise ValueError(f"unknown placement {name}")
+
+
+def rmw_probe(args):
+    """Plain read-modify-write kernels (no gated delta arithmetic) over the
+    decode launch's state bytes -- B slots x 2 MiB read and written once per
+    launch, `layers` pools of `slots` slots cycled so nothing stays in the
+    256 MB memory-side cache -- in several access shapes and slot placements.
+    They show what the memory system gives each access pattern: the decode
+    kernel's own access (2 KiB-interleaved items, spaced loads), the previous
+    kernel's (contiguous 128 KiB items, loads back to back), and small units
+    swept in slot order or at random. Times from HIP events on the launch
+    stream, us per launch."""
+    import ctypes
+
+    import numpy as np
+    import torch
+    lib = ctypes.CDLL(os.path.join(ROOT, "qwen-mlx_amd", "lib", "libgdn_probe.so"))
+    fn = lib.gdn_probe_rmw
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_void_p,
+                   ctypes.POINTER(ctypes.c_int32), ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                   ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    L, S, B = args.layers, args.slots, args.batch
+    slot_bytes = HV * DV * DK * 4
+    gen = torch.Generator(device="cuda:0").manual_seed(args.seed)
+    pools = []
+    for _ in range(L):
+        t = torch.empty(S * slot_bytes // 4, dtype=torch.float32, device="cuda:0")
+        t.normal_(0.0, 0.01, generator=gen)
+        pools.append(t)
+    stream = torch.cuda.current_stream()
+    shapes = [
+        ("decode access: 2 KiB-interleaved items, XCD runs, spaced loads, 1 group/CU", 2, 0, 80 << 10, 1),
+        ("decode access, loads back to back", 2, 0, 80 << 10, 0),
+        ("previous decode access: contiguous 128 KiB items, item-first XCDs, 1 group/CU", 3, 0, 80 << 10, 0),
+        ("4 KiB units in slot order", 0, 4096, 0, 0),
+        ("16 KiB units in slot order", 0, 16384, 0, 0),
+        ("4 KiB units in random order", 1, 4096, 0, 0),
+    ]
+    rng = np.random.default_rng(args.seed + 1)
+    out = {"rmw_probe": {"layers": L, "slots": S, "batch": B,
+                         "bytes_per_launch": 2 * B * slot_bytes, "us_per_launch": {}}}
+    for pname in args.placements.split(","):
+        ids_host = placement_slots(pname, B, S, args.seed)
+        ids = torch.tensor(ids_host, dtype=torch.int32, device="cuda:0")
+        hid = (ctypes.c_int32 * B)(*ids_host)
+        res = {}
+        for label, shape, unit, lds, gap in shapes:
+            perm = None
+            if shape == 1:
+                perm = torch.from_numpy(rng.permutation(B * slot_bytes // unit).astype(np.int32)).cuda()
+
+            def launch(l):
+                rc = fn(pools[l].data_ptr(), S, slot_bytes, ids.data_ptr(), hid, B, shape, unit,
+                        perm.data_ptr() if perm is not None else None, lds, gap,
+                        stream.cuda_stream)
+                if rc != 0:
+                    raise RuntimeError(f"gdn_probe_rmw returned {rc}")
+            for l in range(L):
+                launch(l)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 4
+            e0.record()
+            for _ in range(reps):
+                for l in range(L):
+                    launch(l)
+            e1.record()
+            torch.cuda.synchronize()
+            res[label] = round(e0.elapsed_time(e1) * 1e3 / (reps * L), 2)
+        out["rmw_probe"]["us_per_launch"][pname] = res
+        print(json.dumps({pname: res}), file=sys.stderr, flush=True)
+    print(json.dumps(out), flush=True)
+    return 0
 
 
 # Algorithmic FLOPs of the chunked (WY form, chunk C) prefill per (token,
@@ -785,6 +880,31 @@ class Workload:
             self.churn()
 
 
+def profiled_traffic(args):
+    """HBM bytes per launch of the timed decode kernel from the committed PMC
+    profile (FETCH_SIZE + WRITE_SIZE passes, calibrated on a plain copy), with
+    a label saying so. The figure is used only when the profile was taken on
+    this batch size, on the ungated kernel, and from the kernel source as it is
+    now (sha256 of the source file); otherwise (None, reason)."""
+    import hashlib
+    if not os.path.exists(TRAFFIC_FILE):
+        return None, "no PMC profile"
+    with open(TRAFFIC_FILE) as f:
+        tr = json.load(f)
+    if tr.get("batch") != args.batch or args.gated:
+        return None, "PMC profile is of another batch size or of the ungated kernel"
+    src = os.path.join(ROOT, tr.get("kernel_source", ""))
+    if not os.path.isfile(src):
+        return None, "kernel source of the PMC profile not found"
+    with open(src, "rb") as f:
+        sha = hashlib.sha256(f.read()).hexdigest()[:16]
+    if sha != tr.get("kernel_source_sha256_16"):
+        return None, "kernel source changed since the PMC profile"
+    return tr.get("hbm_bytes_per_launch"), (
+        f"PMC FETCH_SIZE + WRITE_SIZE of {tr.get('kernel')} from {tr.get('source')} "
+        f"(kernel source sha256 {sha}), not measured in this run")
+
+
 def _cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -839,6 +959,8 @@ def main(argv=None):
     if args.rmw_ceiling:
         rmw_ceiling()
         return 0
+    if args.rmw_probe:
+        return rmw_probe(args)
     if args.prefill:
         return prefill_bench(args)
     if args.qlinear:
@@ -865,12 +987,7 @@ def main(argv=None):
     avg_ms = sum(a.elapsed_time(b) for a, b in ev) / (args.steps * args.layers)
     launch_bytes = args.batch * STATE_BYTES
     achieved = launch_bytes / (avg_ms * 1e-3) / 1e9
-    traffic = None
-    if os.path.exists(TRAFFIC_FILE):
-        with open(TRAFFIC_FILE) as f:
-            tr = json.load(f)
-        if tr.get("batch") == args.batch and not args.gated:
-            traffic = tr.get("hbm_bytes_per_launch")
+    traffic, traffic_source = profiled_traffic(args)
     flags = w.pool.check()
     if flags:
         print(f"pool status flags 0x{flags:x}", file=sys.stderr)
@@ -880,29 +997,32 @@ def main(argv=None):
     # measured workload, this one shows what the placement costs.
     placement = None
     if not args.no_placement:
+        # The same 64 sequences moved to other slots (contiguous, every 16th
+        # slot), same kernel, no churn: the scattered placement above is the
+        # measured workload, these show how much the placement matters.
         import torch as _t
-        w.d_ids.copy_(_t.arange(args.batch, dtype=_t.int32))
         w.args.churn_every = 0
-        for _ in range(4):
-            w.step()
-        pev = [(_t.cuda.Event(enable_timing=True), _t.cuda.Event(enable_timing=True))
-               for _ in range(args.placement_steps)]
-        _t.cuda.synchronize()
-        for i in range(args.placement_steps):
-            w.step(pev[i])
-        _t.cuda.synchronize()
-        c_ms = sum(a.elapsed_time(b) for a, b in pev) / (args.placement_steps * args.layers)
-        c_gbs = launch_bytes / (c_ms * 1e-3) / 1e9
-        placement = {
-            "scattered_slots_kernel_avg_us": round(avg_ms * 1e3, 2),
-            "contiguous_slots_kernel_avg_us": round(c_ms * 1e3, 2),
-            "contiguous_slots_frac": round(c_gbs / PEAK_HBM_GBS, 4),
-            "note": "same 64 sequences and kernel, slots 0..63, no churn, "
-                    f"{args.placement_steps} steps",
-        }
-        if w.pool.check():
-            print("pool status flags after the placement run", file=sys.stderr)
-            return 1
+        placement = {"scattered_slots_kernel_avg_us": round(avg_ms * 1e3, 2)}
+        for pname in ("contiguous", "every16"):
+            w.d_ids.copy_(_t.tensor(placement_slots(pname, args.batch, args.slots, args.seed),
+                                    dtype=_t.int32))
+            for _ in range(4):
+                w.step()
+            pev = [(_t.cuda.Event(enable_timing=True), _t.cuda.Event(enable_timing=True))
+                   for _ in range(args.placement_steps)]
+            _t.cuda.synchronize()
+            for i in range(args.placement_steps):
+                w.step(pev[i])
+            _t.cuda.synchronize()
+            p_ms = sum(a.elapsed_time(b) for a, b in pev) / (args.placement_steps * args.layers)
+            key = "contiguous_slots" if pname == "contiguous" else "every16th_slot"
+            placement[f"{key}_kernel_avg_us"] = round(p_ms * 1e3, 2)
+            placement[f"{key}_frac"] = round(launch_bytes / (p_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)
+            if w.pool.check():
+                print(f"pool status flags after the {pname} placement run", file=sys.stderr)
+                return 1
+        placement["note"] = ("same 64 sequences and kernel moved to slots 0..63 and to every 16th "
+                             f"slot, no churn, {args.placement_steps} steps each")
     prefill = None
     if not args.no_prefill:
         del w
@@ -945,6 +1065,7 @@ def main(argv=None):
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": traffic,
+            "traffic_source": traffic_source,
             "kernel": ("gdn_decode_gated (decode_kernel<2, true>)" if args.gated
                        else "gdn_decode (decode_kernel<2, false>)"),
             "kernel_avg_us": round(avg_ms * 1e3, 2),

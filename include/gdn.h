@@ -54,7 +54,12 @@
  *     num_v_heads / num_k_heads in {1, 2, 4}.
  *
  * Tensor layouts (row-major, innermost last)
- *   pool recurrent state, per layer : [num_slots, Hv, Dv, Dk] f32   (metal_gdn.rs:25-26,149)
+ *   pool recurrent state, per layer : [num_slots] slots of Hv*Dv*Dk f32. Within a slot,
+ *       row dv (Dk contiguous floats, metal_gdn.rs:25-26,149) of value head
+ *       hv = hk*R + r (R = Hv/Hk) is item row ir = r*Dv + dv of key head hk,
+ *       stored at float offset ((ir/4)*Hk + hk)*4*Dk + (ir%4)*Dk: the Hk
+ *       key heads' rows interleave in 4-row (2 KiB) pieces. gdn_slots_read /
+ *       gdn_slots_write exchange the reference's [Hv, Dv, Dk] order.
  *   pool conv state, per layer      : [num_slots, K-1, D]   bf16  (qwen3_5.rs:600-604)
  *       D = 2*Hk*Dk + Hv*Dv conv channels, channel order q | k | v (qwen3_5.rs:627-629)
  *   q, k                            : [B, T, Hk, Dk] bf16
@@ -111,7 +116,7 @@ const char* gdn_last_error(void);
 /* Library version string ("gdn <major>.<minor> gfx950"). */
 const char* gdn_version(void);
 
-/* Allocate and zero a pool: per layer, [num_slots,Hv,Dv,Dk] f32 recurrent
+/* Allocate and zero a pool: per layer, num_slots x Hv*Dv*Dk f32 recurrent
  * state and [num_slots,K-1,D] bf16 conv state (both start at +0.0). */
 gdn_status gdn_pool_create(const gdn_pool_desc* desc, gdn_pool** out);
 gdn_status gdn_pool_destroy(gdn_pool* pool);

@@ -310,6 +310,7 @@ static gdn_status slot_move(gdn_pool* pool, int32_t layer, const int32_t* slot_i
   a.n = n;
   a.num_slots = pool->d.num_slots;
   a.Hv = pool->d.num_v_heads;
+  a.R = pool->R;
   a.conv_elems = (int)pool->conv_elems;
   a.slot_ids = slot_ids;
   a.state_buf = sbuf;

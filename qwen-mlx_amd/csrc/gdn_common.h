@@ -15,6 +15,20 @@ constexpr int kDv = 128;
 constexpr int kConvK = 4;
 constexpr int kTileElems = kDv * kDk;  // one (slot, value head) recurrent tile
 
+// Recurrent state layout inside one slot (Hv * Dv * Dk floats). The R = Hv/Hk
+// value heads of key head hk form the item of hk: R * Dv rows, item row
+// ir = r * Dv + dv for hv = hk * R + r. Item rows are cut into pieces of 4 rows
+// (kPieceRows * Dk floats = 2 KiB), and piece p of key head hk is stored at
+// piece index p * Hk + hk of the slot: the Hk items of a slot interleave at
+// 2 KiB. Work-groups that stream the items of one slot side by side, in
+// piece order, then sweep one dense window of the slot instead of Hk separate
+// 128 KiB regions. A row (Dk floats) stays contiguous.
+constexpr int kPieceRows = 4;
+__host__ __device__ __forceinline__ size_t state_row_offset(int hv, int dv, int Hk, int R) {
+  const int hk = hv / R, ir = (hv - hk * R) * kDv + dv;
+  return ((size_t)(ir / kPieceRows) * Hk + hk) * (kPieceRows * kDk) + (size_t)(ir % kPieceRows) * kDk;
+}
+
 // Native 4 x f32 vector (16-byte loads/stores, usable with the nontemporal
 // builtins).
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -160,7 +174,7 @@ struct SlotArgs {
   SlotOp op;
   LayerPtrs layers;     // device arrays of per-layer base pointers
   int layer0, nlayers;  // layers [layer0, layer0 + nlayers)
-  int n, num_slots, Hv, conv_elems;  // conv_elems = (K-1)*D per slot
+  int n, num_slots, Hv, R, conv_elems;  // R = Hv/Hk; conv_elems = (K-1)*D per slot
   const int32_t* slot_ids;
   float* state_buf;     // read: destination [n,...]; write: source
   uint16_t* conv_buf;

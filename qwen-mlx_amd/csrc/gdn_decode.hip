@@ -29,24 +29,28 @@ struct TileRegs {
   v4f s[4][4];
 };
 
-__device__ __forceinline__ void tile_load(TileRegs& t, const float* __restrict__ tile, int grp,
-                                          int sub) {
+// slot: the slot's state (Hv * Dv * Dk floats); rows of value head hv are
+// addressed through state_row_offset.
+__device__ __forceinline__ void tile_load(TileRegs& t, const float* __restrict__ slot, int hv,
+                                          int Hk, int R, int grp, int sub) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 4; ++i) {
+    const float* row = slot + state_row_offset(hv, grp + 32 * i, Hk, R);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      t.s[i][j] = __builtin_nontemporal_load(
-          reinterpret_cast<const v4f*>(tile + (grp + 32 * i) * kDk + 4 * (sub + 8 * j)));
+      t.s[i][j] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(row + 4 * (sub + 8 * j)));
+  }
 }
 
-__device__ __forceinline__ void tile_store(const TileRegs& t, float* __restrict__ tile, int grp,
-                                           int sub) {
+__device__ __forceinline__ void tile_store(const TileRegs& t, float* __restrict__ slot, int hv,
+                                           int Hk, int R, int grp, int sub) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 4; ++i) {
+    float* row = slot + state_row_offset(hv, grp + 32 * i, Hk, R);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      __builtin_nontemporal_store(
-          t.s[i][j], reinterpret_cast<v4f*>(tile + (grp + 32 * i) * kDk + 4 * (sub + 8 * j)));
+      __builtin_nontemporal_store(t.s[i][j], reinterpret_cast<v4f*>(row + 4 * (sub + 8 * j)));
+  }
 }
 
 __device__ __forceinline__ float dot4(const v4f& a, const v4f& b) {
@@ -126,9 +130,9 @@ __global__ __launch_bounds__(256 * R) void recurrent_kernel(
   const int lt = tid & 255, grp = lt >> 3, sub = lt & 7;
   const int hv = hk * R + r;
   const int wave = tid >> 6, lane = tid & 63;
-  float* tile = state + ((size_t)slot * Hv + hv) * kTileElems;
+  float* sslot = state + (size_t)slot * Hv * kTileElems;
   TileRegs t;
-  tile_load(t, tile, grp, sub);
+  tile_load(t, sslot, hv, Hk, R, grp, sub);
 
   for (int tt = 0; tt < T; ++tt) {
     const size_t tok = (size_t)b * T + tt;
@@ -157,27 +161,40 @@ __global__ __launch_bounds__(256 * R) void recurrent_kernel(
       if (sub == i) yo[grp + 32 * i] = f2bf(yrow[i]);
     __syncthreads();
   }
-  tile_store(t, tile, grp, sub);
+  tile_store(t, sslot, hv, Hk, R, grp, sub);
 }
 
 // -------------------------------------------------------------------------
 // Fused S=1 decode (conv update + silu + split + q/k rms-norm + gates +
-// recurrence, optionally the RMSNormGated epilogue), one launch. grid (Hk, B),
-// block 256*R.
+// recurrence, optionally the RMSNormGated epilogue), one launch. 1D grid of
+// B * Hk groups of 256*R threads.
 //
-// The group of (b, hk) owns the q/k conv channels of hk and the v channels of
-// its R value heads, so it is the only reader and writer of those conv-state
-// bytes of the slot. Waves 4r..4r+3 hold the state tile of value head
-// hv = hk*R + r in registers, 16 float4 per thread: lanes 16q..16q+15 of wave
-// 4r+w own rows 32w + 4j + q (j = 0..7); lane l holds columns 4l..4l+3 and
-// 64+4l..64+4l+3 of each. A load instruction of a wave thus reads four rows x
-// 256 contiguous bytes, and every dk-reduction is a 16-lane DPP sum.
+// Items: item i = b*Hk + hk is (sequence b, key head hk). Its group owns the q/k
+// conv channels of hk and the v channels of its R value heads, so it is the
+// only reader and writer of those conv-state bytes of the slot.
 //
-// Load order: the conv window, weights and gate inputs first, then the state
-// rows. Waiting for the conv inputs then leaves the state loads in flight
-// (vmcnt counts in issue order) through the conv, gate and norm phases, whose
-// barriers order LDS only. Results used by only some lanes are computed by
-// all of them (or written to LDS by all of them): a value consumed only
+// XCDs: the dispatcher deals work-groups to the 8 XCDs round-robin (group L
+// runs on XCD L % 8). xcd_item gives each XCD a contiguous run of items, so the
+// Hk items of one sequence run side by side on one XCD. With the slot layout of
+// state_row_offset (the Hk items of a slot interleaved at 2 KiB) and the piece
+// order below, those groups sweep one dense window of the slot together.
+// Measured on 30 layers x 1024-slot pools, B = 64, over 8 seeded random slot
+// sets: 46.7 us per launch (max 46.8; contiguous, every 8th and every 16th
+// slot 46.7-47.9), against 50.4 us (max 51.5; every 8th slot 55.4) for
+// contiguous 64 KiB tiles with groups dealt hk-first across XCDs.
+//
+// Rows: the item's R*Dv rows are 32R pieces of 4 rows. In step j (0..7) wave w
+// of the 4R waves takes piece 4R*j + w, which lies in value head
+// r = 4R*j/32 (the same for every wave of the step). Lanes 16q..16q+15 own row q
+// of the piece; lane l holds columns 4l..4l+3 and 64+4l..64+4l+3. The two load
+// instructions of a wave's step read one contiguous 2 KiB piece, and every
+// dk-reduction is a 16-lane DPP sum.
+//
+// Load order: the conv window, weights and gate inputs first, then all 16
+// state loads. Waiting for the conv inputs then leaves the state loads in
+// flight (vmcnt counts in issue order) through the conv, gate and norm phases,
+// whose barriers order LDS only. Results used by only some lanes are computed
+// by all of them (or written to LDS by all of them): a value consumed only
 // inside a divergent branch drags its loads, and their wait, into the branch
 // behind the state loads.
 __device__ __forceinline__ float conv1(uint16_t c0, uint16_t c1, uint16_t c2, uint16_t x, uint2 w) {
@@ -188,6 +205,17 @@ __device__ __forceinline__ float conv1(uint16_t c0, uint16_t c1, uint16_t c2, ui
   return silu_bf16(rbf(acc));
 }
 
+// Gap between a wave's state load pairs in the fused decode, in units of 64
+// clocks (s_sleep).
+constexpr int kDecodeLoadGap = 4;
+
+// Item of work-group L among n: XCD x = L % 8 takes items
+// [x*(n/8) + min(x, n%8), ...) in order, one per group it receives.
+__device__ __forceinline__ int xcd_item(int L, int n) {
+  const int x = L & 7;
+  return x * (n >> 3) + min(x, n & 7) + (L >> 3);
+}
+
 template <int R, bool GATED>
 __global__ __launch_bounds__(256 * R) void decode_kernel(
     float* __restrict__ state, uint16_t* __restrict__ conv, const int32_t* __restrict__ slot_ids,
@@ -196,13 +224,14 @@ __global__ __launch_bounds__(256 * R) void decode_kernel(
     const float* __restrict__ dt_bias, const uint16_t* __restrict__ conv_w,
     uint16_t* __restrict__ y, const uint16_t* __restrict__ norm_w, float norm_eps,
     uint16_t* __restrict__ out, uint32_t* __restrict__ status) {
-  constexpr int NT = 256 * R;
+  constexpr int NT = 256 * R, NW = 4 * R;
   constexpr int NCH = (2 + R) * kDk;
   constexpr int CPT = (NCH + NT - 1) / NT;
-  const int hk = blockIdx.x, b = blockIdx.y;
+  const int item = xcd_item(blockIdx.x, gridDim.x);
+  const int b = item / Hk, hk = item - b * Hk;
   const int Hv = Hk * R;
   const int D = 2 * Hk * kDk + Hv * kDv;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l = lane & 15;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l = lane & 15, q = lane >> 4;
   const int slot = slot_ids[b];
   if ((unsigned)slot >= (unsigned)num_slots) {
     if (tid == 0) flag_status(status, GDN_FLAG_BAD_SLOT);
@@ -213,22 +242,18 @@ __global__ __launch_bounds__(256 * R) void decode_kernel(
   __shared__ float red[8];
   __shared__ float gsh[R][2];
   // RMSNormGated staging: silu(z) and w per (head, row), y of the rows, and the
-  // per-wave sums of y^2
+  // per-wave sums of y^2 of each head
   __shared__ float zsil[GATED ? R * kDv : 1], wsh[GATED ? R * kDv : 1], ysh[GATED ? R * kDv : 1];
-  __shared__ float ysq[4 * R];
+  __shared__ float ysq[R][NW];
   auto chan = [&](int c) {
     return c < kDk ? hk * kDk + c
                    : (c < 2 * kDk ? Hk * kDk + hk * kDk + (c - kDk)
                                   : 2 * Hk * kDk + hk * R * kDv + (c - 2 * kDk));
   };
-  // this thread's value head, and its rows 32wt + 4j + (lane >> 4), j = 0..7
-  const int r = wave >> 2, wt = wave & 3;
-  const int hv = hk * R + r;
-  const int row0 = 32 * wt + (lane >> 4);
   const uint16_t* xrow = mixed + (size_t)b * xstride;
 
   // 1. conv window, weights and gate inputs (and the gate's z and norm
-  // weight of the thread's rows), then the state rows
+  // weight of the thread's rows), then the state pieces
   uint16_t* cs = conv + (size_t)slot * (kConvK - 1) * D;
   uint2 cw[CPT];
   uint16_t c0[CPT], c1[CPT], c2[CPT], cx[CPT];
@@ -254,13 +279,23 @@ __global__ __launch_bounds__(256 * R) void decode_kernel(
     wr = norm_w[e & (kDv - 1)];
   }
   __builtin_amdgcn_sched_barrier(0);
-  float* tile = state + ((size_t)slot * Hv + hv) * kTileElems;
-  float* base = tile + (size_t)row0 * kDk;
+  // step j: piece NW*j + wave = value head r_of(j), row dv_of(j) of that head
+  auto r_of = [](int j) { return NW * j / 32; };
+  auto dv_of = [&](int j) { return kPieceRows * ((NW * j + wave) & 31) + q; };
+  float* sslot = state + (size_t)slot * Hv * kTileElems;
+  float* rows[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) rows[j] = sslot + state_row_offset(hk * R + r_of(j), dv_of(j), Hk, R);
+  // The wave's 8 load pairs go out kDecodeLoadGap x 64 clocks apart rather than
+  // back to back: with every group of the chip issuing its 128 KiB in one
+  // burst the launch measured 48.5 us; spaced, 46.7 us (gaps of 2-16 x 64
+  // clocks all within 0.1 us; 32 x 64 clocks: 50.9 us).
   v4f s[8][2];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    s[j][0] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(base + 4 * j * kDk + 4 * l));
-    s[j][1] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(base + 4 * j * kDk + 64 + 4 * l));
+    s[j][0] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(rows[j] + 4 * l));
+    s[j][1] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(rows[j] + 64 + 4 * l));
+    if (j < 7) __builtin_amdgcn_s_sleep(kDecodeLoadGap);
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -297,44 +332,52 @@ __global__ __launch_bounds__(256 * R) void decode_kernel(
   const v4f ka = *reinterpret_cast<const v4f*>(&qk[1][4 * l]);
   const v4f kb = *reinterpret_cast<const v4f*>(&qk[1][64 + 4 * l]);
   const float kq = sum16(dot4(ka, qa) + dot4(kb, qb));
-  const float g = gsh[r][0], beta = gsh[r][1];
-  const float* vrow = &xs[2 * kDk + r * kDv + row0];
-  const size_t yoff = ((size_t)b * Hv + hv) * kDv + row0;
+  const size_t ybase = ((size_t)b * Hv + hk * R) * kDv;
   float yb[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
+    const int r = r_of(j), dv = dv_of(j);
+    const float g = gsh[r][0], beta = gsh[r][1];
     const v4f a0 = s[j][0] * g, a1 = s[j][1] * g;
     const float kd = sum16(dot4(a0, ka) + dot4(a1, kb));
     const float qd = sum16(dot4(a0, qa) + dot4(a1, qb));
-    const float d = (vrow[4 * j] - kd) * beta;
-    __builtin_nontemporal_store(a0 + ka * d, reinterpret_cast<v4f*>(base + 4 * j * kDk + 4 * l));
-    __builtin_nontemporal_store(a1 + kb * d, reinterpret_cast<v4f*>(base + 4 * j * kDk + 64 + 4 * l));
+    const float d = (xs[2 * kDk + r * kDv + dv] - kd) * beta;
+    __builtin_nontemporal_store(a0 + ka * d, reinterpret_cast<v4f*>(rows[j] + 4 * l));
+    __builtin_nontemporal_store(a1 + kb * d, reinterpret_cast<v4f*>(rows[j] + 64 + 4 * l));
     yb[j] = rbf(qd + d * kq);
-    if (y != nullptr && l == 0) y[yoff + 4 * j] = f2bf(yb[j]);
+    if (y != nullptr && l == 0) y[ybase + r * kDv + dv] = f2bf(yb[j]);
   }
 
   // 5. RMSNormGated epilogue (qwen3_5.rs:660-665): out = silu(z) *
-  // rms_norm(y, w, eps) over each head's Dv rows. Sum of y^2 per wave (8 rows
-  // per lane group, 4 groups), y staged in LDS; after the barrier thread t < R*Dv
-  // writes row t%Dv of head hk*R + t/Dv (coalesced).
+  // rms_norm(y, w, eps) over each head's Dv rows. Per wave and head, the sum
+  // of y^2 over the wave's rows of that head (its steps, then the 4 lane
+  // groups); y staged in LDS; after the barrier thread t < R*Dv writes row
+  // t%Dv of head hk*R + t/Dv (coalesced), adding the NW wave sums in order.
   if constexpr (GATED) {
-    float ss = 0.f;
+    float ss[R];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) ss += yb[j] * yb[j];
-    ss += __shfl_xor(ss, 16, 64);
-    ss += __shfl_xor(ss, 32, 64);
-    if (lane == 0) ysq[wave] = ss;
+    for (int r = 0; r < R; ++r) ss[r] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss[r_of(j)] += yb[j] * yb[j];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      ss[r] += __shfl_xor(ss[r], 16, 64);
+      ss[r] += __shfl_xor(ss[r], 32, 64);
+      if (lane == 0) ysq[r][wave] = ss[r];
+    }
     if (l == 0) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) ysh[r * kDv + row0 + 4 * j] = yb[j];
+      for (int j = 0; j < 8; ++j) ysh[r_of(j) * kDv + dv_of(j)] = yb[j];
     }
     lds_barrier();
     if (tid < R * kDv) {
       const int h = tid / kDv;
-      const float tot = ysq[4 * h] + ysq[4 * h + 1] + ysq[4 * h + 2] + ysq[4 * h + 3];
+      float tot = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) tot += ysq[h][w];
       const float rn = 1.0f / sqrtf(tot / (float)kDv + norm_eps);
       const float normed = rbf(wsh[tid] * rbf(ysh[tid] * rn));
-      out[((size_t)b * Hv + hk * R) * kDv + tid] = f2bf(zsil[tid] * normed);
+      out[ybase + tid] = f2bf(zsil[tid] * normed);
     }
   }
 
@@ -356,21 +399,20 @@ __global__ __launch_bounds__(256 * R) void decode_kernel(
 
 // Occupancy of the fused decode at R = 2: one 512-thread group per CU. The
 // launch reserves 80 KB of LDS per group (unused; the CU has 160 KB), so a
-// second group cannot start beside the first. With 256 groups resident
-// instead of 512, half as many slots stream at once; measured on 30 layers x
-// B = 64 scattered slots: 50.2-50.9 us per launch against 50.8-51.8 us with
-// two groups per CU (the same results bit for bit).
+// second group cannot start beside the first. Measured on 30 layers x B = 64
+// over 8 random slot sets: 46.7 us per launch against 48.4 us with two groups
+// per CU (the same results bit for bit).
 constexpr size_t kDecodeOccupancyLds = 80 * 1024;
 
 template <int R>
 static hipError_t launch_decode_r(const DecodeArgs& a) {
   const size_t lds = R == 2 ? kDecodeOccupancyLds : 0;
   if (a.out)
-    hipLaunchKernelGGL((decode_kernel<R, true>), dim3(a.Hk, a.B), dim3(256 * R), lds, a.stream,
+    hipLaunchKernelGGL((decode_kernel<R, true>), dim3(a.Hk * a.B), dim3(256 * R), lds, a.stream,
                        a.state, a.conv, a.slot_ids, a.num_slots, a.Hk, a.mixed, a.xstride, a.ab, a.ab_stride,
                        a.A_log, a.dt_bias, a.conv_w, a.y, a.norm_w, a.norm_eps, a.out, a.status);
   else
-    hipLaunchKernelGGL((decode_kernel<R, false>), dim3(a.Hk, a.B), dim3(256 * R), lds, a.stream,
+    hipLaunchKernelGGL((decode_kernel<R, false>), dim3(a.Hk * a.B), dim3(256 * R), lds, a.stream,
                        a.state, a.conv, a.slot_ids, a.num_slots, a.Hk, a.mixed, a.xstride, a.ab, a.ab_stride,
                        a.A_log, a.dt_bias, a.conv_w, a.y, a.norm_w, a.norm_eps, a.out, a.status);
   return hipGetLastError();

@@ -752,7 +752,7 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
   if (en <= st) return;
   const int q0 = lane0 >> 4, c0l = lane0 & 15;
   // this lane's state column (accumulator column c = state row dv0 + c)
-  float* gstate = state + ((size_t)slot * Hv + hv) * kTileElems + (size_t)(dv0 + c0l) * kDk + 4 * q0;
+  float* gstate = state + (size_t)slot * Hv * kTileElems + state_row_offset(hv, dv0 + c0l, Hk, R) + 4 * q0;
   f32x4 acc[8];  // S^T tiles: dk rows 16a + 4q + r, state row dv0 + c
 #pragma unroll
   for (int a = 0; a < 8; ++a) acc[a] = *reinterpret_cast<const f32x4*>(gstate + 16 * a);

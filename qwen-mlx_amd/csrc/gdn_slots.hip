@@ -9,8 +9,10 @@
 // export and tests. All copies are bit-exact 16-byte moves.
 //
 // grid (Hv, n, nlayers), block 256: work-group (x, i, l) moves value-head
-// tile x of slot slot_ids[i] in layer layer0 + l (64 KiB) plus a 1/Hv share of
-// that slot's conv state.
+// tile x of slot slot_ids[i] in layer layer0 + l (64 KiB: Dv rows of 512 B,
+// placed in the slot by state_row_offset) plus a 1/Hv share of that slot's
+// conv state. Caller buffers hold the tiles in the reference's [Hv, Dv, Dk]
+// order.
 
 #include "gdn_common.h"
 
@@ -26,8 +28,13 @@ __global__ __launch_bounds__(kSlotThreads) void slots_kernel(SlotArgs a) {
     if (tid == 0 && hv == 0) flag_status(a.status, GDN_FLAG_BAD_SLOT);
     return;
   }
-  float4* tile = reinterpret_cast<float4*>(a.layers.state[layer] +
-                                           ((size_t)slot * a.Hv + hv) * kTileElems);
+  // the slot's state; row dv of value head hv at state_row_offset(hv, dv)
+  float4* sslot = reinterpret_cast<float4*>(a.layers.state[layer] + (size_t)slot * a.Hv * kTileElems);
+  const int Hk = a.Hv / a.R;
+  // 16-byte unit e of the (hv) tile in the caller's [Dv, Dk] layout
+  auto unit = [&](int e) -> float4& {
+    return sslot[(state_row_offset(hv, e / (kDk / 4), Hk, a.R) >> 2) + e % (kDk / 4)];
+  };
   // conv state of the slot as 16-byte chunks; conv_elems*2 is a multiple of 16.
   const int conv_u4 = a.conv_elems / 8;
   uint4* cs = reinterpret_cast<uint4*>(a.layers.conv[layer] + (size_t)slot * a.conv_elems);
@@ -36,13 +43,13 @@ __global__ __launch_bounds__(kSlotThreads) void slots_kernel(SlotArgs a) {
   const size_t row = (size_t)blockIdx.z * a.n + i;
   if (a.op == SlotOp::kZero) {
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int e = tid; e < kTileElems / 4; e += kSlotThreads) tile[e] = z;
+    for (int e = tid; e < kTileElems / 4; e += kSlotThreads) unit(e) = z;
     const uint4 zc = make_uint4(0u, 0u, 0u, 0u);
     for (int e = hv * kSlotThreads + tid; e < conv_u4; e += a.Hv * kSlotThreads) cs[e] = zc;
   } else if (a.op == SlotOp::kRead) {
     if (a.state_buf) {
       float4* dst = reinterpret_cast<float4*>(a.state_buf + (row * a.Hv + hv) * kTileElems);
-      for (int e = tid; e < kTileElems / 4; e += kSlotThreads) dst[e] = tile[e];
+      for (int e = tid; e < kTileElems / 4; e += kSlotThreads) dst[e] = unit(e);
     }
     if (a.conv_buf) {
       uint4* dst = reinterpret_cast<uint4*>(a.conv_buf + row * a.conv_elems);
@@ -52,7 +59,7 @@ __global__ __launch_bounds__(kSlotThreads) void slots_kernel(SlotArgs a) {
     if (a.state_buf) {
       const float4* src =
           reinterpret_cast<const float4*>(a.state_buf + (row * a.Hv + hv) * kTileElems);
-      for (int e = tid; e < kTileElems / 4; e += kSlotThreads) tile[e] = src[e];
+      for (int e = tid; e < kTileElems / 4; e += kSlotThreads) unit(e) = src[e];
     }
     if (a.conv_buf) {
       const uint4* src = reinterpret_cast<const uint4*>(a.conv_buf + row * a.conv_elems);

@@ -203,7 +203,7 @@ def _stream(stream) -> int | None:
 
 
 class Pool:
-    """Device-resident GDN state pool: per layer [slots,Hv,Dv,Dk] f32 recurrent
+    """Device-resident GDN state pool: per layer `slots` slots of Hv*Dv*Dk f32 recurrent
     state and [slots,K-1,D] bf16 conv state. Tensors passed in are torch device
     tensors; bf16 tensors may be torch.bfloat16 or int16/uint16 bit patterns."""
 
@@ -235,14 +235,16 @@ class Pool:
 
     # -- views of the pool memory (no copies) --
     def layer_views(self, layer: int):
-        """(state [S,Hv,Dv,Dk] f32, conv [S,K-1,D] int16) torch views of one layer."""
+        """(state [S, Hv*Dv*Dk] f32, conv [S,K-1,D] int16) torch views of one layer's
+        pool memory. A slot's state rows are in the pool's interleaved order (see
+        gdn.h); read() and write() give the [Hv, Dv, Dk] order."""
         import torch
         sp, cp = _VP(), _VP()
         _check(self.lib.gdn_pool_layer_state(self.handle, layer, ctypes.byref(sp), ctypes.byref(cp)))
         n_state = self.S * self.Hv * self.Dv * self.Dk
         n_conv = self.S * (self.K - 1) * self.D
         state = _wrap_device(sp.value, n_state, torch.float32, self.device).view(
-            self.S, self.Hv, self.Dv, self.Dk)
+            self.S, self.Hv * self.Dv * self.Dk)
         conv = _wrap_device(cp.value, n_conv, torch.int16, self.device).view(
             self.S, self.K - 1, self.D)
         return state, conv
