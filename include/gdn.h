@@ -308,6 +308,32 @@ gdn_status gdn_qlinear_dims(const gdn_qlinear* layer, int32_t* K, int32_t* N);
 gdn_status gdn_qlinear_forward(const gdn_qlinear* layer, const uint16_t* x, int64_t x_stride,
                                int32_t M, uint16_t* y, int64_t y_stride, void* stream);
 
+/* Residual add and RMSNorm of n hidden-size rows: the decoder layer's seam
+ * around each mixer (qwen3_5.rs:729-739: h = h + mixer output, then
+ * input_layernorm / post_attention_layernorm, an RMSNorm with weight w):
+ *   h  <- bf16(h + d)                       (skipped when d is NULL)
+ *   hn  = bf16(w * bf16(h * r)),  r = 1 / sqrt(mean(h^2) + eps)
+ * group_sums (or NULL; needs n <= 64 and hidden % 64 == 0): the 64-column
+ * group sums of each hn row, each split exactly into three bf16 parts,
+ * [3][64][hidden/64] (hi, mid, lo; rows n..63 untouched), the operand of
+ * gdn_qlinear_forward_sums. hidden <= 4096 and a multiple of 8; h, d, hn and
+ * w 16-byte aligned. Runs on the current device. */
+gdn_status gdn_add_rms_norm(uint16_t* h, const uint16_t* d, int32_t n, int32_t hidden,
+                            const uint16_t* w, float eps, uint16_t* hn, uint16_t* group_sums,
+                            void* stream);
+
+/* gdn_qlinear_forward on rows x whose 64-column group sums a producer has
+ * already formed (gdn_add_rms_norm's group_sums of the same rows). The
+ * decode-sized path (M <= 64) of a K = 2048 layer that runs whole-K tiles
+ * takes the sums instead of forming them with products of x; every other
+ * shape ignores group_sums. Same arguments and results contract as
+ * gdn_qlinear_forward otherwise. It has no counterpart in the reference,
+ * whose quantized_matmul (qwen3_5.rs:572-586) forms the sums itself; it is
+ * the fused norm-to-projection hand-off the executor uses for in_proj. */
+gdn_status gdn_qlinear_forward_sums(const gdn_qlinear* layer, const uint16_t* x, int64_t x_stride,
+                                    const uint16_t* group_sums, int32_t M, uint16_t* y,
+                                    int64_t y_stride, void* stream);
+
 /* ------------------------------------------------------------------------
  * One GatedDeltaNet layer end to end: GatedDeltaNet::forward_with_cache
  * (qwen3_5.rs:558-668) with the (conv_state, recurrent_state) cache pair
@@ -471,7 +497,10 @@ gdn_status gdn_exec_decode_batch(gdn_exec* exec, const uint64_t* seq_ids, const 
  * follows the step's KV plan; later steps at B launch the graphs on the
  * executor's stream. Results are bit-identical to launching kernel by kernel,
  * which the environment variable GDN_EXEC_GRAPHS=0 (read at gdn_exec_create)
- * selects. A batch size whose capture fails runs eagerly. */
+ * selects. A batch size whose capture fails runs eagerly. A GDN layer's
+ * in_proj takes its rows' group sums from the preceding norm
+ * (gdn_add_rms_norm / gdn_qlinear_forward_sums) when B <= 64; the variable
+ * GDN_EXEC_SPLIT_SUMS=0 (read at gdn_exec_create) makes it form them itself. */
 gdn_status gdn_exec_submit_batch(gdn_exec* exec, const uint64_t* seq_ids, const uint32_t* tokens,
                                  int32_t B);
 /* Collects the oldest uncollected step (of at most two, see below). */

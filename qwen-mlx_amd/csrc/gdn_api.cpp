@@ -753,6 +753,39 @@ gdn_status gdn_qlinear_forward(const gdn_qlinear* q, const uint16_t* x, int64_t 
   return gdn::qlinear_forward(q, x, x_stride, M, y, y_stride, stream, nullptr);
 }
 
+gdn_status gdn_qlinear_forward_sums(const gdn_qlinear* q, const uint16_t* x, int64_t x_stride,
+                                    const uint16_t* group_sums, int32_t M, uint16_t* y,
+                                    int64_t y_stride, void* stream) {
+  if (M > 0 && !group_sums)
+    return fail(GDN_ERR_INVALID, "gdn_qlinear_forward_sums: NULL group_sums");
+  if (reinterpret_cast<uintptr_t>(group_sums) % 2 != 0)
+    return fail(GDN_ERR_INVALID, "gdn_qlinear_forward_sums: group_sums must be 2-byte aligned");
+  return gdn::qlinear_forward(q, x, x_stride, M, y, y_stride, stream, nullptr, group_sums);
+}
+
+gdn_status gdn_add_rms_norm(uint16_t* h, const uint16_t* d, int32_t n, int32_t hidden,
+                            const uint16_t* w, float eps, uint16_t* hn, uint16_t* group_sums,
+                            void* stream) {
+  if (n < 0) return fail(GDN_ERR_INVALID, "gdn_add_rms_norm: n = %d < 0", n);
+  if (n == 0) return GDN_OK;
+  if (n > 65535) return fail(GDN_ERR_INVALID, "gdn_add_rms_norm: n = %d > 65535", n);
+  if (!h || !w || !hn) return fail(GDN_ERR_INVALID, "gdn_add_rms_norm: NULL tensor pointer");
+  if (hidden < 8 || hidden > 4096 || hidden % 8 != 0)
+    return fail(GDN_ERR_INVALID, "gdn_add_rms_norm: hidden = %d not a multiple of 8 in [8, 4096]",
+                hidden);
+  for (const void* p : {(const void*)h, (const void*)d, (const void*)w, (const void*)hn})
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0)
+      return fail(GDN_ERR_INVALID, "gdn_add_rms_norm: h, d, w and hn need 16-byte alignment");
+  if (!(eps >= 0.0f)) return fail(GDN_ERR_INVALID, "gdn_add_rms_norm: eps must be >= 0");
+  if (group_sums && (n > 64 || hidden % 64 != 0))
+    return fail(GDN_ERR_INVALID, "gdn_add_rms_norm: group_sums need n <= 64 (got %d) and hidden "
+                "a multiple of 64 (got %d)", n, hidden);
+  hipError_t e = gdn::launch_add_norm(h, d, nullptr, n, hidden, w, eps, hn, as_stream(stream),
+                                      group_sums);
+  if (e != hipSuccess) return hip_fail(e, "gdn_add_rms_norm launch");
+  return GDN_OK;
+}
+
 }  // extern "C"
 
 namespace gdn {

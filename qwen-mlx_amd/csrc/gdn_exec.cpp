@@ -120,6 +120,7 @@ struct gdn_exec {
   // between attention calls captured once as segments (an attention call's
   // launch shape follows the step's KV plan, so it runs eagerly between them).
   bool use_graphs = true;
+  bool use_split_sums = true;  // in_proj takes its rows' group sums from the norm
   hipStream_t cap = nullptr;  // private stream the segments are captured on
   struct StepGraphs {
     std::vector<hipGraphExec_t> seg[2];  // per pinned pick slot the step writes
@@ -244,7 +245,8 @@ gdn_status decode_seg(gdn_exec* x, int B, int k, int ps) {
     const int e = x->stack[p];
     if (seg == k) {
       // a GDN layer's in_proj takes the group sums of its rows from the seam
-      uint16_t* const xsp = e >= 0 && B <= 64 && x->hidden % 64 == 0 ? x->xsplit : nullptr;
+      uint16_t* const xsp =
+          x->use_split_sums && e >= 0 && B <= 64 && x->hidden % 64 == 0 ? x->xsplit : nullptr;
       GDN_TRY(seam(x, p, B, toks, xsp));
       if (e >= 0) {
         GDN_TRY(gdn::layer_decode(x->layers[e], x->d_dec, B, x->hn, x->hidden, x->mix, x->hidden,
@@ -452,6 +454,8 @@ gdn_status gdn_exec_create(const gdn_exec_desc* desc, void* stream, gdn_exec** o
   {
     const char* g = getenv("GDN_EXEC_GRAPHS");
     x->use_graphs = !(g && g[0] == '0' && g[1] == 0);
+    const char* ss = getenv("GDN_EXEC_SPLIT_SUMS");
+    x->use_split_sums = !(ss && ss[0] == '0' && ss[1] == 0);
   }
   const size_t act = (size_t)x->rows * hidden * sizeof(uint16_t);
   bool ok = hipMalloc(&x->d_dec, sizeof(int32_t) * 2 * d.max_batch) == hipSuccess &&

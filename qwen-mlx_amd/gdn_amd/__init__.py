@@ -62,6 +62,9 @@ SIGNATURES = {
     "gdn_qlinear_dims": ([_VP, ctypes.POINTER(_I32), ctypes.POINTER(_I32)], ctypes.c_int),
     "gdn_qlinear_forward": ([_VP, _VP, ctypes.c_int64, _I32, _VP, ctypes.c_int64, _VP],
                             ctypes.c_int),
+    "gdn_qlinear_forward_sums": ([_VP, _VP, ctypes.c_int64, _VP, _I32, _VP, ctypes.c_int64, _VP],
+                                 ctypes.c_int),
+    "gdn_add_rms_norm": ([_VP, _VP, _I32, _I32, _VP, ctypes.c_float, _VP, _VP, _VP], ctypes.c_int),
     "gdn_exec_create": ([_VP, _VP, ctypes.POINTER(_VP)], ctypes.c_int),
     "gdn_exec_destroy": ([_VP], ctypes.c_int),
     "gdn_exec_prefill": ([_VP, ctypes.c_uint64, _VP, _I32, ctypes.POINTER(ctypes.c_uint32)],
@@ -202,6 +205,43 @@ def _stream(stream) -> int | None:
     return stream.cuda_stream
 
 
+class _Dependents:
+    """Destroy order of library objects whose C destroy touches another object.
+
+    An executor's gdn_exec_destroy returns its sequences' slots to the pool and
+    their pages to the KV cache, so the pool and the cache must outlive it.
+    Python finalizes objects in any order when they die together (a failed
+    test's frame, interpreter exit), so the pool and the cache destroy their
+    registered dependents first. The list holds its dependents (objects with
+    `_destroy()`) strongly: a live executor and its pool form a reference cycle
+    that the garbage collector frees as one unit, and whichever of the two is
+    finalized first destroys the executor before the pool. A closed executor
+    leaves the list, so it no longer keeps the pool alive."""
+
+    def __init__(self):
+        self.items = []
+
+    def add(self, obj):
+        self.items.append(obj)
+
+    def remove(self, obj):
+        self.items = [o for o in self.items if o is not obj]
+
+    def close_all(self):
+        items, self.items = self.items, []
+        for obj in reversed(items):
+            obj._destroy()
+
+
+def add_rms_norm(h, d, w, eps, hn, group_sums=None, stream=None):
+    """h <- bf16(h + d) (d may be None), hn = rms_norm(h) * w over the rows of
+    h [n, hidden]; group_sums [3, 64, hidden/64] (or None) receives the split
+    64-column group sums of hn."""
+    n, hidden = h.shape
+    _check(load().gdn_add_rms_norm(_ptr(h), _ptr(d), n, hidden, _ptr(w), float(eps), _ptr(hn),
+                                   _ptr(group_sums), _stream(stream)))
+
+
 class Pool:
     """Device-resident GDN state pool: per layer `slots` slots of Hv*Dv*Dk f32 recurrent
     state and [slots,K-1,D] bf16 conv state. Tensors passed in are torch device
@@ -223,6 +263,9 @@ class Pool:
         self.device = device
 
     def close(self):
+        deps = getattr(self, "_deps", None)
+        if deps is not None:
+            deps.close_all()
         if getattr(self, "handle", None):
             _check(self.lib.gdn_pool_destroy(self.handle))
             self.handle = None
@@ -375,6 +418,18 @@ class QLinear:
         _check(self.lib.gdn_qlinear_forward(self.handle, xp, xs, x.shape[0], yp, ys,
                                             _stream(stream)))
 
+    def forward_sums(self, x, group_sums, y, stream=None):
+        """forward() with x's 64-column group sums supplied (add_rms_norm's
+        group_sums of the same rows)."""
+        xp, xs = _rows(x)
+        yp, ys = _rows(y)
+        if y.shape[0] != x.shape[0]:
+            raise ValueError("x and y row counts differ")
+        if x.shape[1] < self.K or y.shape[1] < self.N:
+            raise ValueError(f"need x [M, >= {self.K}] and y [M, >= {self.N}]")
+        _check(self.lib.gdn_qlinear_forward_sums(self.handle, xp, xs, _ptr(group_sums),
+                                                 x.shape[0], yp, ys, _stream(stream)))
+
     def close(self):
         if getattr(self, "handle", None):
             _check(self.lib.gdn_qlinear_destroy(self.handle))
@@ -490,6 +545,9 @@ class KVCache:
         return k, v
 
     def close(self):
+        deps = getattr(self, "_deps", None)
+        if deps is not None:
+            deps.close_all()
         if getattr(self, "handle", None):
             _check(self.lib.gdn_kv_destroy(self.handle))
             self.handle = None
@@ -533,6 +591,13 @@ class Executor:
         self._stream = stream
         _check(self.lib.gdn_exec_create(ctypes.byref(d), _stream(stream), ctypes.byref(h)))
         self.handle = h
+        self._owners = []
+        for owner in (pool, kv):
+            if owner is not None:
+                if getattr(owner, "_deps", None) is None:
+                    owner._deps = _Dependents()
+                owner._deps.add(self)
+                self._owners.append(owner._deps)
 
     def prefill(self, seq_id: int, prompt) -> int:
         p = (_I32 * len(prompt))(*[int(t) for t in prompt])
@@ -606,10 +671,17 @@ class Executor:
         return _wrap_device(p.value, r.value * v.value, __import__("torch").int16,
                             dev_idx).view(r.value, v.value)
 
-    def close(self):
+    def _destroy(self):
         if getattr(self, "handle", None):
-            _check(self.lib.gdn_exec_destroy(self.handle))
-            self.handle = None
+            h, self.handle = self.handle, None
+            _check(self.lib.gdn_exec_destroy(h))
+        # leave the owners' lists: a closed executor no longer pins the pool
+        for deps in getattr(self, "_owners", ()):
+            deps.remove(self)
+        self._owners = []
+
+    def close(self):
+        self._destroy()
 
     def __del__(self):
         try:
