@@ -84,6 +84,12 @@ def parse_args(argv=None):
                          "hidden 2048 -> q|k|v|z|b|a 12352) over --layers layers instead")
     ap.add_argument("--qlinear-rows", type=int, default=0,
                     help="rows (tokens) per qlinear launch; default --batch (decode)")
+    ap.add_argument("--no-exec", action="store_true",
+                    help="leave the executor sub-measurement out of the default line")
+    ap.add_argument("--exec-steps", type=int, default=32,
+                    help="steps of each executor loop in the default line's exec object")
+    ap.add_argument("--no-components", action="store_true",
+                    help="--exec: skip the per-kernel timing (e.g. under a kernel trace)")
     ap.add_argument("--exec", action="store_true",
                     help="the executor (gdn_exec) decode step over the GDN decoder stack: "
                          "embedding, per layer norm + in_proj + fused decode + out_proj, "
@@ -473,28 +479,19 @@ def _rand_qlinear(K_, parts_rows, gen, dev):
     return q
 
 
-def exec_bench(args):
-    """The executor's decode step (gdn_exec_submit_batch + collect) over the GDN
-    decoder stack of Qwen3.5-35B-A3B's shapes: hidden 2048, `layers` GDN layers
-    (merged 4-bit in_proj 2048 -> 12352, fused conv/norm/gates/recurrence/
-    norm-gate, 4-bit out_proj 4096 -> 2048), 4-bit lm_head 2048 -> vocab,
-    greedy pick; `slots`-slot pools, B sequences prefilled with 16-token
-    prompts. Random weights; tokens are the executor's own picks. Prints one
-    JSON line. `value` times the double-buffered loop (gdn_exec_submit_next:
-    each step queued on the device picks of the step before while that one
-    runs, as src/bin/qwen_mlx_infer.rs:136-187 does); host_fed_ms_per_step
-    times submit + collect with the picks through the host. Both include the
-    host side (staging, launches, the wait for the picked tokens)."""
+def _exec_build(args, max_batch):
+    """The GDN decoder stack of Qwen3.5-35B-A3B's shapes with random weights
+    (and, with --hybrid, the attention layers) behind one executor."""
     import torch
 
     import gdn_amd
     dev = torch.device("cuda:0")
-    L, B, V = args.layers, args.batch, args.vocab
+    L, B, V = args.layers, max_batch, args.vocab
     gen = torch.Generator(device=dev).manual_seed(args.seed)
     bf = torch.bfloat16
     pool = gdn_amd.Pool(L, args.slots, HK, HV)
     P = args.prompt_len
-    gl, keep = [], []
+    gl, parts = [], []
     for l in range(L):
         inp = _rand_qlinear(QL_HIDDEN, QL_PARTS, gen, dev)
         outp = _rand_qlinear(HV * DV, [QL_HIDDEN], gen, dev)
@@ -503,7 +500,7 @@ def exec_bench(args):
         conv_w = (torch.randn((D, KW), generator=gen, device=dev) * 0.25).to(bf)
         norm_w = (1 + 0.1 * torch.randn(DV, generator=gen, device=dev)).to(bf)
         gl.append(gdn_amd.Layer(pool, l, inp, outp, A_log, dt_bias, conv_w, norm_w, 1e-6))
-        keep += [inp, outp]
+        parts.append((inp, outp, A_log, dt_bias, conv_w, norm_w))
     attn, kv, NA = [], None, 0
     if args.hybrid:
         # one attention layer after every three GDN layers (positions 3, 7, ...)
@@ -520,7 +517,6 @@ def exec_bench(args):
             qn = (1 + 0.1 * torch.randn(ATT_HD, generator=gen, device=dev)).to(bf)
             kn = (1 + 0.1 * torch.randn(ATT_HD, generator=gen, device=dev)).to(bf)
             attn.append((4 * i + 3, qkv, o, qn, kn))
-            keep += [qkv, o]
     in_norm = [(1 + 0.1 * torch.randn(QL_HIDDEN, generator=gen, device=dev)).to(bf)
                for _ in range(L + NA)]
     fin = (1 + 0.1 * torch.randn(QL_HIDDEN, generator=gen, device=dev)).to(bf)
@@ -529,6 +525,100 @@ def exec_bench(args):
     ex = gdn_amd.Executor(pool, gl, in_norm, fin, embed, head, 1e-6, max_batch=B,
                           max_prompt=max(64, 4 * P), attn_layers=attn, kv=kv, rope_theta=ATT_THETA,
                           rotary_dim=ATT_ROT)
+    return dict(pool=pool, layers=gl, parts=parts, attn=attn, kv=kv, NA=NA, in_norm=in_norm,
+                fin=fin, head=head, ex=ex)
+
+
+def _exec_components(st, L, B, V, reps=4):
+    """Per-launch averages (us) of the decode step's kernels, from HIP events
+    around HIP-graph replays of each kind of call made over all L layers with
+    the executor's arguments (B rows, the same projections, norms and pool; the
+    fused decode on B slots the executor does not use): the residual add +
+    norm with the group sums, in_proj taking them, the fused decode with the
+    RMSNormGated epilogue, out_proj (summing its K slices itself, where the
+    executor's step leaves them to the next norm), and the final norm +
+    lm_head. A graph of L back-to-back calls keeps the host out of the timed
+    region."""
+    import torch
+
+    import gdn_amd
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(7)
+    bf = torch.bfloat16
+    pool, parts, in_norm = st["pool"], st["parts"], st["in_norm"]
+    h = torch.randn((B, QL_HIDDEN), generator=g, device=dev).to(bf)
+    d = torch.randn((B, QL_HIDDEN), generator=g, device=dev).to(bf)
+    hn = torch.empty_like(h)
+    gs = torch.empty((3, 64, QL_HIDDEN // 64), dtype=bf, device=dev)
+    proj = torch.empty((B, QL_N), dtype=bf, device=dev)
+    gated = torch.empty((B, HV * DV), dtype=bf, device=dev)
+    out = torch.empty((B, QL_HIDDEN), dtype=bf, device=dev)
+    logits = torch.empty((B, V), dtype=bf, device=dev)
+    base = st["pool"].S - B
+    ids = torch.arange(base, base + B, dtype=torch.int32, device=dev)
+    qkvz, ab = proj[:, :D + HV * DV], proj[:, QL_N - 2 * HV:]
+
+    def norm_all():
+        for l in range(L):
+            gdn_amd.add_rms_norm(h, d, in_norm[l], 1e-6, hn, gs)
+
+    def in_all():
+        for l in range(L):
+            parts[l][0].forward_sums(hn, gs, proj)
+
+    def dec_all():
+        for l in range(L):
+            inp, outp, A_log, dt_bias, conv_w, norm_w = parts[l]
+            pool.decode_gated(l, ids, qkvz, ab, A_log, dt_bias, conv_w, norm_w, 1e-6, gated)
+
+    def out_all():
+        for l in range(L):
+            parts[l][1].forward(gated, out)
+
+    def head_one():
+        gdn_amd.add_rms_norm(h, None, st["fin"], 1e-6, hn)
+        st["head"].forward(hn, logits)
+
+    res = {}
+    side = torch.cuda.Stream()
+    for name, fn, n in (("residual_add_norm_us", norm_all, L), ("in_proj_us", in_all, L),
+                        ("decode_gated_us", dec_all, L), ("out_proj_us", out_all, L),
+                        ("final_norm_lm_head_us", head_one, 1)):
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()  # eager warm-up on the capture stream
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        res[name] = round(e0.elapsed_time(e1) * 1e3 / (reps * n), 2)
+        del graph
+    if pool.check():
+        raise RuntimeError("pool status flags after the component timing")
+    return res
+
+
+def exec_measure(args, steps, warmup, components=False):
+    """Time the executor's decode step over `steps` steps after `warmup`, B
+    sequences prefilled with `prompt_len`-token prompts: the double-buffered
+    loop (gdn_exec_submit_next: each step queued on the device picks of the
+    step before while that one runs, as src/bin/qwen_mlx_infer.rs:136-187 does)
+    and the host-fed loop (submit + collect, the picks through the host). Both
+    include the host side (staging, launches, the wait for the picked tokens).
+    Returns a dict, or None on a pool error."""
+    import torch
+    L, B, V, P = args.layers, args.batch, args.vocab, args.prompt_len
+    st = _exec_build(args, B)
+    ex, pool = st["ex"], st["pool"]
     rng = torch.Generator().manual_seed(args.seed)
     ids = list(range(1, B + 1))
     prompts = [torch.randint(0, V, (P,), generator=rng).tolist() for _ in ids]
@@ -545,22 +635,18 @@ def exec_bench(args):
     pre_batched = (time.perf_counter() - t0) / B
     if again != cur:
         print("batched prefill picked other first tokens than single prefills", file=sys.stderr)
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         cur = ex.decode_batch(ids, cur)
     torch.cuda.synchronize()
-    # host-fed: every step's picks go to the host and come back as the next
-    # step's tokens (submit, then collect)
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         ex.submit_batch(ids, cur)
         cur = ex.collect_batch(B)
     fed_elapsed = time.perf_counter() - t0
-    # chained (the double-buffered decode): each step is queued on the device
-    # picks of the one before it while that one runs, and collected after
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     ex.submit_batch(ids, cur)
-    for _ in range(args.steps - 1):
+    for _ in range(steps - 1):
         ex.submit_next(B)
         cur = ex.collect_batch(B)
     cur = ex.collect_batch(B)
@@ -568,8 +654,13 @@ def exec_bench(args):
     flags = pool.check()
     if flags:
         print(f"pool status flags 0x{flags:x}", file=sys.stderr)
-        return 1
-    ms = elapsed / args.steps * 1e3
+        return None
+    comp = _exec_components(st, L, B, V) if components and not args.hybrid else None
+    NA = st["NA"]
+    ex.close()
+    for layer in st["layers"]:
+        layer.close()
+    ms = elapsed / steps * 1e3
     wbytes = L * (QL_N * QL_HIDDEN // 2 + 2 * QL_N * (QL_HIDDEN // 64) * 2
                   + QL_HIDDEN * HV * DV // 2 + 2 * QL_HIDDEN * (HV * DV // 64) * 2) \
         + V * QL_HIDDEN // 2 + 2 * V * (QL_HIDDEN // 64) * 2
@@ -579,17 +670,59 @@ def exec_bench(args):
                         + QL_HIDDEN * ATT_HQ * ATT_HD // 2
                         + 2 * QL_HIDDEN * (ATT_HQ * ATT_HD // 64) * 2)
     # cached keys read per step by the attention layers (mean context over the timed steps)
-    kv_bytes = NA * B * (P + args.warmup + args.steps / 2) * ATT_HKV * ATT_HD * 2 * 2
+    kv_bytes = NA * B * (P + warmup + steps / 2) * ATT_HKV * ATT_HD * 2 * 2
     step_bytes = B * L * STATE_BYTES + wbytes + int(kv_bytes)
-    gbs = step_bytes / (ms * 1e-3) / 1e9
+    return dict(tokens_per_s=B * steps / elapsed, ms=ms, fed_ms=fed_elapsed / steps * 1e3,
+                pre_one=pre_one, pre_batched=pre_batched, g=g, NA=NA, step_bytes=step_bytes,
+                gbs=step_bytes / (ms * 1e-3) / 1e9, components=comp)
+
+
+def exec_summary(args):
+    """The executor sub-object of the default line: the decode step of the
+    30-layer GDN decoder stack (in_proj, fused decode + norm-gate, out_proj,
+    lm_head 2048 -> 248,320, greedy pick) at B = 64."""
+    r = exec_measure(args, args.exec_steps, 8, components=True)
+    if r is None:
+        return None
+    return {
+        "workload": f"executor decode step: {args.layers} GDN layers (in_proj, fused decode + "
+                    f"norm-gate, out_proj) + lm_head {QL_HIDDEN}->{args.vocab}, greedy pick, "
+                    f"B={args.batch}, {args.slots}-slot pools, {args.prompt_len}-token prompts, "
+                    "random 4-bit weights",
+        "tokens_per_s": round(r["tokens_per_s"], 1),
+        "ms_per_step_chained": round(r["ms"], 4),
+        "ms_per_step_host_fed": round(r["fed_ms"], 4),
+        "steps": args.exec_steps,
+        "kernel_avg_us": r["components"],
+        "kernel_timing": "HIP events around HIP-graph replays of each kind of call over all "
+                         "layers (same arguments as the step), divided by the calls",
+        "step_timing": "wall clock over the steps: chained = each step queued on the previous "
+                       "step's device picks (gdn_exec_submit_next); host-fed = submit + collect",
+    }
+
+
+def exec_bench(args):
+    """The executor's decode step over the GDN decoder stack of
+    Qwen3.5-35B-A3B's shapes: hidden 2048, `layers` GDN layers (merged 4-bit
+    in_proj 2048 -> 12352, fused conv/norm/gates/recurrence/norm-gate, 4-bit
+    out_proj 4096 -> 2048), 4-bit lm_head 2048 -> vocab, greedy pick;
+    `slots`-slot pools, B sequences prefilled with `prompt_len`-token prompts.
+    Random weights; tokens are the executor's own picks. Prints one JSON line
+    (see exec_measure for the two loops timed)."""
+    L, B, V, P = args.layers, args.batch, args.vocab, args.prompt_len
+    r = exec_measure(args, args.steps, args.warmup,
+                     components=not (args.hybrid or args.no_components))
+    if r is None:
+        return 1
+    NA, g = r["NA"], r["g"]
     out = {
         "metric": "GDN decoder-stack decode tokens/s through the executor (B sequences, all layers)",
-        "value": round(B * args.steps / elapsed, 1),
+        "value": round(r["tokens_per_s"], 1),
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 4),
+        "ms_per_step": round(r["ms"], 4),
         "higher_is_better": True,
         "dtype": "bf16 activations, 4-bit affine weights, f32 state",
         "data": "synthetic",
@@ -601,22 +734,21 @@ def exec_bench(args):
                                  f"{P}-token prompts",
                    "layers": L, "attention_layers": NA, "batch": B, "slots": args.slots,
                    "hidden": QL_HIDDEN, "vocab": V, "prompt_tokens": P},
-        "host_fed_ms_per_step": round(fed_elapsed / args.steps * 1e3, 4),
+        "host_fed_ms_per_step": round(r["fed_ms"], 4),
         "timing": "wall clock over the steps, each queued on the previous step's device picks "
                   "(gdn_exec_submit_next) and collected after; host_fed_ms_per_step: submit + "
                   "collect per step, the picks through the host",
-        "prefill_ms_per_sequence": {"prompt_tokens": P, "one_per_call": round(pre_one * 1e3, 3),
-                                    f"{g}_per_call": round(pre_batched * 1e3, 3)},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
-                     "algorithmic_bytes_per_step": step_bytes,
+        "prefill_ms_per_sequence": {"prompt_tokens": P, "one_per_call": round(r["pre_one"] * 1e3, 3),
+                                    f"{g}_per_call": round(r["pre_batched"] * 1e3, 3)},
+        "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(r["gbs"] / PEAK_HBM_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_step": r["step_bytes"],
                      "note": "whole step (state read+write of B sequences in every GDN layer, "
                              "every weight byte once, every cached K/V byte once) over the "
                              "host-measured step time"},
     }
-    ex.close()
-    for g in gl:
-        g.close()
+    if r["components"] is not None:
+        out["kernel_avg_us"] = r["components"]
     print(json.dumps(out), flush=True)
     return 0
 
@@ -1037,6 +1169,14 @@ def main(argv=None):
         prefill["one_prompt"] = one_prompt_summary(args)
         if prefill["one_prompt"] is None:
             return 1
+    exec_obj = None
+    if not args.no_exec:
+        import torch as _t
+        w = None
+        _t.cuda.empty_cache()
+        exec_obj = exec_summary(args)
+        if exec_obj is None:
+            return 1
     out = {
         "metric": METRIC,
         "value": round(tok_s, 1),
@@ -1079,6 +1219,8 @@ def main(argv=None):
         out["placement"] = placement
     if prefill is not None:
         out["prefill"] = prefill
+    if exec_obj is not None:
+        out["exec"] = exec_obj
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
         # the reference's CPU-runnable case: one layer, one sequence
