@@ -348,7 +348,12 @@ gdn_status gdn_qlinear_forward_sums(const gdn_qlinear* layer, const uint16_t* x,
  * pool (shared by every layer of the pool, so the pool's calls are ordered
  * on one stream): a call needing more of it than any earlier call
  * synchronises its stream and grows it; gdn_pool_reserve sizes it (and the
- * prefill workspace) up front so later calls allocate nothing.
+ * prefill workspace, for either prefill schedule, also one forced with the
+ * environment variable GDN_PREFILL_WAVES) up front so later calls allocate
+ * nothing. A pool driven by an executor belongs to it: other calls on the
+ * pool must be ordered after the executor's work (its stream, or a
+ * synchronisation). Growing the activation buffer makes the executor drop
+ * and capture anew the step graphs that held the old one.
  * ------------------------------------------------------------------------ */
 typedef struct gdn_layer gdn_layer;
 

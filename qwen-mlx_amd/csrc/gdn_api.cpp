@@ -75,6 +75,7 @@ struct gdn_pool {
   size_t workspace_bytes = 0;
   void* act = nullptr;  // gdn_layer_* activations: projection rows, gated rows
   size_t act_bytes = 0;
+  uint64_t act_gen = 0;  // bumped whenever act is reallocated (captured graphs hold it)
   std::set<int32_t> free_slots;
   std::vector<uint8_t> in_use;
 };
@@ -395,8 +396,9 @@ constexpr int32_t kMaxQLinearRows = 65535 * 128;
 // Grows a pool-held device buffer to at least `need` bytes. Growing waits
 // for the stream, so work still reading the old buffer has finished.
 static gdn_status ensure_buffer(void*& buf, size_t& bytes, size_t need, void* stream,
-                                const char* what) {
+                                const char* what, uint64_t* gen = nullptr) {
   if (need <= bytes) return GDN_OK;
+  if (gen) ++*gen;
   if (buf) {
     hipError_t e = hipStreamSynchronize(as_stream(stream));
     if (e != hipSuccess) return hip_fail(e, "workspace grow sync");
@@ -790,6 +792,8 @@ gdn_status gdn_add_rms_norm(uint16_t* h, const uint16_t* d, int32_t n, int32_t h
 
 namespace gdn {
 
+uint64_t pool_act_generation(const gdn_pool* p) { return p ? p->act_gen : 0; }
+
 gdn_status qlinear_forward(const gdn_qlinear* q, const uint16_t* x, int64_t x_stride, int32_t M,
                            uint16_t* y, int64_t y_stride, void* stream, QPartial* defer,
                            const uint16_t* xsplit) {
@@ -929,7 +933,7 @@ gdn_status gdn_pool_reserve(gdn_pool* pool, int32_t max_tokens, void* stream) {
                 kMaxPrefillTokens);
   DeviceGuard guard(pool->d.device);
   st = ensure_buffer(pool->act, pool->act_bytes, layer_act_bytes(pool, max_tokens), stream,
-                     "layer activation");
+                     "layer activation", &pool->act_gen);
   if (st) return st;
   return ensure_workspace(pool, gdn::prefill_workspace_reserve_bytes(pool->R, pool->d.num_k_heads,
                                                                      max_tokens), stream, "prefill");
@@ -955,7 +959,8 @@ gdn_status gdn::layer_decode(gdn_layer* L, const int32_t* slot_ids, int32_t B, c
                 p->d.num_slots);
   {
     DeviceGuard guard(p->d.device);
-    st = ensure_buffer(p->act, p->act_bytes, layer_act_bytes(p, B), stream, "layer activation");
+    st = ensure_buffer(p->act, p->act_bytes, layer_act_bytes(p, B), stream, "layer activation",
+                       &p->act_gen);
     if (st) return st;
   }
   const int64_t value = (int64_t)p->d.num_v_heads * p->d.head_v_dim;
@@ -991,7 +996,7 @@ gdn_status gdn_layer_prefill(gdn_layer* L, const int32_t* slot_ids, const int32_
   {
     DeviceGuard guard(p->d.device);
     st = ensure_buffer(p->act, p->act_bytes, layer_act_bytes(p, total_tokens), stream,
-                       "layer activation");
+                       "layer activation", &p->act_gen);
     if (st) return st;
   }
   const int64_t value = (int64_t)p->d.num_v_heads * p->d.head_v_dim;

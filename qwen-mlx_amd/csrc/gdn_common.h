@@ -313,6 +313,9 @@ hipError_t launch_embed(const uint16_t* table, const int32_t* tok, int n, int vo
 gdn_status qlinear_forward(const gdn_qlinear* q, const uint16_t* x, int64_t x_stride, int32_t M,
                            uint16_t* y, int64_t y_stride, void* stream, QPartial* defer,
                            const uint16_t* xsplit = nullptr);
+// Bumped each time the pool's layer-activation buffer is reallocated (a graph
+// that captured gdn::layer_decode holds the old buffer's address).
+uint64_t pool_act_generation(const gdn_pool* p);
 gdn_status layer_decode(gdn_layer* L, const int32_t* slot_ids, int32_t B, const uint16_t* x,
                         int64_t x_stride, uint16_t* out, int64_t out_stride, void* stream,
                         QPartial* defer, const uint16_t* xsplit = nullptr);

@@ -28,6 +28,7 @@
 #include <cstdlib>
 #include <cstdio>
 #include <string>
+#include <thread>
 #include <unordered_map>
 #include <unordered_set>
 #include <vector>
@@ -127,6 +128,7 @@ struct gdn_exec {
     bool failed = false;  // capture refused (e.g. a debug check syncing): run eagerly
   };
   std::unordered_map<int32_t, StepGraphs> graphs;
+  uint64_t graphs_act_gen = 0;  // the pool's activation buffer the graphs were captured on
 };
 
 namespace {
@@ -281,7 +283,23 @@ gdn_status decode_seg(gdn_exec* x, int B, int k, int ps) {
 // Captures the B-row decode step's segments into graphs, one set per pinned
 // pick slot (once per B). A capture that fails leaves the batch size on the
 // eager path.
+// Drops every captured step graph (they hold the pool's activation buffer,
+// which a layer call with more rows or gdn_pool_reserve may have reallocated).
+void drop_graphs(gdn_exec* x) {
+  if (x->graphs.empty()) return;
+  (void)hipStreamSynchronize(x->stream);  // no replay still in flight
+  for (auto& kv : x->graphs)
+    for (auto& v : kv.second.seg)
+      for (hipGraphExec_t g : v) (void)hipGraphExecDestroy(g);
+  x->graphs.clear();
+}
+
 gdn_exec::StepGraphs& step_graphs(gdn_exec* x, int B) {
+  const uint64_t gen = gdn::pool_act_generation(x->pool);
+  if (gen != x->graphs_act_gen) {
+    drop_graphs(x);
+    x->graphs_act_gen = gen;
+  }
   gdn_exec::StepGraphs& sg = x->graphs[B];
   if (!sg.seg[0].empty() || sg.failed) return sg;
   const int nseg = (int)x->attn.size() + 1;
@@ -705,6 +723,10 @@ gdn_status gdn_exec_submit_next(gdn_exec* x, int32_t B) {
   return queue_step(x, B);
 }
 
+// Polls of the pick slot with a pause between them before collect starts to
+// yield the core between polls.
+constexpr uint64_t kCollectSpinPolls = 1 << 16;
+
 gdn_status gdn_exec_collect_batch(gdn_exec* x, uint32_t* next_tokens, int32_t B) {
   if (!x || !next_tokens) return efail(GDN_ERR_INVALID, "gdn_exec_collect_batch: NULL argument");
   if (x->pend_n == 0) return efail(GDN_ERR_INVALID, "gdn_exec_collect_batch: nothing submitted");
@@ -715,7 +737,9 @@ gdn_status gdn_exec_collect_batch(gdn_exec* x, uint32_t* next_tokens, int32_t B)
   x->pend_head ^= 1;
   --x->pend_n;
   // The greedy pick writes the step's tokens (>= 0) into the pinned slot, the
-  // step's last device work. Poll it; every 1024 polls ask the stream for an
+  // step's last device work. Poll it, with a pause instruction between polls;
+  // after the first kCollectSpinPolls polls (about a decode step's worth) give
+  // the core up between polls (yield). Every 1024 polls ask the stream for an
   // error, and a stream that has drained with picks missing is one.
   volatile const int32_t* picks = x->p_next + (size_t)e * x->max_batch;
   auto landed = [&]() {
@@ -724,6 +748,10 @@ gdn_status gdn_exec_collect_batch(gdn_exec* x, uint32_t* next_tokens, int32_t B)
     return true;
   };
   for (uint64_t spin = 1; !landed(); ++spin) {
+    if (spin < kCollectSpinPolls)
+      __builtin_ia32_pause();
+    else
+      std::this_thread::yield();
     if (spin % 1024 != 0) continue;
     const hipError_t q = hipStreamQuery(x->stream);
     if (q == hipErrorNotReady) continue;

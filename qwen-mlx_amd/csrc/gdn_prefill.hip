@@ -1172,11 +1172,17 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(
 // head)) where the fused kernel would leave most CUs idle: few sequences of
 // many chunks. The environment variable GDN_PREFILL_WAVES = 2, 4 or 8 forces
 // a path (tests compare the paths with it).
-int prefill_chunk_waves(int R, int Hk, int nseq, int total_tokens) {
+// The path GDN_PREFILL_WAVES forces (2, 4 or 8), or 0.
+static int forced_chunk_waves() {
   if (const char* v = getenv("GDN_PREFILL_WAVES")) {
     const int f = atoi(v);
-    if (f == 2 || f == 4 || f == 8) return total_tokens > 0 ? f : 8;
+    if (f == 2 || f == 4 || f == 8) return f;
   }
+  return 0;
+}
+
+int prefill_chunk_waves(int R, int Hk, int nseq, int total_tokens) {
+  if (const int f = forced_chunk_waves()) return total_tokens > 0 ? f : 8;
   if (nseq <= 0 || total_tokens <= 0 || total_tokens > kSplitMaxTokens) return 8;
   if (total_tokens / nseq < kSplitMinTokens) return 8;
   // measured on 16,384-token prompts (32 value heads): one or two prompts
@@ -1194,6 +1200,11 @@ size_t prefill_workspace_reserve_bytes(int R, int Hk, int max_tokens) {
   // the largest call the split path takes: every sequence count it picks,
   // the gated epilogue's y scratch included
   size_t most = prefill_workspace_bytes(R, Hk, max_tokens, 1, 8, false);
+  // a forced split takes any call: up to one sequence per token
+  const int f = forced_chunk_waves();
+  if (f == 2 || f == 4)
+    most = std::max(most, prefill_workspace_bytes(R, Hk, max_tokens, std::max(max_tokens, 1), f,
+                                                  true));
   if (max_tokens > kSplitMaxTokens) max_tokens = kSplitMaxTokens;
   for (int nseq = 1; nseq * Hk * R <= 96 && nseq <= max_tokens; ++nseq)
     most = std::max(most, prefill_workspace_bytes(R, Hk, max_tokens, nseq, 2, true));

@@ -11,12 +11,17 @@
 #include <hip/hip_runtime_api.h>
 
 #include <cstdlib>
+#include <functional>
+#include <vector>
 #include <cstring>
 
 #include "gdn_common.h"
 
 namespace gdn_fake {
 bool fail_embed = false;  // set by the test: embedding launches fail
+bool capture = false;     // set by the test: stream capture records the stand-in launches
+int graphs_live = 0, graphs_destroyed = 0, graphs_made = 0;
+std::vector<std::function<void()>>* recording = nullptr;  // the capture in progress
 }
 
 extern "C" {
@@ -67,18 +72,47 @@ hipError_t hipStreamDestroy(hipStream_t stream) {
   delete[] reinterpret_cast<char*>(stream);
   return hipSuccess;
 }
-// No stream capture here: the executor's decode steps take their eager path.
-hipError_t hipStreamBeginCapture(hipStream_t, hipStreamCaptureMode) { return hipErrorNotSupported; }
+// Stream capture: refused unless the test sets gdn_fake::capture. Then the
+// stand-in launches made while capturing are recorded instead of run (only the
+// greedy pick has an effect here: it writes the picks) and a graph launch
+// replays them, so the executor's host-side graph bookkeeping (capture,
+// replay, drop) runs as on the device, counted by graphs_*.
+hipError_t hipStreamBeginCapture(hipStream_t, hipStreamCaptureMode) {
+  if (!gdn_fake::capture) return hipErrorNotSupported;
+  gdn_fake::recording = new std::vector<std::function<void()>>();
+  return hipSuccess;
+}
 hipError_t hipStreamEndCapture(hipStream_t, hipGraph_t* graph) {
-  *graph = nullptr;
-  return hipErrorNotSupported;
+  *graph = reinterpret_cast<hipGraph_t>(gdn_fake::recording);
+  gdn_fake::recording = nullptr;
+  return *graph ? hipSuccess : hipErrorNotSupported;
 }
-hipError_t hipGraphInstantiate(hipGraphExec_t*, hipGraph_t, hipGraphNode_t*, char*, size_t) {
-  return hipErrorNotSupported;
+hipError_t hipGraphInstantiate(hipGraphExec_t* exec, hipGraph_t graph, hipGraphNode_t*, char*,
+                               size_t) {
+  if (!gdn_fake::capture || !graph) return hipErrorNotSupported;
+  *exec = reinterpret_cast<hipGraphExec_t>(new std::vector<std::function<void()>>(
+      *reinterpret_cast<std::vector<std::function<void()>>*>(graph)));
+  ++gdn_fake::graphs_live;
+  ++gdn_fake::graphs_made;
+  return hipSuccess;
 }
-hipError_t hipGraphDestroy(hipGraph_t) { return hipSuccess; }
-hipError_t hipGraphExecDestroy(hipGraphExec_t) { return hipSuccess; }
-hipError_t hipGraphLaunch(hipGraphExec_t, hipStream_t) { return hipErrorNotSupported; }
+hipError_t hipGraphDestroy(hipGraph_t graph) {
+  delete reinterpret_cast<std::vector<std::function<void()>>*>(graph);
+  return hipSuccess;
+}
+hipError_t hipGraphExecDestroy(hipGraphExec_t exec) {
+  if (exec) {
+    delete reinterpret_cast<std::vector<std::function<void()>>*>(exec);
+    --gdn_fake::graphs_live;
+    ++gdn_fake::graphs_destroyed;
+  }
+  return hipSuccess;
+}
+hipError_t hipGraphLaunch(hipGraphExec_t exec, hipStream_t) {
+  if (!gdn_fake::capture || !exec) return hipErrorNotSupported;
+  for (auto& fn : *reinterpret_cast<std::vector<std::function<void()>>*>(exec)) fn();
+  return hipSuccess;
+}
 hipError_t hipDeviceSynchronize(void) { return hipSuccess; }
 hipError_t hipGetLastError(void) { return hipSuccess; }
 const char* hipGetErrorString(hipError_t) { return "host stand-in"; }
@@ -158,9 +192,15 @@ hipError_t launch_embed_norm(const uint16_t*, const int32_t*, int, int, int, con
 }
 hipError_t launch_argmax(const uint16_t*, int64_t, int n, int, float*, int*, int32_t* out,
                          int32_t* out_host, hipStream_t) {
-  for (int i = 0; i < n; ++i) out[i] = 0;
-  if (out_host)
-    for (int i = 0; i < n; ++i) out_host[i] = 0;
+  auto run = [=] {
+    for (int i = 0; i < n; ++i) out[i] = 0;
+    if (out_host)
+      for (int i = 0; i < n; ++i) out_host[i] = 0;
+  };
+  if (gdn_fake::recording)
+    gdn_fake::recording->push_back(run);
+  else
+    run();
   return hipSuccess;
 }
 

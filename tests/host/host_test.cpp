@@ -12,6 +12,8 @@
 
 namespace gdn_fake {
 extern bool fail_embed;  // fake_hip.cpp: the next embedding launches fail
+extern bool capture;     // fake_hip.cpp: stream capture makes (empty) graphs
+extern int graphs_live, graphs_destroyed, graphs_made;
 }
 
 static int g_checks = 0;
@@ -272,8 +274,69 @@ static int test_exec() {
   return 0;
 }
 
+// The executor's step graphs hold the pool's activation buffer: after
+// gdn_pool_reserve grows it, the next step drops every graph and captures anew.
+static int test_exec_graphs_follow_pool_buffer() {
+  std::vector<std::vector<char>> keep;
+  const int hidden = 512, vocab = 1024, Hk = 16, Hv = 32, D = 2 * Hk * 128 + Hv * 128;
+  gdn_pool_desc pd{1, 4, Hk, Hv, 128, 128, 4, 0};
+  gdn_pool* pool = nullptr;
+  CHECK(gdn_pool_create(&pd, &pool) == GDN_OK);
+  gdn_qlinear* in = make_qlinear(keep, hidden, {D, Hv * 128, Hv, Hv});
+  gdn_qlinear* out = make_qlinear(keep, Hv * 128, {hidden});
+  gdn_qlinear* head = make_qlinear(keep, hidden, {vocab});
+  CHECK(in && out && head);
+  gdn_layer_desc ld{pool, 0, in, out, dev_alloc<float>(keep, Hv), dev_alloc<float>(keep, Hv),
+                    dev_alloc<uint16_t>(keep, (size_t)D * 4), dev_alloc<uint16_t>(keep, 128),
+                    1e-6f};
+  gdn_layer* layer = nullptr;
+  CHECK(gdn_layer_create(&ld, &layer) == GDN_OK);
+  const uint16_t* norms[1] = {dev_alloc<uint16_t>(keep, hidden)};
+  gdn_exec_desc ed{};
+  ed.pool = pool;
+  ed.num_layers = 1;
+  ed.layers = &layer;
+  ed.input_norm_w = norms;
+  ed.final_norm_w = dev_alloc<uint16_t>(keep, hidden);
+  ed.rms_eps = 1e-6f;
+  ed.embed = dev_alloc<uint16_t>(keep, (size_t)vocab * hidden);
+  ed.head = head;
+  ed.max_batch = 4;
+  ed.max_prompt = 64;
+  ed.device = 0;
+  gdn_fake::capture = true;
+  gdn_fake::graphs_live = gdn_fake::graphs_destroyed = gdn_fake::graphs_made = 0;
+  gdn_exec* ex = nullptr;
+  CHECK(gdn_exec_create(&ed, nullptr, &ex) == GDN_OK && ex);
+  std::vector<int32_t> p(5, 3);
+  uint32_t t = 0;
+  uint64_t ids[2] = {1, 2};
+  CHECK(gdn_exec_prefill(ex, 1, p.data(), 5, &t) == GDN_OK);
+  CHECK(gdn_exec_prefill(ex, 2, p.data(), 5, &t) == GDN_OK);
+  uint32_t toks[2] = {1, 2}, next[2];
+  CHECK(gdn_exec_decode_batch(ex, ids, toks, 2, next) == GDN_OK);
+  const int made = gdn_fake::graphs_made;
+  CHECK(made > 0 && gdn_fake::graphs_destroyed == 0);
+  CHECK(gdn_exec_decode_batch(ex, ids, toks, 2, next) == GDN_OK);
+  CHECK(gdn_fake::graphs_made == made);                      // replayed, not captured again
+  CHECK(gdn_pool_reserve(pool, 4096, nullptr) == GDN_OK);    // activation buffer reallocated
+  CHECK(gdn_exec_decode_batch(ex, ids, toks, 2, next) == GDN_OK);
+  CHECK(gdn_fake::graphs_destroyed == made);                 // every old graph dropped
+  CHECK(gdn_fake::graphs_made == 2 * made);                  // and captured anew
+  CHECK(gdn_pool_reserve(pool, 4096, nullptr) == GDN_OK);    // no growth: graphs kept
+  CHECK(gdn_exec_decode_batch(ex, ids, toks, 2, next) == GDN_OK);
+  CHECK(gdn_fake::graphs_made == 2 * made);
+  CHECK(gdn_exec_destroy(ex) == GDN_OK);
+  CHECK(gdn_fake::graphs_live == 0);
+  gdn_fake::capture = false;
+  CHECK(gdn_layer_destroy(layer) == GDN_OK);
+  for (gdn_qlinear* q : {in, out, head}) CHECK(gdn_qlinear_destroy(q) == GDN_OK);
+  CHECK(gdn_pool_destroy(pool) == GDN_OK);
+  return 0;
+}
+
 int main() {
-  if (test_pool() || test_kv() || test_exec()) return 1;
+  if (test_pool() || test_kv() || test_exec() || test_exec_graphs_follow_pool_buffer()) return 1;
   std::printf("ALL OK (%d checks)\n", g_checks);
   return 0;
 }

@@ -1,7 +1,9 @@
 """GPU test of gdn_prefill_varlen_noalloc (the prefill with a fixed per-device
 scratch workspace) against gdn_prefill_varlen on twin pools: outputs and the
 slots' recurrent and conv states bit-identical, over two calls in a row, the
-second smaller; oversized calls are refused on the host."""
+second smaller; oversized calls are refused on the host. The same call
+captured in a HIP graph and replayed gives the eager call's results, and an
+eager call leaves the device's free memory unchanged."""
 import numpy as np
 import pytest
 
@@ -63,6 +65,67 @@ def test_noalloc_prefill_matches_prefill(gpu):
     pools[1].read(0, _ids(slots), s, c)
     torch.cuda.synchronize()
     assert np.array_equal(host(s), sb) and np.array_equal(host(c), cb)
+    for pool in pools:
+        assert pool.check() == 0
+        pool.close()
+
+
+def test_noalloc_prefill_in_hip_graph(gpu):
+    """gdn_prefill_varlen_noalloc captured in a HIP graph (torch.cuda.graph on
+    the stream the binding passes) and replayed three times, the slots' state
+    restored by eager writes between replays: every replay's y, recurrent and
+    conv state bit-identical to the eager call's. Device memory in use is the
+    same before and after an eager call (hipMemGetInfo)."""
+    import torch
+    import gdn_amd
+    rng = np.random.default_rng(1500)
+    p = gen_layer_params(rng, HK, HV)
+    pools = [gdn_amd.Pool(1, 12, HK, HV) for _ in range(2)]
+    slots = [4, 10, 0, 7]
+    lens = [70, 300, 5, 129]
+    st, cs = gen_states(rng, len(slots), HK, HV)
+    x, ab = gen_tokens(rng, int(sum(lens)), HK, HV)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    total = int(cu[-1])
+    d_ids, d_cu, d_x, d_ab = _ids(slots), dev(cu), dev(x), dev(ab)
+    d_al, d_dt, d_cw = dev(p["A_log"]), dev(p["dt_bias"]), dev(p["conv_w"])
+    d_st, d_cs = dev(st), dev(cs)
+    for pool in pools:
+        pool.write(0, d_ids, d_st, d_cs)
+    torch.cuda.synchronize()
+    # the eager reference on pool 0, free device memory around it
+    ya = torch.zeros((total, HV, DV), dtype=torch.int16, device=gpu)
+    free0 = torch.cuda.mem_get_info()[0]
+    pools[0].prefill_noalloc(0, d_ids, d_cu, total, d_x, d_ab, d_al, d_dt, d_cw, ya)
+    torch.cuda.synchronize()
+    free1 = torch.cuda.mem_get_info()[0]
+    say("noalloc eager call", f"free device memory before {free0} after {free1}")
+    assert free1 == free0, "the no-allocation prefill changed device memory in use"
+    s = torch.empty((len(slots), HV, DV, DK), dtype=torch.float32, device=gpu)
+    c = torch.empty((len(slots), K - 1, pools[0].D), dtype=torch.int16, device=gpu)
+    pools[0].read(0, d_ids, s, c)
+    torch.cuda.synchronize()
+    ref = (host(ya), host(s), host(c))
+    # captured on pool 1 (an eager call first sets the device's scratch address up)
+    yb = torch.zeros((total, HV, DV), dtype=torch.int16, device=gpu)
+    pools[1].prefill_noalloc(0, d_ids, d_cu, total, d_x, d_ab, d_al, d_dt, d_cw, yb)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        pools[1].prefill_noalloc(0, d_ids, d_cu, total, d_x, d_ab, d_al, d_dt, d_cw, yb)
+    for rep in range(3):
+        pools[1].write(0, d_ids, d_st, d_cs)
+        yb.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        pools[1].read(0, d_ids, s, c)
+        torch.cuda.synchronize()
+        say("noalloc graph replay", rep)
+        assert np.array_equal(host(yb), ref[0]), rep
+        assert np.array_equal(host(s), ref[1]), rep
+        assert np.array_equal(host(c), ref[2]), rep
+    del graph
     for pool in pools:
         assert pool.check() == 0
         pool.close()
