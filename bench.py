@@ -536,8 +536,8 @@ def _exec_components(st, L, B, V, reps=4):
     fused decode on B slots the executor does not use): the residual add +
     norm with the group sums, in_proj taking them, the fused decode with the
     RMSNormGated epilogue, out_proj (summing its K slices itself, where the
-    executor's step leaves them to the next norm), and the final norm +
-    lm_head. A graph of L back-to-back calls keeps the host out of the timed
+    executor's step leaves them to the next norm), and the final norm with the
+    group sums + lm_head taking them. A graph of L back-to-back calls keeps the host out of the timed
     region."""
     import torch
 
@@ -576,8 +576,8 @@ def _exec_components(st, L, B, V, reps=4):
             parts[l][1].forward(gated, out)
 
     def head_one():
-        gdn_amd.add_rms_norm(h, None, st["fin"], 1e-6, hn)
-        st["head"].forward(hn, logits)
+        gdn_amd.add_rms_norm(h, None, st["fin"], 1e-6, hn, gs)
+        st["head"].forward_sums(hn, gs, logits)
 
     res = {}
     side = torch.cuda.Stream()

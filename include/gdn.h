@@ -324,12 +324,15 @@ gdn_status gdn_add_rms_norm(uint16_t* h, const uint16_t* d, int32_t n, int32_t h
 
 /* gdn_qlinear_forward on rows x whose 64-column group sums a producer has
  * already formed (gdn_add_rms_norm's group_sums of the same rows). The
- * decode-sized path (M <= 64) of a K = 2048 layer that runs whole-K tiles
- * takes the sums instead of forming them with products of x; every other
- * shape ignores group_sums. Same arguments and results contract as
+ * decode-sized paths (M <= 64) of a K = 2048 layer that runs whole-K tiles
+ * and of every layer at least 131,072 columns wide (lm_head) take the sums
+ * instead of forming them with products of x; every other shape ignores
+ * group_sums. Rows M..63 of group_sums are read but only reach outputs past
+ * row M, which are not written. Same arguments and results contract as
  * gdn_qlinear_forward otherwise. It has no counterpart in the reference,
  * whose quantized_matmul (qwen3_5.rs:572-586) forms the sums itself; it is
- * the fused norm-to-projection hand-off the executor uses for in_proj. */
+ * the fused norm-to-projection hand-off the executor uses for in_proj and
+ * lm_head. */
 gdn_status gdn_qlinear_forward_sums(const gdn_qlinear* layer, const uint16_t* x, int64_t x_stride,
                                     const uint16_t* group_sums, int32_t M, uint16_t* y,
                                     int64_t y_stride, void* stream);
@@ -503,9 +506,10 @@ gdn_status gdn_exec_decode_batch(gdn_exec* exec, const uint64_t* seq_ids, const 
  * executor's stream. Results are bit-identical to launching kernel by kernel,
  * which the environment variable GDN_EXEC_GRAPHS=0 (read at gdn_exec_create)
  * selects. A batch size whose capture fails runs eagerly. A GDN layer's
- * in_proj takes its rows' group sums from the preceding norm
+ * in_proj and lm_head take their rows' group sums from the preceding norm
  * (gdn_add_rms_norm / gdn_qlinear_forward_sums) when B <= 64; the variable
- * GDN_EXEC_SPLIT_SUMS=0 (read at gdn_exec_create) makes it form them itself. */
+ * GDN_EXEC_SPLIT_SUMS=0 (read at gdn_exec_create) makes them form them
+ * themselves. */
 gdn_status gdn_exec_submit_batch(gdn_exec* exec, const uint64_t* seq_ids, const uint32_t* tokens,
                                  int32_t B);
 /* Collects the oldest uncollected step (of at most two, see below). */

@@ -121,7 +121,7 @@ struct gdn_exec {
   // between attention calls captured once as segments (an attention call's
   // launch shape follows the step's KV plan, so it runs eagerly between them).
   bool use_graphs = true;
-  bool use_split_sums = true;  // in_proj takes its rows' group sums from the norm
+  bool use_split_sums = true;  // in_proj and lm_head take their rows' group sums from the norm
   hipStream_t cap = nullptr;  // private stream the segments are captured on
   struct StepGraphs {
     std::vector<hipGraphExec_t> seg[2];  // per pinned pick slot the step writes
@@ -267,12 +267,15 @@ gdn_status decode_seg(gdn_exec* x, int B, int k, int ps) {
   }
   if (seg != k) return GDN_OK;
   gdn::QPartial pp = x->pend;
+  // lm_head, too, takes its rows' group sums from the norm
+  uint16_t* const hxs = x->use_split_sums && B <= 64 && x->hidden % 64 == 0 ? x->xsplit : nullptr;
   HIP_TRY(gdn::launch_add_norm(x->h, x->stack.empty() ? nullptr : x->mix,
                                x->stack.empty() ? nullptr : &pp, B, x->hidden, x->final_norm_w,
-                               x->eps, x->hn, x->stream),
+                               x->eps, x->hn, x->stream, hxs),
           "final norm");
   x->pend = gdn::QPartial{};
-  GDN_TRY(gdn_qlinear_forward(x->head, x->hn, x->hidden, B, x->logits, x->vocab, x->stream));
+  GDN_TRY(gdn::qlinear_forward(x->head, x->hn, x->hidden, B, x->logits, x->vocab, x->stream,
+                               nullptr, hxs));
   // the picks overwrite the step's input tokens (the embedding has read them)
   HIP_TRY(gdn::launch_argmax(x->logits, x->vocab, B, x->vocab, x->d_pv, x->d_pi, toks,
                              x->p_next_dev + (size_t)ps * x->max_batch, x->stream),

@@ -298,68 +298,114 @@ __global__ __launch_bounds__(256) void qlinear_kernel(
 }
 
 
-// Very wide layers at decode sizes (lm_head): the tile of qlinear_kernel (64
-// rows, every wave all of them and NW column fragments), with x copied into
-// LDS by DMA (buffer_load ... lds: wave w copies rows 4w + 16j .. +3 of the
-// stage, 1 KiB per load, lane L to byte 16 L of those rows, i.e. physical
-// chunk L % 16 of row 4w + 16j + L / 16, which holds logical chunk
-// (L % 16) ^ (row % 16) -- the swizzle of qlinear_kernel) instead of through
-// registers. That frees the staging registers, and the register budget of
-// three waves per SIMD (three 48 KiB work-groups per CU) holds without
-// spills. Each stage ends with this wave's copies of the next stage landed
-// (vmcnt 0) and a bare barrier: an LDS fence would also count the copies.
-// The two buffers are separate arrays, so that the compiler can tell copies
-// into one from reads of the other. K a multiple of 256 (whole stage pairs).
-template <int MW, int NW, int WM, int WN>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void qlinear_wide_kernel(
-    const uint16_t* __restrict__ x, int64_t xs, int M, int K, const u32x4* __restrict__ wp,
+// Very wide layers at decode sizes (lm_head): 64 x 128 tiles of four waves in
+// a row, every wave with all 64 rows and two 16-column fragments (the weight
+// fragment is the MFMA A operand, as in qlinear_kernel). Per stage of 128 k:
+//  - x (64 rows x 256 B) is copied into LDS by DMA (buffer_load ... lds: wave
+//    w copies rows 4w + 16j .. +3, 1 KiB per load, lane L to byte 16 L of
+//    those rows, i.e. physical chunk L % 16 of row 4w + 16j + L / 16, which
+//    holds logical chunk (L % 16) ^ (row % 16) -- the swizzle of
+//    qlinear_kernel), double buffered;
+//  - the weights go to registers one stage ahead;
+//  - the scales (64 B per fragment) are copied into LDS by DMA, one 4-byte
+//    copy per wave for its two fragments: a 16-byte load per lane of the
+//    same block costs the vector memory path as much as a weight load.
+// Weights and scales are read through buffer resources with the stage in
+// soffset, so no address registers are kept per stage.
+// Each stage ends with this wave's copies of the next stage landed (vmcnt 0)
+// and a bare barrier: an LDS fence would also count the copies. The ring
+// slots are separate arrays, so that the compiler can tell copies into one
+// from reads of another.
+// Group sums X_g: wave w forms those of its own 16-row block with the
+// ones-MFMA and keeps them in registers, lane group c4 holding group 4t + c4
+// of ring turn t (a shift register of KT values, KT >= G / 4); they are
+// stored to LDS once after the loop. (An LDS store in the loop made the
+// compiler wait there for the DMA copies of the next stage.) With XS the
+// caller's split sums (xsg [3][64][G] bf16, launch_add_norm's) are copied
+// into LDS by DMA with the first stage instead, and no X_g products are
+// formed.
+// K a multiple of 512 (G a multiple of 8), G <= 4 KT; three waves per SIMD
+// for K <= 2048 (KT = 8), two above.
+template <int KT, bool XS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KT <= 8 ? 3 : 2, KT <= 8 ? 3 : 2))) void qlinear_head_kernel(
+    const uint16_t* __restrict__ x, int64_t xs, int M, int K, const uint16_t* __restrict__ wp,
     const uint16_t* __restrict__ sp, const uint16_t* __restrict__ bias,
-    const uint16_t* __restrict__ nsc, int N, uint16_t* __restrict__ y, int64_t ys) {
-  static_assert(WM * WN == 4, "four waves per work-group");
-  constexpr int MT = 16 * MW * WM, NT = 16 * NW * WN;
+    const uint16_t* __restrict__ nsc, int N, int Npad, uint16_t* __restrict__ y, int64_t ys,
+    const uint16_t* __restrict__ xsg) {
+  constexpr int MW = 4, NW = 2, MT = 64;
   constexpr int XROW = kStageK * 2;  // bytes per staged x row
-  constexpr int SJ = MT / 16;        // 1 KiB copies per wave per stage
+  constexpr int GMAX = 4 * KT, GJ = GMAX / 32;
+  static_assert(GMAX % 32 == 0, "whole 32-group chunks");
   __shared__ __align__(16) uint8_t xl0[MT * XROW];
   __shared__ __align__(16) uint8_t xl1[MT * XROW];
-  __shared__ float sx[kMaxGroups * MT];  // X_g[m] at sx[g*MT + m]
+  __shared__ __align__(16) uint8_t sl0[4 * 256];  // per wave: its fragments' 2 x 64 B
+  __shared__ __align__(16) uint8_t sl1[4 * 256];
+  // X_g: f32 [g][m] (formed here) or the caller's bf16 [3][m][G]
+  __shared__ __align__(16) uint8_t sxb[XS ? 3 * MT * GMAX * 2 : GMAX * MT * 4];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave / WN, wn = wave % WN;
   const int G = K >> 6, P = K >> 7;
-  const int m0 = blockIdx.y * MT;
-  const int f0 = blockIdx.x * (NT / 16) + wn * NW;  // first column fragment of the wave
+  const int f0 = blockIdx.x * 8 + wave * NW;  // first column fragment of the wave
   const int r16 = lane & 15, c4 = lane >> 4;
 
   const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)x, (short)0, (int)(((int64_t)(M - 1) * xs + K) * 2), 0x00020000);
-  auto copy_x = [&](int p, uint8_t* dst) {
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)wp, (short)0, (int)((int64_t)(Npad / 16) * P * 1024), 0x00020000);
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)sp, (short)0, (int)((int64_t)(Npad / 16) * P * 64), 0x00020000);
+  int xvo[4];
 #pragma unroll
-    for (int j = 0; j < SJ; ++j) {
-      const int rl = 4 * wave + 16 * j;  // first row of the load
-      const int row = rl + (lane >> 4);
-      const int r = min(m0 + row, M - 1);
-      const int lc = (lane & 15) ^ (row & 15);
-      const int voff = (int)((r * xs + p * kStageK + 8 * lc) * 2);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          xrs, (void __attribute__((address_space(3)))*)(dst + rl * XROW), 16, voff, 0, 0, 0);
-    }
-  };
-  const u32x4* wsrc[NW];
-  const u32x4* ssrc[NW];
-#pragma unroll
-  for (int i = 0; i < NW; ++i) {
-    wsrc[i] = wp + (int64_t)(f0 + i) * P * 64 + lane;
-    ssrc[i] = reinterpret_cast<const u32x4*>(sp) + (int64_t)(f0 + i) * P * 4 + c4;
+  for (int j = 0; j < 4; ++j) {
+    const int row = 4 * (wave + 4 * j) + (lane >> 4);
+    xvo[j] = (int)((min(row, M - 1) * xs + 8 * ((lane & 15) ^ (row & 15))) * 2);
   }
+  const int wvo0 = (f0 * P * 64 + lane) * 16, wvo1 = wvo0 + P * 1024;
+  // scale copy: lane L -> fragment f0 + (L % 32) / 16, dword L % 16 (lanes 32-63 repeat 0-31)
+  const int svo = ((f0 + ((lane & 31) >> 4)) * P * 64 + 4 * (lane & 15));
 
-  u32x4 wc[NW], sc[NW], wnx[NW], snx[NW];
-  copy_x(0, xl0);
+  u32x4 w0[NW], w1[NW];  // the two weight register sets
+  // stage p's loads into ring slot S: x, weights, scales (LB = 4 + NW + 1 loads)
+  auto batch = [&](int p, auto slot) {
+    constexpr int S = decltype(slot)::value;
+    uint8_t* const xd = S ? xl1 : xl0;
 #pragma unroll
-  for (int i = 0; i < NW; ++i) {
-    wc[i] = wsrc[i][0];
-    sc[i] = ssrc[i][0];
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          xrs, (void __attribute__((address_space(3)))*)(xd + 4 * (wave + 4 * j) * XROW), 16,
+          xvo[j], p * XROW, 0, 0);
+    u32x4* const wd = S ? w1 : w0;
+    wd[0] = __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo0, p * 1024, 0);
+    wd[1] = __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo1, p * 1024, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        srs, (void __attribute__((address_space(3)))*)((S ? sl1 : sl0) + wave * 256), 4, svo,
+        p * 64, 0, 0);
+  };
+  // correction operands b and -128 s of this wave's fragments (groups past G: zero)
+  u32x4 Ab[NW][GJ], As[NW][GJ];
+  auto corr = [&]() {
+#pragma unroll
+    for (int i = 0; i < NW; ++i)
+#pragma unroll
+      for (int jb = 0; jb < GJ; ++jb) {
+        const bool gin = 32 * jb + 8 * c4 < G;
+        const int64_t o = (int64_t)((f0 + i) * 16 + r16) * G + (gin ? 32 * jb + 8 * c4 : 0);
+        Ab[i][jb] = *reinterpret_cast<const u32x4*>(bias + o);
+        As[i][jb] = *reinterpret_cast<const u32x4*>(nsc + o);
+        if (!gin) Ab[i][jb] = As[i][jb] = (u32x4){0u, 0u, 0u, 0u};
+      }
+  };
+
+  if constexpr (XS) {  // the caller's split sums, 3 x 64 rows x G bf16, in 1 KiB copies
+    const __amdgpu_buffer_rsrc_t grs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)xsg, (short)0, 3 * MT * G * 2, 0x00020000);
+    for (int c = wave; c < (3 * MT * G * 2 + 1023) / 1024; c += 4)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          grs, (void __attribute__((address_space(3)))*)(sxb + 1024 * c), 16, 1024 * c + 16 * lane,
+          0, 0, 0);
   }
+  batch(0, std::integral_constant<int, 0>{});
   wait_vm<0>();
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup", "global");
@@ -373,16 +419,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   uint32_t nib = 0x000F000Fu;
   asm volatile("" : "+v"(nib));  // keep the nibble mask in a VGPR
-
-  // stage p from buffer cur; the last stage reloads itself into the idle buffer
-  auto stage = [&](int p, uint8_t* cur, uint8_t* idle) {
-    const int pn = min(p + 1, P - 1);
-    copy_x(pn, idle);
+  float pk[KT];
 #pragma unroll
-    for (int i = 0; i < NW; ++i) {
-      wnx[i] = wsrc[i][pn * 64];
-      snx[i] = ssrc[i][pn * 4];
-    }
+  for (int k = 0; k < KT; ++k) pk[k] = 0.f;
+
+  // Stage p from ring slot S. kind 1: first issue stage p+1's loads into the
+  // other slot; kind 2: issue the correction loads. last: no wait and barrier.
+  auto stage = [&](int p, auto slot, auto kindc, auto lastc) {
+    constexpr int S = decltype(slot)::value, kind = decltype(kindc)::value;
+    constexpr bool last = decltype(lastc)::value;
+    if constexpr (kind == 1) batch(p + 1, std::integral_constant<int, 1 - S>{});
+    if constexpr (kind == 2) corr();
+    __builtin_amdgcn_sched_barrier(0);
+    const uint8_t* const cur = S ? xl1 : xl0;
+    const u32x4* const wc = S ? w1 : w0;
 #pragma unroll
     for (int gl = 0; gl < 2; ++gl) {
       u32x4 X[MW][2];
@@ -390,24 +440,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
       for (int u = 0; u < MW; ++u)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const int row = (wm * MW + u) * 16 + r16;
+          const int row = u * 16 + r16;
           const int ch = 8 * gl + 4 * h + c4;
           X[u][h] = *reinterpret_cast<const u32x4*>(&cur[row * XROW + ((ch ^ r16) << 4)]);
         }
-      // X_g of the row fragments this wave owns (u % WN == wn)
+      if constexpr (!XS) {
+        // X_g of group 2p + gl, rows 16 wave + r16: lane group c4 keeps it when
+        // (2 S + gl) == c4, in the newest shift-register slot
 #pragma unroll
-      for (int u = 0; u < MW; ++u)
-        if (u % WN == wn) {
-          f32x4 a = mfma(ones, X[u][0], zero);
-          a = mfma(ones, X[u][1], a);
-          sx[(2 * p + gl) * MT + (wm * MW + u) * 16 + r16] = a[0];  // the 4 lane groups agree
-        }
+        for (int u = 0; u < MW; ++u)
+          if (u == wave) {
+            f32x4 a = mfma(ones, X[u][0], zero);
+            a = mfma(ones, X[u][1], a);
+            pk[KT - 1] = c4 == 2 * S + gl ? a[0] : pk[KT - 1];
+          }
+      }
 #pragma unroll
       for (int i = 0; i < NW; ++i) {
         const u32x4 A0 = unpack_w(wc[i][2 * gl], nib), A1 = unpack_w(wc[i][2 * gl + 1], nib);
+        const u32x4 sv = *reinterpret_cast<const u32x4*>((S ? sl1 : sl0) + wave * 256 + i * 64 + c4 * 16);
         float s[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) s[r] = gl ? bf_hi(sc[i][r]) : bf_lo(sc[i][r]);
+        for (int r = 0; r < 4; ++r) s[r] = gl ? bf_hi(sv[r]) : bf_lo(sv[r]);
 #pragma unroll
         for (int u = 0; u < MW; ++u) {
           f32x4 a = mfma(A0, X[u][0], zero);
@@ -417,57 +471,86 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         }
       }
     }
-    wait_vm<0>();  // this wave's copies of stage pn (and the next weights) have landed
-    wait_lgkm0();
-#pragma unroll
-    for (int i = 0; i < NW; ++i) {
-      wc[i] = wnx[i];
-      sc[i] = snx[i];
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (!last) {
+      wait_vm<0>();  // this wave's copies of stage p + 1 (and its weights) have landed
+      wait_lgkm0();
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup", "global");
     }
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup", "global");
   };
-  for (int p = 0; p < P; p += 2) {
-    stage(p, xl0, xl1);
-    stage(p + 1, xl1, xl0);
+  // a ring turn is two stages; the shift register moves down one slot per turn
+  auto shift = [&]() {
+#pragma unroll
+    for (int k = 0; k + 1 < KT; ++k) pk[k] = pk[k + 1];
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using K2 = std::integral_constant<int, 2>;
+  using NL = std::false_type;
+  int p = 0;
+#pragma nounroll
+  for (; p < P - 2; p += 2) {
+    if constexpr (!XS) shift();
+    stage(p, S0{}, S1{}, NL{});
+    stage(p + 1, S1{}, S1{}, NL{});
   }
+  if constexpr (!XS) shift();
+  stage(p, S0{}, S1{}, NL{});
+  stage(p + 1, S1{}, K2{}, std::true_type{});
+  wait_vm<0>();
+  wait_lgkm0();
+  if constexpr (!XS) {
+    // turn t (of P / 2) sits in pk[KT - P/2 + t]: group 4t + c4 of rows 16 wave + r16
+    float* const sx = reinterpret_cast<float*>(sxb);
+    const int k0 = KT - P / 2;
+#pragma unroll
+    for (int k = 0; k < KT; ++k)
+      if (k >= k0) sx[(4 * (k - k0) + c4) * MT + wave * 16 + r16] = pk[k];
+  }
+  lds_barrier();
 
   // sum_g (b_g - 128 s_g) X_g, X_g = hi + mid + lo exactly
-  for (int j = 0; j < G; j += 32) {
-    const bool gin = j + 8 * c4 < G;  // G is a multiple of 8
 #pragma unroll
-    for (int u = 0; u < MW; ++u) {
-      const int row = (wm * MW + u) * 16 + r16;
+  for (int u = 0; u < MW; ++u) {
+    const int row = u * 16 + r16;
+#pragma unroll
+    for (int jb = 0; jb < GJ; ++jb) {
+      const bool gin = 32 * jb + 8 * c4 < G;
       u32x4 hi, mid, lo;
+      if constexpr (XS) {
+        const uint16_t* const xsl = reinterpret_cast<const uint16_t*>(sxb);
+        const int o = row * G + (gin ? 32 * jb + 8 * c4 : 0);
+        hi = *reinterpret_cast<const u32x4*>(xsl + o);
+        mid = *reinterpret_cast<const u32x4*>(xsl + MT * G + o);
+        lo = *reinterpret_cast<const u32x4*>(xsl + 2 * MT * G + o);
+        if (!gin) hi = mid = lo = (u32x4){0u, 0u, 0u, 0u};
+      } else {
+        const float* const sx = reinterpret_cast<const float*>(sxb);
 #pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        float v0 = 0.f, v1 = 0.f;
-        if (gin) {
-          v0 = sx[(j + 8 * c4 + e) * MT + row];
-          v1 = sx[(j + 8 * c4 + e + 1) * MT + row];
+        for (int e = 0; e < 8; e += 2) {
+          float v0 = 0.f, v1 = 0.f;
+          if (gin) {
+            v0 = sx[(32 * jb + 8 * c4 + e) * MT + row];
+            v1 = sx[(32 * jb + 8 * c4 + e + 1) * MT + row];
+          }
+          const uint32_t h = f2bf2(v0, v1);
+          const float r0 = v0 - bf_lo(h), r1 = v1 - bf_hi(h);
+          const uint32_t md = f2bf2(r0, r1);
+          hi[e >> 1] = h;
+          mid[e >> 1] = md;
+          lo[e >> 1] = f2bf2(r0 - bf_lo(md), r1 - bf_hi(md));
         }
-        const uint32_t h = f2bf2(v0, v1);
-        const float r0 = v0 - bf_lo(h), r1 = v1 - bf_hi(h);
-        const uint32_t md = f2bf2(r0, r1);
-        hi[e >> 1] = h;
-        mid[e >> 1] = md;
-        lo[e >> 1] = f2bf2(r0 - bf_lo(md), r1 - bf_hi(md));
       }
 #pragma unroll
       for (int i = 0; i < NW; ++i) {
-        const int64_t n = (int64_t)(f0 + i) * 16 + r16;
-        u32x4 Ab = {0u, 0u, 0u, 0u}, As = {0u, 0u, 0u, 0u};
-        if (gin) {
-          Ab = *reinterpret_cast<const u32x4*>(bias + n * G + j + 8 * c4);
-          As = *reinterpret_cast<const u32x4*>(nsc + n * G + j + 8 * c4);
-        }
         f32x4 t = T[i][u];
-        t = mfma(Ab, hi, t);
-        t = mfma(Ab, mid, t);
-        t = mfma(Ab, lo, t);
-        t = mfma(As, hi, t);
-        t = mfma(As, mid, t);
-        t = mfma(As, lo, t);
+        t = mfma(Ab[i][jb], hi, t);
+        t = mfma(Ab[i][jb], mid, t);
+        t = mfma(Ab[i][jb], lo, t);
+        t = mfma(As[i][jb], hi, t);
+        t = mfma(As[i][jb], mid, t);
+        t = mfma(As[i][jb], lo, t);
         T[i][u] = t;
       }
     }
@@ -475,7 +558,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 
 #pragma unroll
   for (int u = 0; u < MW; ++u) {
-    const int m = m0 + (wm * MW + u) * 16 + r16;
+    const int m = u * 16 + r16;
 #pragma unroll
     for (int i = 0; i < NW; ++i) {
       const int n = (f0 + i) * 16 + 4 * c4;
@@ -777,13 +860,11 @@ hipError_t launch_cfg(const QLinearArgs& a) {
   return hipGetLastError();
 }
 
-template <int MW, int NW, int WM, int WN>
-hipError_t launch_wide(const QLinearArgs& a) {
-  constexpr int MT = 16 * MW * WM, NT = 16 * NW * WN;
-  const dim3 grid(a.Npad / NT, (a.M + MT - 1) / MT);
-  hipLaunchKernelGGL((qlinear_wide_kernel<MW, NW, WM, WN>), grid, dim3(256), 0, a.stream, a.x, a.xs,
-                     a.M, a.K, reinterpret_cast<const u32x4*>(a.wp), a.sp, a.bias, a.nsc, a.N,
-                     a.y, a.ys);
+template <int KT, bool XS>
+hipError_t launch_head(const QLinearArgs& a) {
+  hipLaunchKernelGGL((qlinear_head_kernel<KT, XS>), dim3(a.Npad / 128), dim3(256), 0, a.stream, a.x,
+                     a.xs, a.M, a.K, reinterpret_cast<const uint16_t*>(a.wp), a.sp, a.bias, a.nsc,
+                     a.N, a.Npad, a.y, a.ys, a.xsplit);
   return hipGetLastError();
 }
 
@@ -835,8 +916,14 @@ int qlinear_decode_slices(int K, int Npad) {
 // waves spills and takes 182).
 hipError_t launch_qlinear(const QLinearArgs& a) {
   if (a.defer) *a.defer = QPartial{};
-  if (a.M <= 64 && a.Npad >= kWideDecodeN)
-    return a.K % 256 == 0 ? launch_wide<4, 2, 1, 4>(a) : launch_cfg<4, 2, 1, 4>(a);
+  if (a.M <= 64 && a.Npad >= kWideDecodeN) {
+    // buffer offsets of the packed weights are 32-bit; K is a multiple of 512
+    if (a.K % 512 != 0 || a.K > 4096 || (int64_t)a.Npad * a.K / 2 > INT32_MAX)
+      return launch_cfg<4, 2, 1, 4>(a);
+    const bool xs = a.xsplit != nullptr;
+    if (a.K <= 2048) return xs ? launch_head<8, true>(a) : launch_head<8, false>(a);
+    return xs ? launch_head<16, true>(a) : launch_head<16, false>(a);
+  }
   if (a.M <= 64) {
     const int ns = a.part ? qlinear_decode_slices(a.K, a.Npad) : 1;
     const int ksl = a.K / ns;  // K of a slice

@@ -17,6 +17,10 @@ Checks, in order:
   of the exact product plus 2^-20 * mag, >= 99% correctly rounded), and the
   same bar for gdn_qlinear_forward on the same rows (the path that forms the
   sums itself).
+
+The same holds for the lm_head tiles (qlinear_head_kernel<8, true>, layers at
+least 131,072 columns wide), checked on sampled columns of a 131,088-column
+layer at M = 1, 37 and 64.
 """
 import numpy as np
 import pytest
@@ -127,3 +131,40 @@ def test_add_rms_norm_adds_and_checks(gpu):
     odd = torch.zeros((2, 100), dtype=torch.int16, device=gpu)
     with pytest.raises(gdn_amd.GdnError):
         gdn_amd.add_rms_norm(odd, None, dev(w), 1e-6, torch.empty_like(odd))  # hidden % 8
+
+
+@pytest.mark.parametrize("M", [1, 37, 64])
+def test_norm_group_sums_wide_head_matches_oracle(gpu, M):
+    """The lm_head route with the norm's group sums: 131,088 columns (over the
+    131,072 threshold, the last 128-column tile part padding), K = 2048. The
+    oracle checks 1,024 sampled columns, the first and last included (y[:, n]
+    depends only on row n of the weights); both paths meet the qlinear bar,
+    and the padding past N stays unwritten."""
+    import torch
+
+    import gdn_amd
+    K, N, eps = QWEN_HIDDEN, 131072 + 16, 1e-6
+    rng = np.random.default_rng(4500 + M)
+    w = rng.integers(0, 2**32, (N, K // 8), dtype=np.uint32)
+    sc = O.f32_to_bf16((rng.random((N, K // 64)) * 0.004 + 0.001).astype(np.float32))
+    bi = O.f32_to_bf16((rng.standard_normal((N, K // 64)) * 0.03).astype(np.float32))
+    h = O.f32_to_bf16((rng.standard_normal((M, K)) * 1.5).astype(np.float32))
+    nw = O.f32_to_bf16((1 + 0.1 * rng.standard_normal(K)).astype(np.float32))
+    hn = torch.empty((M, K), dtype=torch.int16, device=gpu)
+    gs = torch.full((3, 64, K // 64), -1, dtype=torch.int16, device=gpu)
+    gdn_amd.add_rms_norm(dev(h), None, dev(nw), eps, hn, gs)
+    layer = _layer(K, [(w, sc, bi)])
+    y_xs = torch.full((M, N + 8), -1, dtype=torch.int16, device=gpu)
+    layer.forward_sums(hn, gs, y_xs)
+    y_pl = torch.full((M, N + 8), -1, dtype=torch.int16, device=gpu)
+    layer.forward(hn, y_pl)
+    torch.cuda.synchronize()
+    yx, yp, hn_h = host(y_xs), host(y_pl), host(hn)
+    assert np.all(yx[:, N:] == 0xFFFF) and np.all(yp[:, N:] == 0xFFFF), "columns past N written"
+    cols = np.sort(rng.choice(N, 1024, replace=False))
+    cols[0], cols[-1] = 0, N - 1
+    yr, ye, mag = O.qmatmul_w4(hn_h, w[cols], sc[cols], bi[cols])
+    _check(yx[:, cols], ye, mag, yr, f"lm_head tiles with norm group sums M={M}")
+    _check(yp[:, cols], ye, mag, yr, f"lm_head tiles forming their sums M={M}")
+    say(f"wide M={M}", f"paths bit-identical on {float(np.mean(yx[:, :N] == yp[:, :N])):.5f} of outputs")
+    layer.close()
