@@ -910,10 +910,15 @@ int qlinear_decode_slices(int K, int Npad) {
 // fragments (one row of four waves) took 140 us at M = 64, K = 2048, against
 // 196 us for the decode kernel, 159 us for the 2 x 2 wave grid and 157 us for
 // four column fragments per wave (256 VGPRs, one wave per SIMD). The same tile
-// with x copied by DMA (qlinear_wide_kernel, three waves per SIMD) takes 128-130
-// us timed alone (142.7 for the register-staged form in the same harness;
-// 137 with DMA at two waves per SIMD; the register-staged form forced to three
-// waves spills and takes 182).
+// with x copied by DMA at three waves per SIMD took 128-130 us timed alone
+// (142.7 for the register-staged form in the same harness; 137 with DMA at two
+// waves per SIMD; the register-staged form forced to three waves spills and
+// takes 182). qlinear_head_kernel, the DMA tile with its group sums kept in
+// registers through the K loop and its scales copied by DMA, takes 94-96 us
+// timed alone on weights that stream from HBM (106-112 for the DMA tile that
+// stored the sums to LDS in the loop, on the same boxes), 90 us in the
+// executor's step with the norm's split sums. Loads three stages ahead at two
+// waves per SIMD (108-111 us) and eight-wave groups (104-105 us) were slower.
 hipError_t launch_qlinear(const QLinearArgs& a) {
   if (a.defer) *a.defer = QPartial{};
   if (a.M <= 64 && a.Npad >= kWideDecodeN) {
