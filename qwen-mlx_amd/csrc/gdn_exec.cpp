@@ -28,6 +28,7 @@
 #include <cstdlib>
 #include <cstdio>
 #include <string>
+#include <chrono>
 #include <thread>
 #include <unordered_map>
 #include <unordered_set>
@@ -726,9 +727,11 @@ gdn_status gdn_exec_submit_next(gdn_exec* x, int32_t B) {
   return queue_step(x, B);
 }
 
-// Polls of the pick slot with a pause between them before collect starts to
-// yield the core between polls.
-constexpr uint64_t kCollectSpinPolls = 1 << 16;
+// Time collect polls the pick slot with a pause between polls before it starts
+// to yield the core between them: ten decode steps and more. (Yielding from
+// the first step's worth of polls on made host-fed steps of ~2.2 ms take up to
+// 3.4 ms: a yielding thread can lose its core near the end of the wait.)
+constexpr auto kCollectSpinTime = std::chrono::milliseconds(20);
 
 gdn_status gdn_exec_collect_batch(gdn_exec* x, uint32_t* next_tokens, int32_t B) {
   if (!x || !next_tokens) return efail(GDN_ERR_INVALID, "gdn_exec_collect_batch: NULL argument");
@@ -741,21 +744,24 @@ gdn_status gdn_exec_collect_batch(gdn_exec* x, uint32_t* next_tokens, int32_t B)
   --x->pend_n;
   // The greedy pick writes the step's tokens (>= 0) into the pinned slot, the
   // step's last device work. Poll it, with a pause instruction between polls;
-  // after the first kCollectSpinPolls polls (about a decode step's worth) give
-  // the core up between polls (yield). Every 1024 polls ask the stream for an
-  // error, and a stream that has drained with picks missing is one.
+  // after kCollectSpinTime of polling give the core up between polls (yield).
+  // Every 1024 polls look at the clock and ask the stream for an error, and a
+  // stream that has drained with picks missing is one.
   volatile const int32_t* picks = x->p_next + (size_t)e * x->max_batch;
   auto landed = [&]() {
     for (int b = 0; b < B; ++b)
       if (picks[b] < 0) return false;
     return true;
   };
+  const auto t0 = std::chrono::steady_clock::now();
+  bool yielding = false;
   for (uint64_t spin = 1; !landed(); ++spin) {
-    if (spin < kCollectSpinPolls)
-      __builtin_ia32_pause();
-    else
+    if (yielding)
       std::this_thread::yield();
+    else
+      __builtin_ia32_pause();
     if (spin % 1024 != 0) continue;
+    yielding = yielding || std::chrono::steady_clock::now() - t0 > kCollectSpinTime;
     const hipError_t q = hipStreamQuery(x->stream);
     if (q == hipErrorNotReady) continue;
     if (q != hipSuccess) return hfail(q, "gdn_exec_collect_batch");
