@@ -212,8 +212,9 @@ __global__ __launch_bounds__(256) void prefill_qkv_kernel(
       float ss = 0.f;
 #pragma unroll
       for (int c = 0; c < 8; ++c) ss = fmaf(cv[c], cv[c], ss);
-#pragma unroll
-      for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, 64);
+      // the 16 lanes of the token: DPP adds in xor 1, 2, 4, 8 partner order
+      // (the bits of an xor-shuffle butterfly, without the LDS crossbar)
+      ss = sum16(ss);
       const float rn = 1.0f / sqrtf(ss / (float)kDk + kNormEps);
       const float wn = isq ? kQNormW : kKNormW;
 #pragma unroll
@@ -1159,10 +1160,7 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(
   // lane 2k + 1: rows 16k+8..16k+15 (q = 2, 3)
   float p = sumsq4(bf_lo(yv[0]), bf_hi(yv[0]), bf_lo(yv[1]), bf_hi(yv[1])) +
             sumsq4(bf_lo(yv[2]), bf_hi(yv[2]), bf_lo(yv[3]), bf_hi(yv[3]));
-  p += __shfl_xor(p, 1, 16);
-  p += __shfl_xor(p, 2, 16);
-  p += __shfl_xor(p, 4, 16);
-  p += __shfl_xor(p, 8, 16);
+  p = sum16(p);  // xor 1, 2, 4, 8 partner order on DPP
   *reinterpret_cast<u32x4*>(out + row) = norm_gate8(yv, zv, nw, rms_scale(p, norm_eps));
 }
 
