@@ -234,12 +234,14 @@ gdn_status gdn_prefill_varlen(gdn_pool* pool, int32_t layer, const int32_t* slot
 
 /* gdn_prefill_varlen for callers that cannot allocate device memory (code
  * under HIP graph capture, serving loops that forbid hipMalloc). No
- * counterpart in the reference. Same arguments and results (always the
- * one-group-per-head schedule); the
- * workspace is a fixed 16 MiB array per device held by the library until the
- * process ends, instead of the pool's grown buffer. A call whose workspace
- * (16,576 bytes per token at 16 key / 32 value heads: up to 1012 tokens)
- * exceeds it fails with GDN_ERR_INVALID before any launch. Allocates nothing
+ * counterpart in the reference. Same arguments and results; the workspace
+ * is a fixed 64 MiB array per device held by the library until the process
+ * ends, instead of the pool's grown buffer. The call takes the schedule
+ * gdn_prefill_varlen would take when that schedule's workspace fits, else
+ * the one-group-per-head schedule (both give the same bits). A call whose
+ * workspace on that schedule (16,576 bytes per token at 16 key / 32 value
+ * heads: up to 4,048 tokens) exceeds the array fails with GDN_ERR_INVALID
+ * before any launch. Allocates nothing
  * (hipMalloc, hipFree or otherwise). Every call on a device shares that
  * array: calls that overlap on one device race, so order them on one stream. */
 gdn_status gdn_prefill_varlen_noalloc(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,

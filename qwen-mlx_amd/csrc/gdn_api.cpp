@@ -528,11 +528,17 @@ static gdn_status prefill_common(gdn_pool* pool, int32_t layer, const int32_t* s
   DeviceGuard guard(pool->d.device);
   st = debug_check_slots(pool, slot_ids, nseq, stream, who);
   if (st) return st;
-  // the fixed scratch of the no-allocation entry holds the fused path's workspace only
-  const int waves =
-      noalloc ? 8 : gdn::prefill_chunk_waves(pool->R, pool->d.num_k_heads, nseq, total_tokens);
-  const size_t need = gdn::prefill_workspace_bytes(pool->R, pool->d.num_k_heads, total_tokens, nseq,
-                                                   waves, out && !y);
+  // The no-allocation entry takes the library's schedule when its workspace
+  // fits the fixed scratch, and otherwise the fused schedule, whose workspace
+  // is the smallest.
+  int waves = gdn::prefill_chunk_waves(pool->R, pool->d.num_k_heads, nseq, total_tokens);
+  size_t need = gdn::prefill_workspace_bytes(pool->R, pool->d.num_k_heads, total_tokens, nseq,
+                                             waves, out && !y);
+  if (noalloc && waves != 8 && need > gdn::noalloc_scratch_bytes()) {
+    waves = 8;
+    need = gdn::prefill_workspace_bytes(pool->R, pool->d.num_k_heads, total_tokens, nseq, waves,
+                                        out && !y);
+  }
   void* ws = nullptr;
   size_t ws_bytes = 0;
   if (noalloc) {

@@ -1214,7 +1214,7 @@ size_t prefill_workspace_reserve_bytes(int R, int Hk, int max_tokens) {
 // place of the pool's grown workspace. Every call on a device shares it and
 // finds the previous call's contents (the prefill writes every workspace byte
 // it reads, so nothing needs clearing); calls that overlap on one device race.
-constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 size_t noalloc_scratch_bytes() { return kNoAllocScratchBytes; }

@@ -1,7 +1,8 @@
 """GPU test of gdn_prefill_varlen_noalloc (the prefill with a fixed per-device
 scratch workspace) against gdn_prefill_varlen on twin pools: outputs and the
 slots' recurrent and conv states bit-identical, over two calls in a row, the
-second smaller; oversized calls are refused on the host. The same call
+second smaller, and a 2,048-token prompt on the split schedule; oversized calls
+are refused on the host. The same call
 captured in a HIP graph and replayed gives the eager call's results, and an
 eager call leaves the device's free memory unchanged."""
 import numpy as np
@@ -43,17 +44,25 @@ def test_noalloc_prefill_matches_prefill(gpu):
     st, cs = gen_states(rng, len(slots), HK, HV)
     for pool in pools:
         pool.write(0, _ids(slots), dev(st), dev(cs))
-    # two calls in a row on the same slots, the second smaller
-    for lens in ([70, 300, 5, 129], [33, 2, 64, 1]):
-        say("gdn_prefill_varlen_noalloc", f"lens={lens}")
+    # two calls in a row on the same slots, the second smaller; then one prompt
+    # of 2,048 tokens alone, which takes the split schedule (its records fit the
+    # scratch), continuing slot 9
+    for sl, lens in ((slots, [70, 300, 5, 129]), (slots, [33, 2, 64, 1]), ([9], [2048])):
+        say("gdn_prefill_varlen_noalloc", f"slots={sl} lens={lens}")
         x, ab = gen_tokens(rng, int(sum(lens)), HK, HV)
-        ya, sa, ca = _call(pools[0], False, slots, lens, x, ab, p, gpu)
-        yb, sb, cb = _call(pools[1], True, slots, lens, x, ab, p, gpu)
+        ya, sa, ca = _call(pools[0], False, sl, lens, x, ab, p, gpu)
+        yb, sb, cb = _call(pools[1], True, sl, lens, x, ab, p, gpu)
         assert np.array_equal(ya, yb)
         assert np.array_equal(sa, sb)
         assert np.array_equal(ca, cb)
-    # a call beyond the fixed scratch fails before any launch, changing nothing
-    big = 1013
+    s0 = torch.empty((len(slots), HV, DV, DK), dtype=torch.float32, device=gpu)
+    c0 = torch.empty((len(slots), K - 1, pools[1].D), dtype=torch.int16, device=gpu)
+    pools[1].read(0, _ids(slots), s0, c0)
+    torch.cuda.synchronize()
+    sb, cb = host(s0), host(c0)
+    # a call beyond the fixed scratch (64 MiB: 4,048 tokens at 16/32 heads on the
+    # fused schedule) fails before any launch, changing nothing
+    big = 4049
     x, ab = gen_tokens(rng, big, HK, HV)
     ybig = torch.zeros((big, HV, DV), dtype=torch.int16, device=gpu)
     with pytest.raises(gdn_amd.GdnError, match="scratch"):
