@@ -73,6 +73,10 @@ def parse_args(argv=None):
     ap.add_argument("--placements", default="scattered,contiguous,every8,every16",
                     help="--rmw-probe placements (comma list of scattered, contiguous, "
                          "every8, every16)")
+    ap.add_argument("--copy-floor", action="store_true",
+                    help="only time plain device copies (torch copy_ and the streaming copy "
+                         "kernel of lib/libgdn_probe.so) of the prefill qkv kernel's bytes "
+                         "at --prefill-seqs x --prefill-len tokens; one JSON line")
     ap.add_argument("--rmw-ceiling", action="store_true",
                     help="only time a plain in-place multiply over 30 x 128 MiB buffers "
                          "(the decode's per-launch state bytes, read + write)")
@@ -120,6 +124,66 @@ def copy_calibration(mib: int):
     torch.cuda.synchronize()
     print(json.dumps({"copy_calibration_bytes_read": n * 4, "copy_calibration_bytes_written": n * 4,
                       "launches": 5}), flush=True)
+
+
+# Algorithmic bytes of prefill_qkv_kernel per token (Hk = 16, Hv = 32, d = 128):
+# mixed_qkv row read 16,384 + qn, kn, vc rows written 16,384 + b, a read 128 +
+# beta written 64 + log decay written 128.
+QKV_BYTES_PER_TOKEN = (2 * 16 + 32) * 128 * 2 * 2 + 2 * 32 * 2 + 32 * 2 + 32 * 4  # 33,088
+
+
+def copy_floor(args, reps: int = 5):
+    """The copy rate of the device for the prefill qkv kernel's bytes: half of
+    them copied from one buffer to another (each byte read once and written
+    once), by torch's copy_ (hipMemcpy device to device) and by a plain
+    streaming copy kernel at several grid sizes, with and without nontemporal
+    hints. A kernel that reads and writes the same bytes once takes at least
+    about the best of these times. HIP events on the launch stream."""
+    import ctypes
+
+    import torch
+    lib = ctypes.CDLL(os.path.join(ROOT, "qwen-mlx_amd", "lib", "libgdn_probe.so"))
+    fn = lib.gdn_probe_copy
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                   ctypes.c_void_p]
+    tokens = args.prefill_seqs * args.prefill_len
+    moved = tokens * QKV_BYTES_PER_TOKEN           # bytes read + written
+    half = (moved // 2) // 16 * 16                  # bytes copied
+    src = torch.ones(half // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    stream = torch.cuda.current_stream()
+
+    def timed(launch):
+        for _ in range(2):
+            launch()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            launch()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps
+
+    res = {"torch copy_ (hipMemcpy device to device)": timed(lambda: dst.copy_(src))}
+    for grid in (8192, 16384, 32768, half // 16 // 1024):
+        for nt in (0, 1):
+            def launch(grid=grid, nt=nt):
+                rc = fn(src.data_ptr(), dst.data_ptr(), half, grid, nt, stream.cuda_stream)
+                if rc != 0:
+                    raise RuntimeError(f"gdn_probe_copy returned {rc}")
+            res[f"copy kernel, grid {grid}{', nontemporal' if nt else ''}"] = timed(launch)
+    best = min(res.values())
+    out = {"copy_floor": {
+        "workload": f"prefill qkv bytes of {args.prefill_seqs} x {args.prefill_len} tokens "
+                    f"({QKV_BYTES_PER_TOKEN} B per token), half copied",
+        "bytes_read_plus_written": 2 * half,
+        "us": {k: round(v, 1) for k, v in res.items()},
+        "TBps": {k: round(2 * half / v * 1e-6, 3) for k, v in res.items()},
+        "best_us": round(best, 1),
+        "floor_us_for_qkv_bytes": round(best * moved / (2 * half), 1)}}
+    print(json.dumps(out), flush=True)
+    return 0
 
 
 def rmw_ceiling(layers: int = 30, mib: int = 128, reps: int = 8):
@@ -1091,6 +1155,8 @@ def main(argv=None):
     if args.rmw_ceiling:
         rmw_ceiling()
         return 0
+    if args.copy_floor:
+        return copy_floor(args)
     if args.rmw_probe:
         return rmw_probe(args)
     if args.prefill:

@@ -229,7 +229,9 @@ __global__ __launch_bounds__(256) void prefill_qkv_kernel(
       for (int h = 0; h < 4; ++h) o[h] = f2bf2(cv[2 * h], cv[2 * h + 1]);
       dst = vc + ((size_t)t * Hv + (head - 2 * Hk)) * kDv;
     }
-    if (t < T) reinterpret_cast<uint4*>(dst)[l] = make_uint4(o[0], o[1], o[2], o[3]);
+    // streamed past the caches: the chunk kernel reads the 2 GB of outputs
+    // back from HBM either way
+    if (t < T) __builtin_nontemporal_store(u32x4{o[0], o[1], o[2], o[3]}, reinterpret_cast<u32x4*>(dst) + l);
   }
   if (!isq && !isk && tid < kTT && t0 + tid < T) {
     const int t = t0 + tid, h = head - 2 * Hk;

@@ -1,5 +1,6 @@
-// probe_rmw.hip -- measurement-only kernels behind bench.py --rmw-probe (built
-// into lib/libgdn_probe.so, not part of libgdn's interface).
+// probe_rmw.hip -- measurement-only kernels behind bench.py --rmw-probe and
+// --copy-floor (built into lib/libgdn_probe.so, not part of libgdn's
+// interface).
 //
 // Plain read-modify-write of the decode step's state bytes with no gated delta
 // arithmetic: n slots of slot_bytes each, every byte read and written once per
@@ -22,6 +23,11 @@
 // Every unit index is checked against the unit count and every slot id
 // against num_slots on the host before launch; the kernels index only
 // [pool, pool + num_slots * slot_bytes).
+//
+// gdn_probe_copy: a plain streaming copy (16 bytes per lane, four loads in
+// flight per lane, a grid-stride loop), with or without nontemporal hints: the
+// device's copy rate for a byte count, the floor of a kernel that reads and
+// writes those bytes once (the prefill's qkv kernel).
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -79,7 +85,48 @@ __global__ __launch_bounds__(512) void rmw_items(float* __restrict__ pool, const
   }
 }
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// b[i] = a[i], i < n (16-byte units); every index below n.
+template <bool NT>
+__global__ __launch_bounds__(256) void copy_units(const u32x4* __restrict__ a, u32x4* __restrict__ b,
+                                                  size_t n) {
+  const size_t st = (size_t)gridDim.x * 256;
+  size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  for (; i + 3 * st < n; i += 4 * st) {
+    u32x4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = NT ? __builtin_nontemporal_load(a + i + j * st) : a[i + j * st];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (NT) __builtin_nontemporal_store(v[j], b + i + j * st);
+      else b[i + j * st] = v[j];
+    }
+  }
+  for (; i < n; i += st) b[i] = a[i];
+}
+
 }  // namespace
+
+// Copies `bytes` (a multiple of 16, both pointers 16-byte aligned) from src to
+// dst with `grid` groups of 256 threads (1 .. 2^20); nontemporal != 0 uses
+// nontemporal loads and stores. Returns 0, or a negative value for bad
+// arguments.
+extern "C" int gdn_probe_copy(const void* src, void* dst, int64_t bytes, int grid, int nontemporal,
+                              void* stream) {
+  if (!src || !dst || bytes <= 0 || bytes % 16 != 0) return -1;
+  if ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) % 16 != 0) return -1;
+  if (grid < 1 || grid > (1 << 20)) return -2;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const size_t n = (size_t)bytes / 16;
+  const u32x4* a = static_cast<const u32x4*>(src);
+  u32x4* b = static_cast<u32x4*>(dst);
+  if (nontemporal)
+    hipLaunchKernelGGL((copy_units<true>), dim3(grid), dim3(256), 0, s, a, b, n);
+  else
+    hipLaunchKernelGGL((copy_units<false>), dim3(grid), dim3(256), 0, s, a, b, n);
+  return hipGetLastError() == hipSuccess ? 0 : -8;
+}
 
 // pool: num_slots slots of slot_bytes; ids: n slot ids (device); perm: for
 // shape 1, a permutation of the n * slot_bytes / unit_bytes units (device);
