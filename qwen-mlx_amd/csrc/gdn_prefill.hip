@@ -949,6 +949,32 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
 #pragma unroll
       for (int r = 0; r < 4; ++r) x[I][r] = bt[r] * fmaf(-eg[r], yk[I][r], bf2f((uint16_t)vt[r]));
     }
+    // (f) on the split path, first half: S^T <- exp(G_C) S^T + K^T (exp(G_C -
+    // G) V'), V' hi and lo, for tokens 32p .. 32p + 31 (acc[a] takes p = 0 hi,
+    // lo, then p = 1 hi, lo, as in the fused path's (f)). The p = 0 half goes
+    // out as soon as blocks 0 and 1 of V' are known, so that its MFMAs fill
+    // the dependent chain of blocks 2 and 3: a group of W <= 4 waves has one
+    // wave per SIMD, with nothing else to issue there. (The fused path's two
+    // waves per SIMD already fill it: the same order measured no faster.)
+    auto update_half = [&](int p) {
+      s16x4 h0, l0, h1, l1;
+      const f32x4 d0 = *reinterpret_cast<const f32x4*>(&sm.dec[32 * p + 4 * q]);
+      const f32x4 d1 = *reinterpret_cast<const f32x4*>(&sm.dec[32 * p + 16 + 4 * q]);
+      split4(vf[2 * p] * d0, h0, l0);
+      split4(vf[2 * p + 1] * d1, h1, l1);
+      const bf16x8 vth = cat(h0, h1), vtl = cat(l0, l1);
+      if (p == 0) {
+        const float eC = sm.eG[kC - 1];
+#pragma unroll
+        for (int a = 0; a < 8; ++a) acc[a] *= eC;
+      }
+#pragma unroll
+      for (int a = 0; a < 8; ++a) {
+        const bf16x8 ka = cat(ktr(sm.K, kt, 2 * p, a), ktr(sm.K, kt, 2 * p + 1, a));
+        acc[a] = mfma32(ka, vth, acc[a]);
+        acc[a] = mfma32(ka, vtl, acc[a]);
+      }
+    };
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       s16x4 xh, xl;
@@ -967,6 +993,7 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
         x[J] = mfma32(nl, vpd, x[J]);   // (NLh + NLl) V'h
         x[J] = mfma32(nl, vplz, x[J]);  // NLh V'l
       }
+      if (!FUSED && I == 1) update_half(0);
     }
     if constexpr (FUSED) load_gates(c0 + kC); else load_rec(c0 + kC);
     // GATED: z of this thread's two write-out tokens of this chunk, read here
@@ -1001,27 +1028,31 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
       }
     }
     // (f) S^T <- exp(G_C) S^T + K^T (exp(G_C - G) V'), V' hi and lo
-    bf16x8 vth[2], vtl[2];
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      s16x4 h0, l0, h1, l1;
-      const f32x4 d0 = *reinterpret_cast<const f32x4*>(&sm.dec[32 * p + 4 * q]);
-      const f32x4 d1 = *reinterpret_cast<const f32x4*>(&sm.dec[32 * p + 16 + 4 * q]);
-      split4(vf[2 * p] * d0, h0, l0);
-      split4(vf[2 * p + 1] * d1, h1, l1);
-      vth[p] = cat(h0, h1);
-      vtl[p] = cat(l0, l1);
-    }
-    const float eC = sm.eG[kC - 1];
-#pragma unroll
-    for (int a = 0; a < 8; ++a) {
-      acc[a] *= eC;
+    if constexpr (FUSED) {
+      bf16x8 vth[2], vtl[2];
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        const bf16x8 ka = cat(ktr(sm.K, kt, 2 * p, a), ktr(sm.K, kt, 2 * p + 1, a));
-        acc[a] = mfma32(ka, vth[p], acc[a]);
-        acc[a] = mfma32(ka, vtl[p], acc[a]);
+        s16x4 h0, l0, h1, l1;
+        const f32x4 d0 = *reinterpret_cast<const f32x4*>(&sm.dec[32 * p + 4 * q]);
+        const f32x4 d1 = *reinterpret_cast<const f32x4*>(&sm.dec[32 * p + 16 + 4 * q]);
+        split4(vf[2 * p] * d0, h0, l0);
+        split4(vf[2 * p + 1] * d1, h1, l1);
+        vth[p] = cat(h0, h1);
+        vtl[p] = cat(l0, l1);
       }
+      const float eC = sm.eG[kC - 1];
+#pragma unroll
+      for (int a = 0; a < 8; ++a) {
+        acc[a] *= eC;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const bf16x8 ka = cat(ktr(sm.K, kt, 2 * p, a), ktr(sm.K, kt, 2 * p + 1, a));
+          acc[a] = mfma32(ka, vth[p], acc[a]);
+          acc[a] = mfma32(ka, vtl[p], acc[a]);
+        }
+      }
+    } else {
+      update_half(1);  // second half: tokens 32 .. 63
     }
     __syncthreads();
     // (g) write-out: thread (tokens oi and oi + 32, rows od..od+7) stores 16
