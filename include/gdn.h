@@ -224,7 +224,17 @@ gdn_status gdn_decode_gated(gdn_pool* pool, int32_t layer, const int32_t* slot_i
  * tokens per sequence on average, 262,144 tokens per call), the chunks'
  * state-independent blocks formed for all chunks at once and 2 or 4
  * work-groups per (sequence, value head). The environment variable
- * GDN_PREFILL_WAVES = 8 (the first), 4 or 2 (the second) forces one. */
+ * GDN_PREFILL_WAVES = 8 (the first), 4 or 2 (the second) forces one.
+ * The second schedule, with at least 8,192 tokens in the call, runs as a
+ * pipeline of 2 to 8 token segments (each twice the one before): the next
+ * segment's conv/norm and block-forming kernels go to a second stream that
+ * the pool makes on first use and keeps (default priority, non-blocking),
+ * beside the state products of the segment before on `stream`. The call is
+ * still ordered on `stream` alone (it starts after the work already queued
+ * there, and what is queued there after it waits for all of it) and gives the
+ * same bits as one pass. Not under stream capture, nor in
+ * gdn_prefill_varlen_noalloc; GDN_PREFILL_SEGMENTS = n forces n segments (1:
+ * one pass). */
 gdn_status gdn_prefill_varlen(gdn_pool* pool, int32_t layer, const int32_t* slot_ids,
                               const int32_t* cu_seqlens, int32_t nseq,
                               int32_t total_tokens, const uint16_t* mixed_qkv,

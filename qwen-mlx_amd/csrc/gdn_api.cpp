@@ -78,6 +78,9 @@ struct gdn_pool {
   uint64_t act_gen = 0;  // bumped whenever act is reallocated (captured graphs hold it)
   std::set<int32_t> free_slots;
   std::vector<uint8_t> in_use;
+  // pipelined prefill: a second stream and its events, made on first use
+  hipStream_t aux = nullptr;
+  hipEvent_t pipe_ev[gdn::kPrefillPipeEvents] = {};
 };
 
 namespace {
@@ -92,6 +95,9 @@ void release(gdn_pool* p) {
   if (p->d_status) (void)hipFree(p->d_status);
   if (p->workspace) (void)hipFree(p->workspace);
   if (p->act) (void)hipFree(p->act);
+  for (hipEvent_t e : p->pipe_ev)
+    if (e) (void)hipEventDestroy(e);
+  if (p->aux) (void)hipStreamDestroy(p->aux);
   delete p;
 }
 
@@ -419,6 +425,29 @@ static gdn_status ensure_workspace(gdn_pool* pool, size_t need, void* stream, co
   return ensure_buffer(pool->workspace, pool->workspace_bytes, need, stream, what);
 }
 
+// The pool's second stream and events for a pipelined prefill (default
+// priority, not blocking on the null stream), made once on the pool's device.
+// false when they cannot be made: the call then runs in one pass.
+static bool ensure_pipeline(gdn_pool* pool) {
+  if (pool->aux) return true;
+  hipStream_t s = nullptr;
+  if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  for (hipEvent_t& e : pool->pipe_ev) {
+    if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+      (void)hipGetLastError();
+      for (hipEvent_t& f : pool->pipe_ev)
+        if (f) (void)hipEventDestroy(f), f = nullptr;
+      (void)hipStreamDestroy(s);
+      return false;
+    }
+  }
+  pool->aux = s;
+  return true;
+}
+
 // Shared checks and launch of the fused decode (gdn_decode, gdn_decode_gated).
 static gdn_status decode_common(gdn_pool* pool, int32_t layer, const int32_t* slot_ids, int32_t B,
                                 const uint16_t* qkv, int64_t xstride, const uint16_t* ab,
@@ -583,6 +612,19 @@ static gdn_status prefill_common(gdn_pool* pool, int32_t layer, const int32_t* s
   a.workspace = ws;
   a.workspace_bytes = ws_bytes;
   a.stream = as_stream(stream);
+  // The split path pipelines its segments over a second stream, except under
+  // stream capture and in the no-allocation entry (which makes no objects).
+  if (!noalloc && gdn::prefill_pipeline_segments(waves, total_tokens) > 1) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(a.stream, &cs) != hipSuccess) {
+      (void)hipGetLastError();
+      cs = hipStreamCaptureStatusActive;
+    }
+    if (cs == hipStreamCaptureStatusNone && ensure_pipeline(pool)) {
+      a.aux = pool->aux;
+      a.events = pool->pipe_ev;
+    }
+  }
   hipError_t e = gdn::launch_prefill(a);
   if (e != hipSuccess) return hip_fail(e, who);
   return GDN_OK;

@@ -106,11 +106,13 @@ __device__ __forceinline__ float sigmoid_fast(float x) {
 //     beta = sigmoid(b), lg = log g = -exp(A_log) softplus(a + dt_bias).
 // The 64 + K-1 input rows of the tile are staged in LDS once (one HBM read per
 // element plus a 3-row halo); lane l of a 16-lane group owns channels 8l..8l+7
-// of one token. grid (2Hk+Hv, ceil(T/64)), block 256.
+// of one token. grid (2Hk+Hv, tiles), block 256: token tiles tile0 ..
+// tile0 + tiles - 1 (all ceil(T/64) of them, or one segment of a pipelined
+// call).
 template <int R>
 __global__ __launch_bounds__(256) void prefill_qkv_kernel(
     const uint16_t* __restrict__ conv, const int32_t* __restrict__ slot_ids,
-    const int32_t* __restrict__ cu, int nseq, int num_slots, int Hk, int T,
+    const int32_t* __restrict__ cu, int nseq, int num_slots, int Hk, int T, int tile0,
     const uint16_t* __restrict__ x, int64_t xs, const uint16_t* __restrict__ conv_w,
     const uint16_t* __restrict__ ab, int64_t abs_, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, uint16_t* __restrict__ qn, uint16_t* __restrict__ kn,
@@ -119,7 +121,7 @@ __global__ __launch_bounds__(256) void prefill_qkv_kernel(
   __shared__ uint4 tile[kTT + KH][16];
   __shared__ int tok_st[kTT];    // first token of the token's sequence (clamped <= t)
   __shared__ int tok_slot[kTT];  // slot of that sequence, -1 if invalid
-  const int head = blockIdx.x, t0 = blockIdx.y * kTT;
+  const int head = blockIdx.x, t0 = (blockIdx.y + tile0) * kTT;
   const int Hv = Hk * R;
   const int D = (2 * Hk + Hv) * kDk;
   const int tid = threadIdx.x;
@@ -707,10 +709,15 @@ inline int rec_slots(int T, int nseq) { return T / kC + nseq; }
 // 1D grid of Hv * nseq * (8/W) groups. Work-groups are dealt to the 8 XCDs
 // round-robin; the R * 8/W groups that read one key head's k and q are
 // numbered 8 apart, so they run on one XCD and fetch those rows once.
+//
+// A launch runs the chunks whose last token + 1 lies in (plo, phi] (0 and T:
+// all of them), from the state in the slot and back into it: a pipelined call
+// runs its chunks in several launches, in order, the state between them
+// exact in f32.
 template <int R, bool GATED, int W>
 __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
     float* __restrict__ state, const int32_t* __restrict__ slot_ids,
-    const int32_t* __restrict__ cu, int num_slots, int Hk, int T,
+    const int32_t* __restrict__ cu, int num_slots, int Hk, int T, int plo, int phi,
     const uint16_t* __restrict__ qn, const uint16_t* __restrict__ kn,
     const uint16_t* __restrict__ vc, const float* __restrict__ lgv,
     const uint16_t* __restrict__ betav, const uint16_t* __restrict__ rec, uint16_t* __restrict__ y,
@@ -752,7 +759,12 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
     return;
   }
   const int st = min(max(cu[s], 0), T), en = min(max(cu[s + 1], st), T);
-  if (en <= st) return;
+  if (en <= st || en <= plo || phi <= st) return;
+  // the window's chunks: cb = the first one ending past plo, ce = the end of
+  // the last one ending at or before phi
+  const int cb = plo > st ? st + kC * ((plo - st) / kC) : st;
+  const int ce = en > phi ? st + kC * ((phi - st) / kC) : en;
+  if (ce <= cb) return;
   const int q0 = lane0 >> 4, c0l = lane0 & 15;
   // this lane's state column (accumulator column c = state row dv0 + c)
   float* gstate = state + (size_t)slot * Hv * kTileElems + state_row_offset(hv, dv0 + c0l, Hk, R) + 4 * q0;
@@ -775,8 +787,9 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
   // cycle, and a wave that issues into a full queue stalls, so the four
   // groups go out at four points of the chunk (k in (b), q in (c), v in (d),
   // the gates in (e)). Every read goes through a buffer resource whose size
-  // ends at the chunk's last token (0 past the end of the sequence), so rows
-  // beyond it read 0 without a branch: a load under a branch leaves a merge of
+  // ends at the chunk's last token (0 past the window's last chunk: the
+  // tokens after it may still be in the making), so rows beyond it read 0
+  // without a branch: a load under a branch leaves a merge of
   // its result with the zero of the other path, and the copy that merge needs
   // makes the wave wait for the load right after issuing it instead of one
   // chunk later. Sizes go through readfirstlane: a resource held in VGPRs
@@ -784,7 +797,7 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
   u32x4 kv[UK], qv[UK], vv[UV], rv[UR];
   uint16_t pb = 0;
   float pl = 0.f;
-  auto rows_of = [&](int c) { return __builtin_amdgcn_readfirstlane(max(0, min(kC, en - c))); };
+  auto rows_of = [&](int c) { return __builtin_amdgcn_readfirstlane(max(0, min(kC, ce - c))); };
   // k (KQ = 0) or q (KQ = 1) rows of the chunk at token c
   auto load_kq = [&](int c, auto KQ) {
     const int n = rows_of(c);
@@ -845,11 +858,11 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
   }
   using KLoad = std::integral_constant<int, 0>;
   using QLoad = std::integral_constant<int, 1>;
-  load_kq(st, KLoad{});
-  load_kq(st, QLoad{});
-  load_v(st);
-  if constexpr (FUSED) load_gates(st); else load_rec(st);
-  for (int c0 = st; c0 < en; c0 += kC) {
+  load_kq(cb, KLoad{});
+  load_kq(cb, QLoad{});
+  load_v(cb);
+  if constexpr (FUSED) load_gates(cb); else load_rec(cb);
+  for (int c0 = cb; c0 < ce; c0 += kC) {
     const int n = min(kC, en - c0);
     // Lane-derived values are recomputed in every chunk (a few VALU ops)
     // instead of being held in registers across the loop.
@@ -891,7 +904,7 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
           *static_cast<u32x4*>(__builtin_assume_aligned(reinterpret_cast<char*>(&sm) + roff[j], 16)) = rv[j];
     }
     __syncthreads();
-    load_kq(c0 + kC, KLoad{});  // past the sequence end: no memory access, reads 0
+    load_kq(c0 + kC, KLoad{});  // past the window: no memory access, reads 0
 
     if constexpr (FUSED) {
       // (b) the chunk's matrices: waves 0-3 the diagonal blocks of L and their
@@ -1095,15 +1108,16 @@ struct __attribute__((aligned(16))) FormSmem {
 // Split path, step 1 of 2: for every (chunk, value head) of the call at once,
 // the chunk's blocks of L and P, the inverses D_I and the gates, formed by the
 // same code as in the chunk kernel's step (b), written as the chunk's record
-// (see rec_slot). Item = (record slot x, value head); slots that hold no
-// chunk (see rec_slots) exit. 8 waves: waves 0-3 invert the diagonal blocks,
+// (see rec_slot). Item = (record slot x0 + item / Hv, value head); slots
+// that hold no chunk (see rec_slots), and chunks whose last token + 1 lies
+// outside (plo, phi], exit. 8 waves: waves 0-3 invert the diagonal blocks,
 // waves 4-7 form the other 16. The R heads of one (slot, key head) are
 // numbered 8 apart, so they run on one XCD and share its k and q rows.
 template <int R>
 __global__ __launch_bounds__(512) void prefill_form_kernel(
-    const int32_t* __restrict__ cu, int nseq, int Hk, int T, const uint16_t* __restrict__ qn,
-    const uint16_t* __restrict__ kn, const float* __restrict__ lgv,
-    const uint16_t* __restrict__ betav, uint16_t* __restrict__ rec) {
+    const int32_t* __restrict__ cu, int nseq, int Hk, int T, int x0, int plo, int phi,
+    const uint16_t* __restrict__ qn, const uint16_t* __restrict__ kn,
+    const float* __restrict__ lgv, const uint16_t* __restrict__ betav, uint16_t* __restrict__ rec) {
   constexpr int NT = 512;
   __shared__ FormSmem sm;
   const int Hv = Hk * R;
@@ -1119,7 +1133,7 @@ __global__ __launch_bounds__(512) void prefill_form_kernel(
       r = L % R;
     }
   }
-  const int x = g / Hk, hk = g % Hk, hv = hk * R + r;
+  const int x = x0 + g / Hk, hk = g % Hk, hv = hk * R + r;
   // the sequence of slot x: the largest s with floor(st_s / 64) + s <= x
   int lo = 0, hi = nseq - 1;
   while (lo < hi) {
@@ -1133,6 +1147,7 @@ __global__ __launch_bounds__(512) void prefill_form_kernel(
   const int c0 = st + kC * (x - st / kC - s);
   if (c0 >= en) return;
   const int n = min(kC, en - c0);
+  if (c0 + n <= plo || c0 + n > phi) return;  // another segment's chunk
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q = lane >> 4, c = lane & 15, kf = kseg(c, q);
@@ -1223,6 +1238,21 @@ int prefill_chunk_waves(int R, int Hk, int nseq, int total_tokens) {
   return groups <= 64 ? 2 : groups <= 96 ? 4 : 8;
 }
 
+// The split path leaves CUs idle (one or two 2- or 4-wave groups per CU on
+// half of them), so a call of at least two segments of kPipeSegmentTokens
+// runs its qkv and form kernels one segment ahead on a second stream, beside
+// the chunk kernel of the previous segment. GDN_PREFILL_SEGMENTS = n forces n
+// segments (1: one pass) on the split path.
+constexpr int kPipeSegmentTokens = 4096;
+
+int prefill_pipeline_segments(int waves, int total_tokens) {
+  if (waves != 2 && waves != 4) return 1;
+  const int tiles = (total_tokens + kTT - 1) / kTT;
+  int n = total_tokens / kPipeSegmentTokens;
+  if (const char* v = getenv("GDN_PREFILL_SEGMENTS")) n = atoi(v);
+  return std::max(1, std::min({n, kPrefillPipeSegmentsMax, tiles}));
+}
+
 size_t prefill_workspace_bytes(int R, int Hk, int total_tokens, int nseq, int waves, bool y_scratch) {
   return carve(nullptr, R, Hk, total_tokens, nseq, waves, y_scratch, nullptr);
 }
@@ -1273,27 +1303,107 @@ hipError_t noalloc_scratch(void** out) {
   return hipSuccess;
 }
 
-template <int R, int W>
-static hipError_t launch_split(const PrefillArgs& a, const Workspace& ws) {
-  const int Hv = a.Hk * R;
+// Split path with out: the RMSNormGated epilogue over y.
+static hipError_t launch_split_norm_gate(const PrefillArgs& a, const uint16_t* yb) {
+  const int Hv = a.Hk * a.R;
   const int D = 2 * a.Hk * kDk + Hv * kDv;
-  hipLaunchKernelGGL(prefill_form_kernel<R>, dim3(rec_slots(a.total_tokens, a.nseq) * Hv), dim3(512),
-                     0, a.stream, a.cu_seqlens, a.nseq, a.Hk, a.total_tokens, ws.qn, ws.kn, ws.lg,
-                     ws.beta, ws.rec);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  uint16_t* yb = a.y ? a.y : ws.y;
-  hipLaunchKernelGGL((prefill_chunk_kernel<R, false, W>), dim3(Hv * a.nseq * (8 / W)), dim3(64 * W), 0,
-                     a.stream, a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk, a.total_tokens,
-                     ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, ws.rec, yb, nullptr, a.xstride, nullptr,
-                     0.0f, nullptr, a.status);
-  e = hipGetLastError();
-  if (e != hipSuccess || !a.out) return e;
   const long items = (long)a.total_tokens * Hv;
   hipLaunchKernelGGL(prefill_norm_gate_kernel, dim3((unsigned)((items + 15) / 16)), dim3(256), 0,
                      a.stream, yb, a.mixed + D, a.xstride, a.norm_w, a.norm_eps, a.out,
                      a.total_tokens, Hv);
   return hipGetLastError();
+}
+
+template <int R, int W>
+static hipError_t launch_split(const PrefillArgs& a, const Workspace& ws) {
+  const int Hv = a.Hk * R;
+  hipLaunchKernelGGL(prefill_form_kernel<R>, dim3(rec_slots(a.total_tokens, a.nseq) * Hv), dim3(512),
+                     0, a.stream, a.cu_seqlens, a.nseq, a.Hk, a.total_tokens, 0, 0, a.total_tokens,
+                     ws.qn, ws.kn, ws.lg, ws.beta, ws.rec);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  uint16_t* yb = a.y ? a.y : ws.y;
+  hipLaunchKernelGGL((prefill_chunk_kernel<R, false, W>), dim3(Hv * a.nseq * (8 / W)), dim3(64 * W), 0,
+                     a.stream, a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk, a.total_tokens,
+                     0, a.total_tokens, ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, ws.rec, yb, nullptr,
+                     a.xstride, nullptr, 0.0f, nullptr, a.status);
+  e = hipGetLastError();
+  if (e != hipSuccess || !a.out) return e;
+  return launch_split_norm_gate(a, yb);
+}
+
+// The split path in `segs` segments of whole 64-token tiles, each twice the
+// one before: segment 0 is short, so little of its qkv and form work is
+// exposed, and each later segment's qkv and form kernels (on the second
+// stream) take less time than the chunk kernel of the segment before, beside
+// which they run (one 16,384-token prompt, 4 segments: 0.930 ms per layer
+// with growth 2, 0.937-0.944 with 1.5-1.75 or 2.25, 0.969-0.986 with 3-4,
+// 0.973 with equal segments, 1.022 in one pass). Segment 0's kernels go to the caller's stream (no
+// cross-stream wait ahead of them), and the second stream starts once
+// segment 0's qkv kernel is done (a chunk of segment 1 may begin in segment
+// 0's tokens, and the conv-state update must follow every read of the old
+// rows); segment j >= 1's chunk kernel waits for its qkv and form kernels on
+// the caller's stream. The conv-state update follows the last qkv kernel on
+// the second stream, and the caller's stream waits for it. Every kernel does
+// the same arithmetic as in one pass: the same bits.
+static int pipeline_tile(int tiles, int segs, int j) {
+  // tiles * (2^j - 1) / (2^segs - 1), every segment at least one tile
+  const int t = (int)((int64_t)tiles * ((1 << j) - 1) / ((1 << segs) - 1));
+  return std::min(std::max(t, j), tiles - (segs - j));
+}
+
+template <int R, int W>
+static hipError_t launch_split_pipelined(const PrefillArgs& a, const Workspace& ws, int segs) {
+  const int Hv = a.Hk * R;
+  const int D = 2 * a.Hk * kDk + Hv * kDv;
+  const int T = a.total_tokens, tiles = (T + kTT - 1) / kTT;
+  const int slots = rec_slots(T, a.nseq);
+  uint16_t* yb = a.y ? a.y : ws.y;
+  hipEvent_t* ev = a.events;
+  hipError_t e = hipSuccess;
+  for (int j = 0; j < segs && e == hipSuccess; ++j) {
+    const int t0 = pipeline_tile(tiles, segs, j), t1 = pipeline_tile(tiles, segs, j + 1);
+    const int plo = t0 * kTT, phi = j + 1 == segs ? T : t1 * kTT;
+    hipStream_t sq = j == 0 ? a.stream : a.aux;
+    hipLaunchKernelGGL(prefill_qkv_kernel<R>, dim3(2 * a.Hk + Hv, t1 - t0), dim3(256), 0, sq,
+                       a.conv, a.slot_ids, a.cu_seqlens, a.nseq, a.num_slots, a.Hk, T, t0, a.mixed,
+                       a.xstride, a.conv_w, a.ab, a.ab_stride, a.A_log, a.dt_bias, ws.qn, ws.kn,
+                       ws.vc, ws.beta, ws.lg);
+    if (j == 0) {  // the second stream starts after segment 0's qkv kernel
+      e = hipGetLastError();
+      if (e == hipSuccess) e = hipEventRecord(ev[0], a.stream);
+      if (e == hipSuccess) e = hipStreamWaitEvent(a.aux, ev[0], 0);
+      if (e != hipSuccess) break;
+    }
+    // record slots of the chunks ending in (plo, phi]: the chunk starts lie
+    // in (plo - 64, phi), slot = floor(start / 64) + its sequence
+    const int x0 = plo >= kTT ? (plo - kTT + 1) / kTT : 0;
+    const int x1 = std::min(slots, (phi - 1) / kTT + a.nseq);
+    if (x1 > x0)
+      hipLaunchKernelGGL(prefill_form_kernel<R>, dim3((x1 - x0) * Hv), dim3(512), 0, sq,
+                         a.cu_seqlens, a.nseq, a.Hk, T, x0, plo, phi, ws.qn, ws.kn, ws.lg, ws.beta,
+                         ws.rec);
+    e = hipGetLastError();
+    if (j > 0) {
+      if (e == hipSuccess) e = hipEventRecord(ev[1 + j], a.aux);
+      if (e == hipSuccess) e = hipStreamWaitEvent(a.stream, ev[1 + j], 0);
+    }
+    if (e != hipSuccess) break;
+    hipLaunchKernelGGL((prefill_chunk_kernel<R, false, W>), dim3(Hv * a.nseq * (8 / W)), dim3(64 * W),
+                       0, a.stream, a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk, T, plo,
+                       phi, ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, ws.rec, yb, nullptr, a.xstride,
+                       nullptr, 0.0f, nullptr, a.status);
+    e = hipGetLastError();
+  }
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(prefill_conv_state_kernel, dim3(a.nseq, (D + 255) / 256), dim3(256), 0, a.aux,
+                     a.conv, a.slot_ids, a.cu_seqlens, a.nseq, a.num_slots, D, T, a.mixed, a.xstride,
+                     a.status);
+  e = hipGetLastError();
+  if (e == hipSuccess) e = hipEventRecord(ev[1 + segs], a.aux);
+  if (e == hipSuccess) e = hipStreamWaitEvent(a.stream, ev[1 + segs], 0);
+  if (e != hipSuccess || !a.out) return e;
+  return launch_split_norm_gate(a, yb);
 }
 
 template <int R>
@@ -1302,10 +1412,15 @@ static hipError_t launch_prefill_r(const PrefillArgs& a) {
   const int D = 2 * a.Hk * kDk + Hv * kDv;
   Workspace ws;
   carve(a.workspace, R, a.Hk, a.total_tokens, a.nseq, a.waves, a.out && !a.y, &ws);
+  const int segs = a.aux && a.events ? prefill_pipeline_segments(a.waves, a.total_tokens) : 1;
+  if (segs > 1) {
+    if (a.waves == 2) return launch_split_pipelined<R, 2>(a, ws, segs);
+    return launch_split_pipelined<R, 4>(a, ws, segs);
+  }
   if (a.total_tokens > 0) {
     hipLaunchKernelGGL(prefill_qkv_kernel<R>, dim3(2 * a.Hk + Hv, (a.total_tokens + kTT - 1) / kTT),
                        dim3(256), 0, a.stream, a.conv, a.slot_ids, a.cu_seqlens, a.nseq,
-                       a.num_slots, a.Hk, a.total_tokens, a.mixed, a.xstride, a.conv_w, a.ab,
+                       a.num_slots, a.Hk, a.total_tokens, 0, a.mixed, a.xstride, a.conv_w, a.ab,
                        a.ab_stride, a.A_log,
                        a.dt_bias, ws.qn, ws.kn, ws.vc, ws.beta, ws.lg);
     hipError_t e = hipGetLastError();
@@ -1321,14 +1436,14 @@ static hipError_t launch_prefill_r(const PrefillArgs& a) {
   const int units = Hv * a.nseq;
   if (a.out)
     hipLaunchKernelGGL((prefill_chunk_kernel<R, true, 8>), dim3(units), dim3(512), 0, a.stream,
-                       a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk, a.total_tokens,
-                       ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, nullptr, a.y, a.mixed + D, a.xstride,
-                       a.norm_w, a.norm_eps, a.out, a.status);
+                       a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk, a.total_tokens, 0,
+                       a.total_tokens, ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, nullptr, a.y,
+                       a.mixed + D, a.xstride, a.norm_w, a.norm_eps, a.out, a.status);
   else
     hipLaunchKernelGGL((prefill_chunk_kernel<R, false, 8>), dim3(units), dim3(512), 0, a.stream,
-                       a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk, a.total_tokens,
-                       ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, nullptr, a.y, nullptr, a.xstride, nullptr,
-                       0.0f, nullptr, a.status);
+                       a.state, a.slot_ids, a.cu_seqlens, a.num_slots, a.Hk, a.total_tokens, 0,
+                       a.total_tokens, ws.qn, ws.kn, ws.vc, ws.lg, ws.beta, nullptr, a.y, nullptr,
+                       a.xstride, nullptr, 0.0f, nullptr, a.status);
   return hipGetLastError();
 }
 

@@ -10,6 +10,7 @@
 // tested here.
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cstdlib>
 #include <functional>
 #include <vector>
@@ -20,6 +21,7 @@
 namespace gdn_fake {
 bool fail_embed = false;  // set by the test: embedding launches fail
 bool capture = false;     // set by the test: stream capture records the stand-in launches
+bool split = false;       // set by the test: prefill calls take the split path (2-wave groups)
 int graphs_live = 0, graphs_destroyed = 0, graphs_made = 0;
 std::vector<std::function<void()>>* recording = nullptr;  // the capture in progress
 }
@@ -80,6 +82,10 @@ hipError_t hipStreamDestroy(hipStream_t stream) {
 hipError_t hipStreamBeginCapture(hipStream_t, hipStreamCaptureMode) {
   if (!gdn_fake::capture) return hipErrorNotSupported;
   gdn_fake::recording = new std::vector<std::function<void()>>();
+  return hipSuccess;
+}
+hipError_t hipStreamIsCapturing(hipStream_t, hipStreamCaptureStatus* status) {
+  *status = gdn_fake::recording ? hipStreamCaptureStatusActive : hipStreamCaptureStatusNone;
   return hipSuccess;
 }
 hipError_t hipStreamEndCapture(hipStream_t, hipGraph_t* graph) {
@@ -149,7 +155,10 @@ hipError_t launch_decode(const DecodeArgs&) { return hipSuccess; }
 hipError_t launch_recurrent(const RecurrentArgs&) { return hipSuccess; }
 hipError_t launch_slots(const SlotArgs&) { return hipSuccess; }
 hipError_t launch_validate(const int32_t*, int, int, uint32_t*, hipStream_t) { return hipSuccess; }
-int prefill_chunk_waves(int, int, int, int) { return 8; }
+int prefill_chunk_waves(int, int, int, int) { return gdn_fake::split ? 2 : 8; }
+int prefill_pipeline_segments(int waves, int total_tokens) {
+  return (waves == 2 || waves == 4) && total_tokens >= 8192 ? std::min(8, total_tokens / 4096) : 1;
+}
 size_t prefill_workspace_bytes(int R, int Hk, int T, int nseq, int waves, bool y_scratch) {
   const size_t Hv = (size_t)Hk * R;
   size_t b = (size_t)T * (2 * (size_t)Hk * kDk * 2 + Hv * kDv * 2 + Hv * 6) + 5 * 256;

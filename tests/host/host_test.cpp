@@ -13,6 +13,7 @@
 namespace gdn_fake {
 extern bool fail_embed;  // fake_hip.cpp: the next embedding launches fail
 extern bool capture;     // fake_hip.cpp: stream capture makes (empty) graphs
+extern bool split;       // fake_hip.cpp: prefill calls take the split path
 extern int graphs_live, graphs_destroyed, graphs_made;
 }
 
@@ -101,6 +102,18 @@ static int test_pool() {
   ids[1] = 3;
   CHECK(gdn_prefill_varlen(pool, 0, ids, cu, 2, 900, xp, abp, al, dt, cw, yp, nullptr) ==
         GDN_ERR_SLOTS);
+  // a long split-path call pipelines over the pool's second stream (made on
+  // the first such call, reused by the next, released with the pool); the
+  // no-allocation form never makes it
+  ids[1] = 4;
+  gdn_fake::split = true;
+  cu[1] = 4000; cu[2] = 9000;
+  uint16_t* xl = dev_alloc<uint16_t>(keep, (size_t)9000 * D);
+  uint16_t* abl = dev_alloc<uint16_t>(keep, (size_t)9000 * 64);
+  uint16_t* yl = dev_alloc<uint16_t>(keep, (size_t)9000 * 32 * 128);
+  for (int k = 0; k < 2; ++k)
+    CHECK(gdn_prefill_varlen(pool, 0, ids, cu, 2, 9000, xl, abl, al, dt, cw, yl, nullptr) == GDN_OK);
+  gdn_fake::split = false;
   uint32_t flags = 1;
   CHECK(gdn_pool_check(pool, nullptr, &flags) == GDN_OK && flags == 0);
   CHECK(gdn_pool_destroy(pool) == GDN_OK);

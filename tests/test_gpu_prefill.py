@@ -314,3 +314,103 @@ def test_prefill_split_path_matches_fused(gpu, prefill_waves, Hk, Hv):
         worst_s = max(worst_s, rel_l2(s2[i], sr))
     say("split path |dy|", worst_y, "state relL2", worst_s)
     assert worst_y <= Y_TOL and worst_s <= STATE_TOL
+
+
+@pytest.fixture
+def prefill_segments(monkeypatch):
+    """Force the split path's pipeline: GDN_PREFILL_SEGMENTS = n segments (1:
+    one pass); 0 leaves the choice to the library."""
+    def force(n):
+        if n:
+            monkeypatch.setenv("GDN_PREFILL_SEGMENTS", str(n))
+        else:
+            monkeypatch.delenv("GDN_PREFILL_SEGMENTS", raising=False)
+    return force
+
+
+@pytest.mark.parametrize("Hk,Hv", [(16, 32), (4, 16)])
+@pytest.mark.parametrize("waves", [2, 4])
+def test_prefill_pipelined_segments_match_one_pass(gpu, prefill_waves, prefill_segments, Hk, Hv,
+                                                   waves):
+    """The split path run as a pipeline of token segments (qkv and form
+    kernels of segment j + 1 on a second stream beside the chunk kernel of
+    segment j, the state carried through the slot between the chunk kernel's
+    launches) gives the bits of the one-pass call and of the fused path: y,
+    state, conv window and the gated output. Segment counts 3 and 8 over
+    sequences that start and end mid-way through 64-token tiles, an empty
+    and a one-token sequence; states start nonzero."""
+    import gdn_amd
+    import torch
+    lens = [700, 0, 1, 64, 129, 333, 5000]
+    say("gdn_prefill_varlen pipelined", f"lens={lens} Hk={Hk} Hv={Hv} waves={waves}")
+    rng = np.random.default_rng(590 + Hk + Hv + waves)
+    n, D = len(lens), conv_dim(Hk, Hv)
+    p = gen_layer_params(rng, Hk, Hv)
+    st0, cs0 = gen_states(rng, n, Hk, Hv, state_std=0.05)
+    T = sum(lens)
+    mixed, ab = gen_tokens(rng, T, Hk, Hv)
+    z = O.f32_to_bf16(rng.standard_normal((T, Hv * DV)).astype(np.float32))
+    norm_w = O.f32_to_bf16((1.0 + 0.1 * rng.standard_normal(DV)).astype(np.float32))
+    qkvz = np.zeros((T, D + Hv * DV), np.uint16)
+    qkvz[:, :D] = mixed
+    qkvz[:, D:] = z
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    slots = rng.permutation(n + 2)[:n].astype(np.int32)
+    ids = _ids(slots)
+    args = (dev(p["A_log"]), dev(p["dt_bias"]), dev(p["conv_w"]))
+    res = {}
+    for w, segs in ((8, 1), (waves, 1), (waves, 3), (waves, 8)):
+        prefill_waves(w)
+        prefill_segments(segs)
+        pool = gdn_amd.Pool(1, n + 2, Hk, Hv)
+        pool.write(0, ids, dev(st0), dev(cs0))
+        y = torch.zeros((T, Hv, DV), dtype=torch.int16, device=gpu)
+        pool.prefill(0, ids, dev(cu), T, dev(mixed), dev(ab), *args, y)
+        s, c = _read(pool, 0, slots, gpu)
+        gpool = gdn_amd.Pool(1, n + 2, Hk, Hv)
+        gpool.write(0, ids, dev(st0), dev(cs0))
+        out = torch.zeros((T, Hv, DV), dtype=torch.int16, device=gpu)
+        gpool.prefill_gated(0, ids, dev(cu), T, dev(qkvz), dev(ab), *args, dev(norm_w), 1e-6, out)
+        gs, gc = _read(gpool, 0, slots, gpu)
+        assert pool.check() == 0 and gpool.check() == 0
+        assert np.array_equal(s, gs) and np.array_equal(c, gc)
+        res[(w, segs)] = (host(y), s, c, host(out))
+        pool.close()
+        gpool.close()
+    ref = res[(8, 1)]
+    for key, got in res.items():
+        for a, b, what in zip(ref, got, ("y", "state", "conv", "gated out")):
+            assert np.array_equal(a, b), f"waves, segments = {key}: {what} differs from the fused path"
+
+
+def test_prefill_one_long_prompt_pipelined_matches_one_pass(gpu, prefill_segments):
+    """One 16,384-token prompt takes the split path in 4 segments by default;
+    its y, state and conv window equal the one-pass call's bit for bit, and a
+    second call on the same pool (reusing its stream and events) gives the
+    same bits again."""
+    import gdn_amd
+    import torch
+    Hk, Hv, L = 16, 32, 16384
+    say("gdn_prefill_varlen one long prompt, pipelined", f"L={L}")
+    rng = np.random.default_rng(620)
+    p = gen_layer_params(rng, Hk, Hv)
+    st0, cs0 = gen_states(rng, 1, Hk, Hv, state_std=0.05)
+    mixed, ab = gen_tokens(rng, L, Hk, Hv)
+    cu = dev(np.asarray([0, L], np.int32))
+    ids = _ids([1])
+    args = (dev(mixed), dev(ab), dev(p["A_log"]), dev(p["dt_bias"]), dev(p["conv_w"]))
+    res = []
+    for segs in (1, 0, 0):
+        prefill_segments(segs)
+        pool = gdn_amd.Pool(1, 2, Hk, Hv)
+        for _ in range(2 if segs == 0 else 1):
+            pool.write(0, ids, dev(st0), dev(cs0))
+            y = torch.zeros((L, Hv, DV), dtype=torch.int16, device=gpu)
+            pool.prefill(0, ids, cu, L, *args, y)
+            s, c = _read(pool, 0, [1], gpu)
+            res.append((host(y), s, c))
+        assert pool.check() == 0
+        pool.close()
+    for got in res[1:]:
+        for a, b, what in zip(res[0], got, ("y", "state", "conv")):
+            assert np.array_equal(a, b), f"pipelined call: {what} differs from one pass"
