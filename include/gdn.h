@@ -225,8 +225,10 @@ gdn_status gdn_decode_gated(gdn_pool* pool, int32_t layer, const int32_t* slot_i
  * state-independent blocks formed for all chunks at once and 2 or 4
  * work-groups per (sequence, value head). The environment variable
  * GDN_PREFILL_WAVES = 8 (the first), 4 or 2 (the second) forces one.
- * The second schedule, with at least 8,192 tokens in the call, runs as a
- * pipeline of 2 to 8 token segments (each twice the one before): the next
+ * The second schedule, with at least 8,192 tokens in the call and at most
+ * half as many work-groups as the device has CUs (one 16,384-token prompt at
+ * 32 value heads: 128), runs as a pipeline of 2 to 8 token segments (each
+ * twice the one before): the next
  * segment's conv/norm and block-forming kernels go to a second stream that
  * the pool makes on first use and keeps (default priority, non-blocking),
  * beside the state products of the segment before on `stream`. The call is

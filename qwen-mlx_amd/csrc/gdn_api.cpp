@@ -78,6 +78,7 @@ struct gdn_pool {
   uint64_t act_gen = 0;  // bumped whenever act is reallocated (captured graphs hold it)
   std::set<int32_t> free_slots;
   std::vector<uint8_t> in_use;
+  int cus = 0;  // compute units of the pool's device
   // pipelined prefill: a second stream and its events, made on first use
   hipStream_t aux = nullptr;
   hipEvent_t pipe_ev[gdn::kPrefillPipeEvents] = {};
@@ -189,6 +190,10 @@ gdn_status gdn_pool_create(const gdn_pool_desc* desc, gdn_pool** out) {
   gdn_pool* p = new gdn_pool();
   p->d = d;
   p->R = R;
+  if (hipDeviceGetAttribute(&p->cus, hipDeviceAttributeMultiprocessorCount, d.device) != hipSuccess) {
+    (void)hipGetLastError();
+    p->cus = 0;  // unknown: no pipelined prefill
+  }
   p->D = 2 * d.num_k_heads * gdn::kDk + d.num_v_heads * gdn::kDv;
   p->state_elems = (size_t)d.num_v_heads * gdn::kTileElems;
   p->conv_elems = (size_t)(gdn::kConvK - 1) * p->D;
@@ -614,7 +619,9 @@ static gdn_status prefill_common(gdn_pool* pool, int32_t layer, const int32_t* s
   a.stream = as_stream(stream);
   // The split path pipelines its segments over a second stream, except under
   // stream capture and in the no-allocation entry (which makes no objects).
-  if (!noalloc && gdn::prefill_pipeline_segments(waves, total_tokens) > 1) {
+  const int groups = pool->d.num_v_heads * nseq * (waves ? 8 / waves : 1);
+  const int segs = gdn::prefill_pipeline_segments(waves, total_tokens, groups, pool->cus);
+  if (!noalloc && segs > 1) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(a.stream, &cs) != hipSuccess) {
       (void)hipGetLastError();
@@ -623,6 +630,7 @@ static gdn_status prefill_common(gdn_pool* pool, int32_t layer, const int32_t* s
     if (cs == hipStreamCaptureStatusNone && ensure_pipeline(pool)) {
       a.aux = pool->aux;
       a.events = pool->pipe_ev;
+      a.segments = segs;
     }
   }
   hipError_t e = gdn::launch_prefill(a);

@@ -204,10 +204,12 @@ struct PrefillArgs {
   void* workspace;       // device scratch sized by prefill_workspace_bytes
   size_t workspace_bytes;
   hipStream_t stream;
-  // Pipelined split path (prefill_pipeline_segments > 1): a second stream of
-  // the caller's device and kPrefillPipeEvents events; null: one pass.
+  // Pipelined split path: `segments` (> 1) token segments over a second
+  // stream of the caller's device with kPrefillPipeEvents events; aux null:
+  // one pass.
   hipStream_t aux;
   hipEvent_t* events;
+  int segments;
 };
 constexpr int kPrefillPipeSegmentsMax = 8;
 constexpr int kPrefillPipeEvents = kPrefillPipeSegmentsMax + 2;
@@ -264,9 +266,10 @@ hipError_t launch_slots(const SlotArgs& a);
 hipError_t launch_validate(const int32_t* slot_ids, int n, int num_slots, uint32_t* status,
                            hipStream_t stream);
 int prefill_chunk_waves(int R, int Hk, int nseq, int total_tokens);
-// Segments of a pipelined prefill call on the path `waves` picked (1: one
+// Segments of a pipelined prefill call on the path `waves` picked, whose
+// chunk kernel has `groups` work-groups, on a device of `cus` CUs (1: one
 // pass, no second stream).
-int prefill_pipeline_segments(int waves, int total_tokens);
+int prefill_pipeline_segments(int waves, int total_tokens, int groups, int cus);
 size_t prefill_workspace_bytes(int R, int Hk, int total_tokens, int nseq, int waves, bool y_scratch);
 size_t prefill_workspace_reserve_bytes(int R, int Hk, int max_tokens);
 // Fixed per-device workspace of gdn_prefill_varlen_noalloc (gdn_prefill.hip).

@@ -61,6 +61,10 @@ hipError_t hipGetDevice(int* id) {
   *id = 0;
   return hipSuccess;
 }
+hipError_t hipDeviceGetAttribute(int* value, hipDeviceAttribute_t attr, int) {
+  *value = attr == hipDeviceAttributeMultiprocessorCount ? 256 : 0;
+  return hipSuccess;
+}
 hipError_t hipGetDeviceCount(int* count) {
   *count = 1;
   return hipSuccess;
@@ -156,8 +160,10 @@ hipError_t launch_recurrent(const RecurrentArgs&) { return hipSuccess; }
 hipError_t launch_slots(const SlotArgs&) { return hipSuccess; }
 hipError_t launch_validate(const int32_t*, int, int, uint32_t*, hipStream_t) { return hipSuccess; }
 int prefill_chunk_waves(int, int, int, int) { return gdn_fake::split ? 2 : 8; }
-int prefill_pipeline_segments(int waves, int total_tokens) {
-  return (waves == 2 || waves == 4) && total_tokens >= 8192 ? std::min(8, total_tokens / 4096) : 1;
+int prefill_pipeline_segments(int waves, int total_tokens, int groups, int cus) {
+  return (waves == 2 || waves == 4) && 2 * groups <= cus && total_tokens >= 8192
+             ? std::min(8, total_tokens / 4096)
+             : 1;
 }
 size_t prefill_workspace_bytes(int R, int Hk, int T, int nseq, int waves, bool y_scratch) {
   const size_t Hv = (size_t)Hk * R;

@@ -102,17 +102,19 @@ static int test_pool() {
   ids[1] = 3;
   CHECK(gdn_prefill_varlen(pool, 0, ids, cu, 2, 900, xp, abp, al, dt, cw, yp, nullptr) ==
         GDN_ERR_SLOTS);
-  // a long split-path call pipelines over the pool's second stream (made on
-  // the first such call, reused by the next, released with the pool); the
-  // no-allocation form never makes it
+  // a long one-prompt split-path call (128 groups on 256 CUs) pipelines over
+  // the pool's second stream (made on the first such call, reused by the
+  // next, released with the pool); two prompts (256 groups) run in one pass
   ids[1] = 4;
   gdn_fake::split = true;
-  cu[1] = 4000; cu[2] = 9000;
+  cu[1] = 9000; cu[2] = 9000;
   uint16_t* xl = dev_alloc<uint16_t>(keep, (size_t)9000 * D);
   uint16_t* abl = dev_alloc<uint16_t>(keep, (size_t)9000 * 64);
   uint16_t* yl = dev_alloc<uint16_t>(keep, (size_t)9000 * 32 * 128);
   for (int k = 0; k < 2; ++k)
-    CHECK(gdn_prefill_varlen(pool, 0, ids, cu, 2, 9000, xl, abl, al, dt, cw, yl, nullptr) == GDN_OK);
+    CHECK(gdn_prefill_varlen(pool, 0, ids, cu, 1, 9000, xl, abl, al, dt, cw, yl, nullptr) == GDN_OK);
+  cu[1] = 4000;
+  CHECK(gdn_prefill_varlen(pool, 0, ids, cu, 2, 9000, xl, abl, al, dt, cw, yl, nullptr) == GDN_OK);
   gdn_fake::split = false;
   uint32_t flags = 1;
   CHECK(gdn_pool_check(pool, nullptr, &flags) == GDN_OK && flags == 0);
