@@ -1244,13 +1244,15 @@ int prefill_chunk_waves(int R, int Hk, int nseq, int total_tokens) {
 // ahead on a second stream, beside the chunk kernel of the previous segment.
 // With more groups the chunk kernel's next launch waits for CUs that the
 // other stream's groups hold (measured for two prompts at 256 groups: 1.82
-// against 1.23 ms per layer), so those calls run in one pass.
+// against 1.23 ms per layer), so those calls run in one pass. Only 2-wave
+// groups are pipelined by default: two prompts forced onto 128 4-wave groups
+// measured 1.87 ms pipelined against 1.24 in one pass.
 // GDN_PREFILL_SEGMENTS = n forces n segments (1: one pass) on the split path.
 constexpr int kPipeSegmentTokens = 4096;
 
 int prefill_pipeline_segments(int waves, int total_tokens, int groups, int cus) {
   if (waves != 2 && waves != 4) return 1;
-  if (2 * (int64_t)groups > cus && !getenv("GDN_PREFILL_SEGMENTS")) return 1;
+  if ((waves != 2 || 2 * (int64_t)groups > cus) && !getenv("GDN_PREFILL_SEGMENTS")) return 1;
   const int tiles = (total_tokens + kTT - 1) / kTT;
   int n = total_tokens / kPipeSegmentTokens;
   if (const char* v = getenv("GDN_PREFILL_SEGMENTS")) n = atoi(v);

@@ -161,7 +161,7 @@ hipError_t launch_slots(const SlotArgs&) { return hipSuccess; }
 hipError_t launch_validate(const int32_t*, int, int, uint32_t*, hipStream_t) { return hipSuccess; }
 int prefill_chunk_waves(int, int, int, int) { return gdn_fake::split ? 2 : 8; }
 int prefill_pipeline_segments(int waves, int total_tokens, int groups, int cus) {
-  return (waves == 2 || waves == 4) && 2 * groups <= cus && total_tokens >= 8192
+  return waves == 2 && 2 * groups <= cus && total_tokens >= 8192
              ? std::min(8, total_tokens / 4096)
              : 1;
 }
