@@ -19,6 +19,7 @@ baseline (the oracle's C restatement of the reference step, OpenMP).
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -351,11 +352,14 @@ def prefill_measure(L, n, P, seed=0, reps=1):
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(reps)]
     torch.cuda.synchronize()
+    gc.collect()
+    gc.disable()  # no collector pause inside the timed region
     t0 = time.perf_counter()
     for e in ev:
         run_layers(e)
     torch.cuda.synchronize()
     elapsed = (time.perf_counter() - t0) / reps
+    gc.enable()
     gpu_s = sum(a.elapsed_time(b) for a, b in ev) * 1e-3 / reps
     flags = pool.check()
     pool.close()
@@ -702,11 +706,20 @@ def exec_measure(args, steps, warmup, components=False):
     for _ in range(warmup):
         cur = ex.decode_batch(ids, cur)
     torch.cuda.synchronize()
+    # Python's cyclic garbage collector can stop the host loop for tens of ms
+    # (measured: one step of 40-65 ms in some runs, the median 2.17 ms); the
+    # timed loops run with it off
+    gc.collect()
+    gc.disable()
+    fed_steps = []
     t0 = time.perf_counter()
     for _ in range(steps):
+        ts = time.perf_counter()
         ex.submit_batch(ids, cur)
         cur = ex.collect_batch(B)
+        fed_steps.append(time.perf_counter() - ts)
     fed_elapsed = time.perf_counter() - t0
+    fed_steps.sort()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     ex.submit_batch(ids, cur)
@@ -715,6 +728,7 @@ def exec_measure(args, steps, warmup, components=False):
         cur = ex.collect_batch(B)
     cur = ex.collect_batch(B)
     elapsed = time.perf_counter() - t0
+    gc.enable()
     flags = pool.check()
     if flags:
         print(f"pool status flags 0x{flags:x}", file=sys.stderr)
@@ -737,6 +751,7 @@ def exec_measure(args, steps, warmup, components=False):
     kv_bytes = NA * B * (P + warmup + steps / 2) * ATT_HKV * ATT_HD * 2 * 2
     step_bytes = B * L * STATE_BYTES + wbytes + int(kv_bytes)
     return dict(tokens_per_s=B * steps / elapsed, ms=ms, fed_ms=fed_elapsed / steps * 1e3,
+                fed_median_ms=fed_steps[len(fed_steps) // 2] * 1e3, fed_max_ms=fed_steps[-1] * 1e3,
                 pre_one=pre_one, pre_batched=pre_batched, g=g, NA=NA, step_bytes=step_bytes,
                 gbs=step_bytes / (ms * 1e-3) / 1e9, components=comp)
 
@@ -756,6 +771,8 @@ def exec_summary(args):
         "tokens_per_s": round(r["tokens_per_s"], 1),
         "ms_per_step_chained": round(r["ms"], 4),
         "ms_per_step_host_fed": round(r["fed_ms"], 4),
+        "host_fed_step_median_ms": round(r["fed_median_ms"], 4),
+        "host_fed_step_max_ms": round(r["fed_max_ms"], 4),
         "steps": args.exec_steps,
         "kernel_avg_us": r["components"],
         "kernel_timing": "HIP events around HIP-graph replays of each kind of call over all "
@@ -799,6 +816,8 @@ def exec_bench(args):
                    "layers": L, "attention_layers": NA, "batch": B, "slots": args.slots,
                    "hidden": QL_HIDDEN, "vocab": V, "prompt_tokens": P},
         "host_fed_ms_per_step": round(r["fed_ms"], 4),
+        "host_fed_step_median_ms": round(r["fed_median_ms"], 4),
+        "host_fed_step_max_ms": round(r["fed_max_ms"], 4),
         "timing": "wall clock over the steps, each queued on the previous step's device picks "
                   "(gdn_exec_submit_next) and collected after; host_fed_ms_per_step: submit + "
                   "collect per step, the picks through the host",
@@ -1176,11 +1195,14 @@ def main(argv=None):
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(args.steps)]
     torch.cuda.synchronize()
+    gc.collect()
+    gc.disable()  # no collector pause inside the timed region
     t0 = time.perf_counter()
     for i in range(args.steps):
         w.step(ev[i])
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    gc.enable()
     tok_s = args.batch * args.steps / elapsed
     avg_ms = sum(a.elapsed_time(b) for a, b in ev) / (args.steps * args.layers)
     launch_bytes = args.batch * STATE_BYTES
