@@ -1401,13 +1401,17 @@ static hipError_t launch_split_pipelined(const PrefillArgs& a, const Workspace& 
                        nullptr, 0.0f, nullptr, a.status);
     e = hipGetLastError();
   }
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(prefill_conv_state_kernel, dim3(a.nseq, (D + 255) / 256), dim3(256), 0, a.aux,
-                     a.conv, a.slot_ids, a.cu_seqlens, a.nseq, a.num_slots, D, T, a.mixed, a.xstride,
-                     a.status);
-  e = hipGetLastError();
-  if (e == hipSuccess) e = hipEventRecord(ev[1 + segs], a.aux);
-  if (e == hipSuccess) e = hipStreamWaitEvent(a.stream, ev[1 + segs], 0);
+  if (e == hipSuccess) {
+    hipLaunchKernelGGL(prefill_conv_state_kernel, dim3(a.nseq, (D + 255) / 256), dim3(256), 0,
+                       a.aux, a.conv, a.slot_ids, a.cu_seqlens, a.nseq, a.num_slots, D, T, a.mixed,
+                       a.xstride, a.status);
+    e = hipGetLastError();
+  }
+  // the caller's stream waits for the second stream's work, also after an
+  // error, so that no later call on the pool overlaps what was queued there
+  hipError_t j = hipEventRecord(ev[1 + segs], a.aux);
+  if (j == hipSuccess) j = hipStreamWaitEvent(a.stream, ev[1 + segs], 0);
+  if (e == hipSuccess) e = j;
   if (e != hipSuccess || !a.out) return e;
   return launch_split_norm_gate(a, yb);
 }
