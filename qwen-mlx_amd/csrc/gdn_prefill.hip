@@ -1344,14 +1344,15 @@ static hipError_t launch_split(const PrefillArgs& a, const Workspace& ws) {
 // stream) take less time than the chunk kernel of the segment before, beside
 // which they run (one 16,384-token prompt, 4 segments: 0.930 ms per layer
 // with growth 2, 0.937-0.944 with 1.5-1.75 or 2.25, 0.969-0.986 with 3-4,
-// 0.973 with equal segments, 1.022 in one pass). Segment 0's kernels go to the caller's stream (no
-// cross-stream wait ahead of them), and the second stream starts once
-// segment 0's qkv kernel is done (a chunk of segment 1 may begin in segment
-// 0's tokens, and the conv-state update must follow every read of the old
-// rows); segment j >= 1's chunk kernel waits for its qkv and form kernels on
-// the caller's stream. The conv-state update follows the last qkv kernel on
-// the second stream, and the caller's stream waits for it. Every kernel does
-// the same arithmetic as in one pass: the same bits.
+// 0.973 with equal segments, 1.022 in one pass).
+// Segment 0's kernels go to the caller's stream (no cross-stream wait ahead
+// of them), and the second stream starts once segment 0's qkv kernel is done
+// (a chunk of segment 1 may begin in segment 0's tokens, and the conv-state
+// update must follow every read of the old rows); segment j >= 1's chunk
+// kernel waits for its qkv and form kernels on the caller's stream. The
+// conv-state update follows the last qkv kernel on the second stream, and the
+// caller's stream waits for it. Every kernel does the same arithmetic as in
+// one pass: the same bits.
 static int pipeline_tile(int tiles, int segs, int j) {
   // tiles * (2^j - 1) / (2^segs - 1), every segment at least one tile
   const int t = (int)((int64_t)tiles * ((1 << j) - 1) / ((1 << segs) - 1));
