@@ -858,6 +858,44 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
   }
   using KLoad = std::integral_constant<int, 0>;
   using QLoad = std::integral_constant<int, 1>;
+  // Split path: a chunk's outputs (step (e)) are formed during the next
+  // chunk's products, where a wave alone on its SIMD has issue slots to
+  // spare, from the chunk's Zt, V'h, P fragments and exp(G) kept in
+  // registers, and written out after that chunk's closing barrier; the last
+  // chunk's after the loop. The same products in the same order: the same
+  // bits.
+  f32x4 ztp[FUSED ? 1 : 4];   // Zt of the previous chunk
+  s16x4 vpp[FUSED ? 1 : 4];   // its V'h
+  bf16x8 ppp[FUSED ? 1 : 6];  // its P fragments: rows 16I + c, pairs p <= I / 2
+  float egp[FUSED ? 1 : 4];   // exp(G) of its tokens 16I + c
+  int cp = -1, np = 0;        // its first token and rows (cp < 0: none yet)
+  auto out_prev = [&]() {
+    int k = 0;
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      f32x4 o = ztp[I] * egp[I];
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        if (2 * p > I) continue;
+        o = mfma32(cat(vpp[2 * p], vpp[2 * p + 1]), ppp[k++], o);
+      }
+      *reinterpret_cast<uint2*>(&sm.Y[16 * I + c0l][dv0 + 4 * q0]) =
+          make_uint2(f2bf2(o[0], o[1]), f2bf2(o[2], o[3]));
+    }
+  };
+  // write-out of the chunk at token cx (rows nx) from the LDS rows of y:
+  // thread (tokens oi and oi + 32, rows od..od+7), 16 bytes of y per token
+  auto write_out = [&](int cx, int nx) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int i = oi + 32 * h;
+      if (i >= nx) continue;
+      const uint2 ya = *reinterpret_cast<const uint2*>(&sm.Y[i][od]);
+      const uint2 yb = *reinterpret_cast<const uint2*>(&sm.Y[i][od + 4]);
+      *reinterpret_cast<uint4*>(y + ((size_t)(cx + i) * Hv + hv) * kDv + od) =
+          make_uint4(ya.x, ya.y, yb.x, yb.y);
+    }
+  };
   load_kq(cb, KLoad{});
   load_kq(cb, QLoad{});
   load_v(cb);
@@ -905,6 +943,8 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
     }
     __syncthreads();
     load_kq(c0 + kC, KLoad{});  // past the window: no memory access, reads 0
+    if constexpr (!FUSED)
+      if (cp >= 0) out_prev();  // the previous chunk's outputs into the LDS rows of y
 
     if constexpr (FUSED) {
       // (b) the chunk's matrices: waves 0-3 the diagonal blocks of L and their
@@ -1022,9 +1062,22 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
       }
     }
     // (e) O^T_I = exp(G) Zt_I + V'^T P^T: rows dv0 + 4q + r, token 16I + c
-    // y (bf16) into the LDS rows; with GATED each wave's sum of y^2 per token
+    // y (bf16) into the LDS rows; with GATED each wave's sum of y^2 per token.
+    // The split path keeps its operands for the next chunk instead.
+    if constexpr (!FUSED) {
+      int k = 0;
 #pragma unroll
-    for (int I = 0; I < 4; ++I) {
+      for (int I = 0; I < 4; ++I) {
+        ztp[I] = zt[I];
+        vpp[I] = vph[I];
+        egp[I] = sm.eG[16 * I + c];
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+          if (2 * p <= I) ppp[k++] = lds8(&sm.P[16 * I + c][32 * p + qs]);
+      }
+    }
+#pragma unroll
+    for (int I = 0; I < (FUSED ? 4 : 0); ++I) {
       f32x4 o = zt[I] * sm.eG[16 * I + c];
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
@@ -1068,11 +1121,16 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
       update_half(1);  // second half: tokens 32 .. 63
     }
     __syncthreads();
+    if constexpr (!FUSED) {  // (g) of the previous chunk, whose rows out_prev formed
+      if (cp >= 0) write_out(cp, np);
+      cp = c0;
+      np = n;
+    }
     // (g) write-out: thread (tokens oi and oi + 32, rows od..od+7) stores 16
     // bytes of y per token; GATED: out = silu(z) * bf16(w * bf16(y * rn)), rn
     // from the 8 waves' sums of y^2
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < (FUSED ? 2 : 0); ++h) {
       const int i = oi + 32 * h;
       if (i >= n) continue;
       const uint2 ya = *reinterpret_cast<const uint2*>(&sm.Y[i][od]);
@@ -1088,6 +1146,12 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
         *reinterpret_cast<u32x4*>(out + row) = o;
       }
     }
+  }
+  if constexpr (!FUSED) {  // the last chunk's outputs
+    __syncthreads();  // every wave's reads of the LDS rows of y are done
+    out_prev();
+    __syncthreads();
+    write_out(cp, np);
   }
 #pragma unroll
   for (int a = 0; a < 8; ++a)
