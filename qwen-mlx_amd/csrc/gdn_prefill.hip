@@ -858,16 +858,18 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
   }
   using KLoad = std::integral_constant<int, 0>;
   using QLoad = std::integral_constant<int, 1>;
-  // Split path: a chunk's outputs (step (e)) are formed during the next
-  // chunk's products, where a wave alone on its SIMD has issue slots to
-  // spare, from the chunk's Zt, V'h, P fragments and exp(G) kept in
-  // registers, and written out after that chunk's closing barrier; the last
-  // chunk's after the loop. The same products in the same order: the same
-  // bits.
-  f32x4 ztp[FUSED ? 1 : 4];   // Zt of the previous chunk
-  s16x4 vpp[FUSED ? 1 : 4];   // its V'h
-  bf16x8 ppp[FUSED ? 1 : 6];  // its P fragments: rows 16I + c, pairs p <= I / 2
-  float egp[FUSED ? 1 : 4];   // exp(G) of its tokens 16I + c
+  // Without the gated epilogue a chunk's outputs (step (e)) are formed during
+  // the next chunk's products, where the SIMDs have issue slots to spare
+  // (most on the split path, one wave per SIMD), from the chunk's Zt, V'h, P
+  // fragments and exp(G) kept in registers, and written out after that
+  // chunk's closing barrier; the last chunk's after the loop. The same
+  // products in the same order: the same bits. (The gated epilogue also
+  // needs every wave's sums of y^2 and z: it stays in its own chunk.)
+  constexpr bool DEFER = !GATED;
+  f32x4 ztp[DEFER ? 4 : 1];   // Zt of the previous chunk
+  s16x4 vpp[DEFER ? 4 : 1];   // its V'h
+  bf16x8 ppp[DEFER ? 6 : 1];  // its P fragments: rows 16I + c, pairs p <= I / 2
+  float egp[DEFER ? 4 : 1];   // exp(G) of its tokens 16I + c
   int cp = -1, np = 0;        // its first token and rows (cp < 0: none yet)
   auto out_prev = [&]() {
     int k = 0;
@@ -943,7 +945,7 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
     }
     __syncthreads();
     load_kq(c0 + kC, KLoad{});  // past the window: no memory access, reads 0
-    if constexpr (!FUSED)
+    if constexpr (DEFER)
       if (cp >= 0) out_prev();  // the previous chunk's outputs into the LDS rows of y
 
     if constexpr (FUSED) {
@@ -1063,8 +1065,8 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
     }
     // (e) O^T_I = exp(G) Zt_I + V'^T P^T: rows dv0 + 4q + r, token 16I + c
     // y (bf16) into the LDS rows; with GATED each wave's sum of y^2 per token.
-    // The split path keeps its operands for the next chunk instead.
-    if constexpr (!FUSED) {
+    // Without GATED the operands are kept for the next chunk instead.
+    if constexpr (DEFER) {
       int k = 0;
 #pragma unroll
       for (int I = 0; I < 4; ++I) {
@@ -1077,7 +1079,7 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
       }
     }
 #pragma unroll
-    for (int I = 0; I < (FUSED ? 4 : 0); ++I) {
+    for (int I = 0; I < (DEFER ? 0 : 4); ++I) {
       f32x4 o = zt[I] * sm.eG[16 * I + c];
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
@@ -1121,8 +1123,8 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
       update_half(1);  // second half: tokens 32 .. 63
     }
     __syncthreads();
-    if constexpr (!FUSED) {  // (g) of the previous chunk, whose rows out_prev formed
-      if (cp >= 0) write_out(cp, np);
+    if constexpr (DEFER) {  // (g) of the previous chunk, whose rows out_prev formed
+      if (cp >= 0 && y != nullptr) write_out(cp, np);
       cp = c0;
       np = n;
     }
@@ -1130,7 +1132,7 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
     // bytes of y per token; GATED: out = silu(z) * bf16(w * bf16(y * rn)), rn
     // from the 8 waves' sums of y^2
 #pragma unroll
-    for (int h = 0; h < (FUSED ? 2 : 0); ++h) {
+    for (int h = 0; h < (DEFER ? 0 : 2); ++h) {
       const int i = oi + 32 * h;
       if (i >= n) continue;
       const uint2 ya = *reinterpret_cast<const uint2*>(&sm.Y[i][od]);
@@ -1147,11 +1149,11 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
       }
     }
   }
-  if constexpr (!FUSED) {  // the last chunk's outputs
+  if constexpr (DEFER) {  // the last chunk's outputs
     __syncthreads();  // every wave's reads of the LDS rows of y are done
     out_prev();
     __syncthreads();
-    write_out(cp, np);
+    if (y != nullptr) write_out(cp, np);
   }
 #pragma unroll
   for (int a = 0; a < 8; ++a)
