@@ -357,6 +357,9 @@ __device__ __forceinline__ int qrow(int e) { return 2 * (e >> 5) + ((e >> 3) & 1
 __device__ __forceinline__ int qunit(int e) { return (e & 7) + 8 * ((e >> 4) & 1); }
 
 struct __attribute__((aligned(16))) ChunkSmem {
+  static constexpr int kNLRow0 = 0;   // first row of -L held (see nl_row)
+  static constexpr int kLdV = kLdQ;   // row strides of V and Y
+  static constexpr int kLdY = kDv + 4;
   uint16_t K[4 * kKBlk];       // k, natural dk order, segments swizzled (kseg)
   uint16_t Q[kC][kLdQ];        // q, dk in pair order: 32b + 16h + 4m + u at 32b + 8m + 4h + u
   uint16_t P[kC][kLdP];        // P, token columns in pair order; blocks above the diagonal stay 0
@@ -364,13 +367,42 @@ struct __attribute__((aligned(16))) ChunkSmem {
   uint16_t D[4 * kLdDB];       // D_I, rows of kLdD, hi/lo interleaved per 4 columns
   float Ld[4 * kLdLB];         // diagonal blocks of L (f32): row i, column 4m + p at 4p + m
   float beta[kC], G[kC], eG[kC], dec[kC];  // G: cumulative log2 decay
-  uint16_t V[kC][kLdQ];        // v rows (row stride 288 B: the transposing reads of 8
+  uint16_t V[kC][kLdV];        // v rows (row stride 288 B: the transposing reads of 8
                                // consecutive rows x 32 bytes hit distinct banks)
-  uint16_t Y[kC][kDv + 4];     // the chunk's outputs y (bf16), written out as whole rows; the
+  uint16_t Y[kC][kLdY];        // the chunk's outputs y (bf16), written out as whole rows; the
                                // 66-dword stride puts the 16 rows of an 8-byte write pass and
                                // the 2 rows of an 8-byte read pass in distinct banks
   float ysq[kC][8];            // gated epilogue: per token, each wave's sum of y^2
 };
+
+// LDS of the split path's chunk kernel (W waves, 16W state rows): what the
+// chain needs, about 77 KB at W = 2, so that a form-kernel group fits beside
+// it on a CU. Block row 0 of -L has no block left of the diagonal, so -L
+// starts at row 16; v and y hold the group's 16W columns (relative to its
+// first state row). Row strides: v 32W + 32 bytes, so the transposing reads
+// of 8 consecutive rows x 32 bytes still hit distinct banks; y 32W + 8 bytes,
+// so the 16 rows of an 8-byte write pass of the O tiles do. No diagonal-block
+// scratch, no G, no gated-epilogue sums.
+template <int W>
+struct __attribute__((aligned(16))) SplitSmem {
+  static constexpr int kNLRow0 = 16;
+  static constexpr int kLdV = 16 * W + 16;
+  static constexpr int kLdY = 16 * W + 4;
+  uint16_t K[4 * kKBlk];
+  uint16_t Q[kC][kLdQ];
+  uint16_t P[kC][kLdP];
+  uint16_t NL[kC - 16][kLdN];
+  uint16_t D[4 * kLdDB];
+  float beta[kC], eG[kC], dec[kC];
+  uint16_t V[kC][kLdV];
+  uint16_t Y[kC][kLdY];
+};
+
+// Row `row` of -L (row >= S::kNLRow0)
+template <class S>
+__device__ __forceinline__ uint16_t* nl_row(S& sm, int row) { return sm.NL[row - S::kNLRow0]; }
+template <class S>
+__device__ __forceinline__ const uint16_t* nl_row(const S& sm, int row) { return sm.NL[row - S::kNLRow0]; }
 
 // DPP move of a float (lanes without a source read 0)
 template <int CTRL, int ROW_MASK>
@@ -429,7 +461,8 @@ __device__ __forceinline__ s16x4 ktr(const uint16_t* K, int kt, int blk, int a) 
 // v operand of the solve, a transposing read like ktr: lane (q, c) passes
 // row 16I + 4q + (c >> 2) and column dv0 + 4(c & 3) and receives
 // V[16I + 4q + u][dv0 + c], u = 0..3.
-__device__ __forceinline__ s16x4 vtr(const ChunkSmem& sm, int row, int col) {
+template <class S>
+__device__ __forceinline__ s16x4 vtr(const S& sm, int row, int col) {
   lds_bf16x4* p = (lds_bf16x4*)&sm.V[row][col];
   return __builtin_bit_cast(s16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(p));
 }
@@ -473,7 +506,7 @@ __device__ __forceinline__ void put_l(S& sm, const f32x4& t, int I, int J, int q
   } else {
     s16x4 h, l;
     split4(-lv, h, l);
-    *reinterpret_cast<bf16x8*>(&sm.NL[i][32 * J + 8 * (q ^ gsw(c))]) = cat(h, l);
+    *reinterpret_cast<bf16x8*>(nl_row(sm, i) + 32 * J + 8 * (q ^ gsw(c))) = cat(h, l);
   }
 }
 // P block (I, J), J <= I: row 16I+c, columns 16J+4q..+3 at their pair-order place.
@@ -645,7 +678,7 @@ __device__ __forceinline__ void* rec_slot(S& sm, int u) {
       row = 48 + r;
       g = off - 12 * r;
     }
-    return &sm.NL[row][8 * (g ^ gsw(row))];
+    return nl_row(sm, row) + 8 * (g ^ gsw(row));
   }
   if (u < 640) {
     const int v = u - 384;
@@ -731,7 +764,7 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
   constexpr int UV = 2;                         // 16-byte v units per thread (2W per row)
   constexpr int UR = (kRecUnits + NT - 1) / NT; // 16-byte record units per thread
   constexpr int M = R * (8 / W);                // groups per (sequence, key head)
-  __shared__ ChunkSmem sm;
+  __shared__ std::conditional_t<FUSED, ChunkSmem, SplitSmem<W>> sm;
   const int Hv = Hk * R;
   int hv, s, split;
   {
@@ -881,7 +914,7 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
         if (2 * p > I) continue;
         o = mfma32(cat(vpp[2 * p], vpp[2 * p + 1]), ppp[k++], o);
       }
-      *reinterpret_cast<uint2*>(&sm.Y[16 * I + c0l][dv0 + 4 * q0]) =
+      *reinterpret_cast<uint2*>(&sm.Y[16 * I + c0l][16 * w + 4 * q0]) =
           make_uint2(f2bf2(o[0], o[1]), f2bf2(o[2], o[3]));
     }
   };
@@ -892,8 +925,8 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
     for (int h = 0; h < 2; ++h) {
       const int i = oi + 32 * h;
       if (i >= nx) continue;
-      const uint2 ya = *reinterpret_cast<const uint2*>(&sm.Y[i][od]);
-      const uint2 yb = *reinterpret_cast<const uint2*>(&sm.Y[i][od + 4]);
+      const uint2 ya = *reinterpret_cast<const uint2*>(&sm.Y[i][od - dvb]);
+      const uint2 yb = *reinterpret_cast<const uint2*>(&sm.Y[i][od - dvb + 4]);
       *reinterpret_cast<uint4*>(y + ((size_t)(cx + i) * Hv + hv) * kDv + od) =
           make_uint4(ya.x, ya.y, yb.x, yb.y);
     }
@@ -933,7 +966,7 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
 #pragma unroll
     for (int u = 0; u < UV; ++u) {
       const int e = tid + NT * u, i = e / (2 * W), m = e % (2 * W);
-      *static_cast<u32x4*>(__builtin_assume_aligned(&sm.V[i][dvb + 8 * m], 16)) = vv[u];
+      *static_cast<u32x4*>(__builtin_assume_aligned(&sm.V[i][8 * m], 16)) = vv[u];
     }
     if constexpr (FUSED) {
       if (w == 0) form_gates(sm, pb, pl, lane0);
@@ -1000,7 +1033,7 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
       const f32x4 eg = *reinterpret_cast<const f32x4*>(&sm.eG[16 * I + 4 * q]);
       // v of tokens 16I + 4q + r, state row dv0 + c (a transposing read: lane
       // 4u + s of each 16-lane group reads row 4q + u, columns 4s..4s+3)
-      const s16x4 vt = vtr(sm, 16 * I + 4 * q + (c >> 2), dv0 + 4 * (c & 3));
+      const s16x4 vt = vtr(sm, 16 * I + 4 * q + (c >> 2), 16 * w + 4 * (c & 3));
 #pragma unroll
       for (int r = 0; r < 4; ++r) x[I][r] = bt[r] * fmaf(-eg[r], yk[I][r], bf2f((uint16_t)vt[r]));
     }
@@ -1044,7 +1077,7 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
       const bf16x8 vpd = cat(vph[I], vph[I]), vplz = cat(vl, kZero4);
 #pragma unroll
       for (int J = I + 1; J < 4; ++J) {
-        const bf16x8 nl = lds8(&sm.NL[16 * J + c][32 * I + qs]);  // -L_JI hi | lo
+        const bf16x8 nl = lds8(nl_row(sm, 16 * J + c) + 32 * I + qs);  // -L_JI hi | lo
         x[J] = mfma32(nl, vpd, x[J]);   // (NLh + NLl) V'h
         x[J] = mfma32(nl, vplz, x[J]);  // NLh V'l
       }
@@ -1087,7 +1120,7 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
         o = mfma32(cat(vph[2 * p], vph[2 * p + 1]), lds8(&sm.P[16 * I + c][32 * p + qs]), o);
       }
       const uint2 yb = make_uint2(f2bf2(o[0], o[1]), f2bf2(o[2], o[3]));
-      *reinterpret_cast<uint2*>(&sm.Y[16 * I + c][dv0 + 4 * q]) = yb;
+      *reinterpret_cast<uint2*>(&sm.Y[16 * I + c][16 * w + 4 * q]) = yb;
       if constexpr (GATED) {
         float ss = sumsq4(bf_lo(yb.x), bf_hi(yb.x), bf_lo(yb.y), bf_hi(yb.y));
         ss += __shfl_xor(ss, 16, 64);
@@ -1135,8 +1168,8 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
     for (int h = 0; h < (DEFER ? 0 : 2); ++h) {
       const int i = oi + 32 * h;
       if (i >= n) continue;
-      const uint2 ya = *reinterpret_cast<const uint2*>(&sm.Y[i][od]);
-      const uint2 yb = *reinterpret_cast<const uint2*>(&sm.Y[i][od + 4]);
+      const uint2 ya = *reinterpret_cast<const uint2*>(&sm.Y[i][od - dvb]);
+      const uint2 yb = *reinterpret_cast<const uint2*>(&sm.Y[i][od - dvb + 4]);
       const uint4 yv = make_uint4(ya.x, ya.y, yb.x, yb.y);
       const size_t row = ((size_t)(c0 + i) * Hv + hv) * kDv + od;
       if (y != nullptr) *reinterpret_cast<uint4*>(y + row) = yv;
@@ -1162,10 +1195,11 @@ __global__ __launch_bounds__(64 * W) void prefill_chunk_kernel(
 
 // Shared memory of prefill_form_kernel: the block-forming part of ChunkSmem.
 struct __attribute__((aligned(16))) FormSmem {
+  static constexpr int kNLRow0 = 16;  // block row 0 of -L holds no record block
   uint16_t K[4 * kKBlk];
   uint16_t Q[kC][kLdQ];
   uint16_t P[kC][kLdP];
-  uint16_t NL[kC][kLdN];
+  uint16_t NL[kC - 16][kLdN];
   uint16_t D[4 * kLdDB];
   float Ld[4 * kLdLB];
   float beta[kC], G[kC], eG[kC], dec[kC];
