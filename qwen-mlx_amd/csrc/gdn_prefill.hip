@@ -357,13 +357,13 @@ __device__ __forceinline__ int qrow(int e) { return 2 * (e >> 5) + ((e >> 3) & 1
 __device__ __forceinline__ int qunit(int e) { return (e & 7) + 8 * ((e >> 4) & 1); }
 
 struct __attribute__((aligned(16))) ChunkSmem {
-  static constexpr int kNLRow0 = 0;   // first row of -L held (see nl_row)
+  static constexpr int kNLRow0 = 16;  // block row 0 of -L has no block left of the diagonal
   static constexpr int kLdV = kLdQ;   // row strides of V and Y
   static constexpr int kLdY = kDv + 4;
   uint16_t K[4 * kKBlk];       // k, natural dk order, segments swizzled (kseg)
   uint16_t Q[kC][kLdQ];        // q, dk in pair order: 32b + 16h + 4m + u at 32b + 8m + 4h + u
   uint16_t P[kC][kLdP];        // P, token columns in pair order; blocks above the diagonal stay 0
-  uint16_t NL[kC][kLdN];       // -L, hi/lo interleaved per 4 columns
+  uint16_t NL[kC - 16][kLdN];  // -L rows 16..63, hi/lo interleaved per 4 columns
   uint16_t D[4 * kLdDB];       // D_I, rows of kLdD, hi/lo interleaved per 4 columns
   float Ld[4 * kLdLB];         // diagonal blocks of L (f32): row i, column 4m + p at 4p + m
   float beta[kC], G[kC], eG[kC], dec[kC];  // G: cumulative log2 decay
