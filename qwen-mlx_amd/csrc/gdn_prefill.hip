@@ -1342,11 +1342,10 @@ int prefill_chunk_waves(int R, int Hk, int nseq, int total_tokens) {
 // groups, one per CU, number at most half the CUs), a call of at least two
 // segments of kPipeSegmentTokens runs its qkv and form kernels one segment
 // ahead on a second stream, beside the chunk kernel of the previous segment.
-// With more groups the chunk kernel's next launch waits for CUs that the
-// other stream's groups hold (measured for two prompts at 256 groups: 1.82
-// against 1.23 ms per layer), so those calls run in one pass. Only 2-wave
-// groups are pipelined by default: two prompts forced onto 128 4-wave groups
-// measured 1.87 ms pipelined against 1.24 in one pass.
+// Calls of several prompts run in one pass: segments cut the packed tokens,
+// so a later prompt falls wholly into the last segments and its chain starts
+// only after the first prompt's (two prompts at 256 2-wave groups: 1.72-1.75
+// against 1.19 ms per layer; at 128 4-wave groups 1.68-1.72).
 // GDN_PREFILL_SEGMENTS = n forces n segments (1: one pass) on the split path.
 constexpr int kPipeSegmentTokens = 4096;
 
