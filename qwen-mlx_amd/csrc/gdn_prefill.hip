@@ -1342,10 +1342,11 @@ int prefill_chunk_waves(int R, int Hk, int nseq, int total_tokens) {
 // groups, one per CU, number at most half the CUs), a call of at least two
 // segments of kPipeSegmentTokens runs its qkv and form kernels one segment
 // ahead on a second stream, beside the chunk kernel of the previous segment.
-// Calls of several prompts run in one pass: segments cut the packed tokens,
-// so a later prompt falls wholly into the last segments and its chain starts
-// only after the first prompt's (two prompts at 256 2-wave groups: 1.72-1.75
-// against 1.19 ms per layer; at 128 4-wave groups 1.68-1.72).
+// At 32 value heads that admits one prompt. Pipelining several long prompts
+// loses: segments cut the packed tokens, so a later prompt falls wholly into
+// the last segments and its chain starts only after the first prompt's (two
+// 16,384-token prompts forced into segments: 1.72-1.75 ms per layer at 256
+// 2-wave groups, 1.68-1.72 at 128 4-wave groups, against 1.19 in one pass).
 // GDN_PREFILL_SEGMENTS = n forces n segments (1: one pass) on the split path.
 constexpr int kPipeSegmentTokens = 4096;
 
