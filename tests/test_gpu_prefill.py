@@ -114,7 +114,7 @@ def test_prefill_mixed_batch_config3(gpu, prefill_waves, waves):
     assert pool.check() == 0
 
 
-@pytest.mark.parametrize("Hk,Hv", [(16, 32), (2, 8)])
+@pytest.mark.parametrize("Hk,Hv", [(16, 32), (2, 8), (4, 4)])
 def test_prefill_edge_lengths_from_nonzero_state(gpu, Hk, Hv):
     """Lengths 1, 2, 3 (conv state mixes old rows), 0 (empty sequence: slot
     untouched), 63/64/65 around a chunk boundary; sequences continue from a
@@ -254,7 +254,7 @@ def test_prefill_gated_matches_oracle_and_plain_prefill(gpu, Hk, Hv):
         assert pool.check() == 0
 
 
-@pytest.mark.parametrize("Hk,Hv", [(16, 32), (4, 16), (2, 8)])
+@pytest.mark.parametrize("Hk,Hv", [(16, 32), (4, 16), (2, 8), (4, 4)])
 def test_prefill_split_path_matches_fused(gpu, prefill_waves, Hk, Hv):
     """The split path (chunk records formed by prefill_form_kernel for all
     chunks at once, then 2 or 4 groups of 4 or 2 waves per head running only
@@ -328,7 +328,7 @@ def prefill_segments(monkeypatch):
     return force
 
 
-@pytest.mark.parametrize("Hk,Hv", [(16, 32), (4, 16)])
+@pytest.mark.parametrize("Hk,Hv", [(16, 32), (4, 16), (4, 4)])
 @pytest.mark.parametrize("waves", [2, 4])
 def test_prefill_pipelined_segments_match_one_pass(gpu, prefill_waves, prefill_segments, Hk, Hv,
                                                    waves):
