@@ -111,17 +111,19 @@ def test_qlinear_extreme_values(gpu):
     layer.close()
 
 
-@pytest.mark.parametrize("M", [1, 37, 64])
-def test_qlinear_wide_decode_columns_sampled(gpu, M):
+@pytest.mark.parametrize("M,K", [(1, 2048), (37, 2048), (64, 2048), (64, 512), (17, 1536),
+                                 (64, 4096)])
+def test_qlinear_wide_decode_columns_sampled(gpu, M, K):
     """Decode-sized call on a layer wide enough (131,088 columns) for the
-    64 x 128 tile route that lm_head takes; the oracle checks 1,024 sampled
-    columns (columns are independent: y[:, n] depends only on row n of the
-    weights), the first and last included, and the padding past N stays
-    unwritten."""
+    64 x 128 tile route that lm_head takes, at K = 2048 (lm_head's) and at
+    the other stage counts its loop takes (K = 512, 1536; K = 4096, the
+    kernel for K above 2048); the oracle checks 1,024 sampled columns
+    (columns are independent: y[:, n] depends only on row n of the weights),
+    the first and last included, and the padding past N stays unwritten."""
     import torch
-    say("gdn_qlinear_forward", f"wide decode M={M} K=2048 N=131088 (sampled columns)")
-    rng = np.random.default_rng(503 + M)
-    N, K = 131072 + 16, QWEN_HIDDEN
+    say("gdn_qlinear_forward", f"wide decode M={M} K={K} N=131088 (sampled columns)")
+    rng = np.random.default_rng(503 + M + K)
+    N = 131072 + 16
     w = rng.integers(0, 2**32, (N, K // 8), dtype=np.uint32)
     s = O.f32_to_bf16((rng.random((N, K // 64)) * 0.004 + 0.001).astype(np.float32))
     b = O.f32_to_bf16((rng.standard_normal((N, K // 64)) * 0.03).astype(np.float32))

@@ -133,18 +133,19 @@ def test_add_rms_norm_adds_and_checks(gpu):
         gdn_amd.add_rms_norm(odd, None, dev(w), 1e-6, torch.empty_like(odd))  # hidden % 8
 
 
-@pytest.mark.parametrize("M", [1, 37, 64])
-def test_norm_group_sums_wide_head_matches_oracle(gpu, M):
+@pytest.mark.parametrize("M,K", [(1, 2048), (37, 2048), (64, 2048), (5, 1024), (64, 4096)])
+def test_norm_group_sums_wide_head_matches_oracle(gpu, M, K):
     """The lm_head route with the norm's group sums: 131,088 columns (over the
-    131,072 threshold, the last 128-column tile part padding), K = 2048. The
-    oracle checks 1,024 sampled columns, the first and last included (y[:, n]
+    131,072 threshold, the last 128-column tile part padding), K = 2048
+    (lm_head's), 1024 and 4096 (the kernel for K above 2048). The oracle
+    checks 1,024 sampled columns, the first and last included (y[:, n]
     depends only on row n of the weights); both paths meet the qlinear bar,
     and the padding past N stays unwritten."""
     import torch
 
     import gdn_amd
-    K, N, eps = QWEN_HIDDEN, 131072 + 16, 1e-6
-    rng = np.random.default_rng(4500 + M)
+    N, eps = 131072 + 16, 1e-6
+    rng = np.random.default_rng(4500 + M + K)
     w = rng.integers(0, 2**32, (N, K // 8), dtype=np.uint32)
     sc = O.f32_to_bf16((rng.random((N, K // 64)) * 0.004 + 0.001).astype(np.float32))
     bi = O.f32_to_bf16((rng.standard_normal((N, K // 64)) * 0.03).astype(np.float32))
