@@ -74,8 +74,8 @@ def _run(gpu, M, K, rows, seed, x_pad=0, y_pad=0, x_scale=1.0):
     (65, 512, [128], 8, 0),                    # first multi-tile row count
     (130, QWEN_HIDDEN, [256, 64], 0, 8),
     (200, 4096, [144], 16, 4),                 # widest K, N not a tile multiple
-    (40, 4096, [2048], 8, 4),                  # out_proj shape: K split in 8 slices
-    (64, 2048, [1024, 16], 0, 0),              # narrow N: K split in 4 slices
+    (40, 4096, [2048], 8, 4),                  # out_proj shape: K split in 4 slices of 1024
+    (64, 2048, [1024, 16], 0, 0),              # narrow N: K split in 2 slices of 1024
 ])
 def test_qlinear_matches_oracle(gpu, M, K, rows, x_pad, y_pad):
     say("gdn_qlinear_forward", f"M={M} K={K} rows={rows}")
